@@ -1,0 +1,281 @@
+#!/usr/bin/env python3
+"""MoE-layer decode µs/token and achieved HBM GB/s at W4A16 on one MI355X.
+
+Workload (default, ``moe_decode``): one Kimi-Linear MoE layer decoding one
+token: hidden 2304, 256 routed experts + 1 shared, moe_intermediate 1024,
+sigmoid top-8 router (routed_scaling_factor 2.446) on logits ~N(0, 1), W4A16
+weights drawn from N(0, 0.02) and quantised at group 128 on the GPU. A step is
+router + gate/up + SwiGLU + W2 + weighted combine + shared expert for one
+token. 26 distinct layer banks (24.4 GB) are rotated so every step reads its
+weights from HBM, not from the 256 MB MALL. Steps are captured in a HIP graph
+and replayed; inputs are resident in HBM before the timed region.
+
+``--workload dense_decode``: x [1, 2304] x W [9216, 2304] at group 128, 40
+rotated weight copies (439 MB).
+
+Prints ONE JSON line. ``roofline`` is for the dominant kernel (gate/up +
+SwiGLU, or the dense GEMV), timed with HIP events on the stream it runs on;
+``cpu_baseline`` times the numpy oracle of the same step on the host (one
+thread, a bounded sample of tokens).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+H, E_ROUTED, INTER, TOP_K, G, SCALING = 2304, 256, 1024, 8, 128, 2.446
+DENSE_N = 9216
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def w4a16_bytes(n: int, k: int, g: int = G) -> int:
+    return n * k // 2 + n * (k // g) * 2
+
+
+EXPERT_BYTES = 2 * w4a16_bytes(INTER, H) + w4a16_bytes(H, INTER)       # 3,649,536
+GATEUP_EXPERT_BYTES = 2 * w4a16_bytes(INTER, H)                         # 2,433,024
+TOKEN_IO_BYTES = H * 2 + E_ROUTED * 4 + H * 2                           # x + logits + y
+
+
+def make_bank(rows: int, cols: int, experts: int, gen: torch.Generator, dev):
+    from local_kimi_amd.quant import quantise
+
+    packed = torch.empty((experts, rows, cols // 2), dtype=torch.uint8, device=dev)
+    scales = torch.empty((experts, rows, cols // G), dtype=torch.bfloat16, device=dev)
+    for e in range(experts):
+        w = (torch.randn((rows, cols), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        enc = quantise(w, group_size=G)
+        packed[e].copy_(enc.packed)
+        scales[e].copy_(enc.scales)
+    return packed, scales
+
+
+def time_graph(graph: torch.cuda.CUDAGraph, replays: int, stream: torch.cuda.Stream) -> float:
+    """Milliseconds for `replays` graph replays, HIP events on the replay stream."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end)
+
+
+def capture(fn, stream: torch.cuda.Stream) -> torch.cuda.CUDAGraph:
+    with torch.cuda.stream(stream):
+        fn()  # warm-up outside the graph (allocations, library load)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def cpu_baseline_moe(banks_l0, xs, logits, sample: int) -> dict:
+    """Oracle decode of `sample` tokens on one host thread (layer-0 weights)."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import moe as OM
+
+    host = [t.cpu().numpy() if t.dtype == torch.uint8 else
+            t.cpu().view(torch.int16).numpy().view(np.uint16) for t in banks_l0]
+    times = []
+    with threadpool_limits(1):
+        for i in range(sample):
+            x = xs[i].cpu().view(torch.int16).numpy().view(np.uint16)
+            lg = logits[i].cpu().numpy()
+            t0 = time.perf_counter()
+            OM.moe_block(x, lg, None, *host, top_k=TOP_K, routed_scaling_factor=SCALING, group_size=G)
+            times.append(time.perf_counter() - t0)
+    us = float(np.median(times)) * 1e6
+    return {"value": round(us, 1), "unit": "us/token", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle of the full MoE decode step (router, dequantise 9 experts, "
+                      f"gate/up, SwiGLU, W2, combine) for {sample} tokens on one host thread, median"}
+
+
+def cpu_baseline_dense(packed, scales, x, sample: int) -> dict:
+    from threadpoolctl import threadpool_limits
+
+    from oracle import w4a16 as OW
+
+    p = packed.cpu().numpy()
+    s = scales.cpu().view(torch.int16).numpy().view(np.uint16)
+    xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
+    times = []
+    with threadpool_limits(1):
+        for _ in range(sample):
+            t0 = time.perf_counter()
+            OW.dense(xb, p, s, G)
+            times.append(time.perf_counter() - t0)
+    us = float(np.median(times)) * 1e6
+    return {"value": round(us, 1), "unit": "us/token", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle dense GEMV (dequantise + matmul) x{sample}, one host thread, median"}
+
+
+def run_moe(args, dev) -> dict:
+    from local_kimi_amd.kernels import w4a16_moe_block, w4a16_moe_gateup
+
+    layers = args.layers
+    gen = torch.Generator(device=dev).manual_seed(20260729)
+    t0 = time.time()
+    master = (*make_bank(INTER, H, E_ROUTED + 1, gen, dev), *make_bank(INTER, H, E_ROUTED + 1, gen, dev),
+              *make_bank(H, INTER, E_ROUTED + 1, gen, dev))
+    banks = [master] + [tuple(t.clone() for t in master) for _ in range(layers - 1)]
+    xs = [(torch.randn((1, H), device=dev, generator=gen)).to(torch.bfloat16) for _ in range(layers)]
+    logits = [torch.randn((1, E_ROUTED), device=dev, generator=gen) for _ in range(layers)]
+    torch.cuda.synchronize()
+    log(f"[bench] {layers} layer banks ready in {time.time() - t0:.1f}s "
+        f"({layers * (E_ROUTED + 1) * EXPERT_BYTES / 1e9:.1f} GB)")
+
+    stream = torch.cuda.Stream(device=dev)
+
+    def block_all():
+        for l in range(layers):
+            w4a16_moe_block(xs[l], logits[l], None, *banks[l], TOP_K, SCALING)
+
+    def gateup_all():
+        for l in range(layers):
+            w1p, w1s, w3p, w3s = banks[l][:4]
+            w4a16_moe_gateup(xs[l], logits[l], None, w1p, w1s, w3p, w3s, TOP_K, SCALING)
+
+    g_block = capture(block_all, stream)
+    g_gateup = capture(gateup_all, stream)
+
+    steps = max(layers, (args.steps + layers - 1) // layers * layers)
+    warm = max(1, (args.warmup + layers - 1) // layers)
+    for _ in range(warm):
+        g_block.replay()
+        g_gateup.replay()
+    torch.cuda.synchronize()
+    log(f"[bench] warm-up done ({warm * layers} steps); timing {steps} steps")
+    block_ms = time_graph(g_block, steps // layers, stream)
+    gateup_ms = time_graph(g_gateup, steps // layers, stream)
+    us_per_token = block_ms * 1000.0 / steps
+    gateup_us = gateup_ms * 1000.0 / steps
+    block_bytes = (TOP_K + 1) * EXPERT_BYTES + TOKEN_IO_BYTES
+    gateup_bytes = (TOP_K + 1) * GATEUP_EXPERT_BYTES + H * 2 + E_ROUTED * 4 + (TOP_K + 1) * INTER * 2
+    log(f"[bench] block {us_per_token:.2f} us/token, gate/up kernel {gateup_us:.2f} us/launch")
+
+    result = {
+        "metric": "MoE-layer decode us/token + achieved HBM GB/s (% of peak) at W4A16",
+        "value": round(us_per_token, 3),
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm * layers,
+        "ms_per_step": round(block_ms / steps, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x and logits",
+        "config": {"workload": "moe_decode_batch1", "hidden": H, "routed_experts": E_ROUTED,
+                   "shared_experts": 1, "moe_intermediate": INTER, "top_k": TOP_K, "group_size": G,
+                   "tokens_per_step": 1, "layer_banks_rotated": layers, "launches_per_step": 2},
+        "achieved_gbps": round(block_bytes / (us_per_token * 1e3), 1),
+        "pct_hbm_peak": round(100.0 * block_bytes / (us_per_token * 1e3) / HBM_PEAK_GBPS, 2),
+        "algorithmic_bytes_per_step": block_bytes,
+        "roofline": {"kernel": "moe_gateup_kernel (router + gate/up + SwiGLU)", "bound": "hbm",
+                     "achieved": round(gateup_bytes / (gateup_us * 1e3), 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s",
+                     "frac": round(gateup_bytes / (gateup_us * 1e3) / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "bytes_per_launch": gateup_bytes,
+                     "avg_launch_us": round(gateup_us, 3)},
+    }
+    if args.cpu_sample > 0:
+        log(f"[bench] timing the CPU oracle on {args.cpu_sample} tokens")
+        result["cpu_baseline"] = cpu_baseline_moe(banks[0], xs, logits, args.cpu_sample)
+    return result
+
+
+def run_dense(args, dev) -> dict:
+    from local_kimi_amd.kernels import w4a16_dense
+    from local_kimi_amd.quant import quantise
+
+    copies = args.copies
+    gen = torch.Generator(device=dev).manual_seed(20260729)
+    w = (torch.randn((DENSE_N, H), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+    enc = quantise(w, group_size=G)
+    weights = [(enc.packed.clone(), enc.scales.clone()) for _ in range(copies)]
+    x = torch.randn((1, H), device=dev, generator=gen).to(torch.bfloat16)
+    stream = torch.cuda.Stream(device=dev)
+
+    def all_copies():
+        for p, s in weights:
+            w4a16_dense(x, p, s)
+
+    graph = capture(all_copies, stream)
+    steps = max(copies, (args.steps + copies - 1) // copies * copies)
+    warm = max(1, (args.warmup + copies - 1) // copies)
+    for _ in range(warm):
+        graph.replay()
+    ms = time_graph(graph, steps // copies, stream)
+    us = ms * 1000.0 / steps
+    nbytes = w4a16_bytes(DENSE_N, H) + H * 2 + DENSE_N * 2
+    result = {
+        "metric": "Dense W4A16 GEMV decode us/token + achieved HBM GB/s (% of peak)",
+        "value": round(us, 3), "unit": "us/token", "n_gpus": 1, "steps": steps,
+        "warmup": warm * copies, "ms_per_step": round(ms / steps, 6), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x",
+        "config": {"workload": "dense_gemv_decode", "m": 1, "n": DENSE_N, "k": H, "group_size": G,
+                   "weight_copies_rotated": copies},
+        "achieved_gbps": round(nbytes / (us * 1e3), 1),
+        "pct_hbm_peak": round(100.0 * nbytes / (us * 1e3) / HBM_PEAK_GBPS, 2),
+        "roofline": {"kernel": "dense_gemv_kernel", "bound": "hbm",
+                     "achieved": round(nbytes / (us * 1e3), 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(nbytes / (us * 1e3) / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3)},
+    }
+    if args.cpu_sample > 0:
+        result["cpu_baseline"] = cpu_baseline_dense(weights[0][0], weights[0][1], x, args.cpu_sample)
+    return result
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2600)
+    ap.add_argument("--warmup", type=int, default=260)
+    ap.add_argument("--workload", choices=["moe_decode", "dense_decode"], default="moe_decode")
+    ap.add_argument("--layers", type=int, default=26, help="MoE layer banks rotated")
+    ap.add_argument("--copies", type=int, default=40, help="dense weight copies rotated")
+    ap.add_argument("--cpu-sample", type=int, default=4, help="tokens for the CPU oracle baseline (0: skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
+              "multi-GPU path. Run with --gpus 1.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    from local_kimi_amd import _lib
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    log(f"[bench] device {torch.cuda.get_device_name(0)}, workload {args.workload}")
+    result = run_moe(args, dev) if args.workload == "moe_decode" else run_dense(args, dev)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,163 @@
+/*
+ * C ABI of the MI355X (gfx950) W4A16 / MXFP4 quantized-matmul library.
+ *
+ * Every entry point takes plain device pointers, element counts and a
+ * hipStream_t passed as void*. Nothing allocates, synchronises the device or
+ * reads device memory on the host, so each call is safe inside HIP graph
+ * capture. Return value: LK_OK, or an error code with a message available
+ * from lk_last_error() (per calling thread).
+ *
+ * Layouts (engine/quant/w4a16.py:1-6, 46-47, 94-99 of the reference):
+ *   bf16          uint16_t bit patterns
+ *   packed        uint8_t [N, K/2]; byte j holds k=2j in the low nibble and
+ *                 k=2j+1 in the high nibble; 4-bit two's complement codes
+ *   scales        bf16 [N, K/G]; one scale per G consecutive k
+ *   grouped banks packed [E, N, K/2], scales [E, N, K/G]
+ *   MXFP4         packed uint8_t [N, K/2] E2M1 (low nibble first),
+ *                 scale uint8_t [N, K/32] E8M0 (bias 127)
+ * All tensors are dense row-major. G must be a multiple of 32 dividing K.
+ * The reference fixes G=32 (engine/quant/w4a16.py:14); here G is an argument.
+ *
+ * Each declaration cites the reference interface it replaces.
+ */
+#ifndef LK_W4A16_H
+#define LK_W4A16_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define LK_API __attribute__((visibility("default")))
+#else
+#define LK_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LK_OK 0
+#define LK_ERR_ARGUMENT 1
+#define LK_ERR_HIP 2
+
+/* Message describing the last failure on this thread ("" when none). */
+LK_API const char* lk_last_error(void);
+
+/* ABI version of this library. */
+LK_API int lk_abi_version(void);
+
+/* ---- codec: engine/quant/w4a16.py:68-105 (quantise), :108-129 (dequantise) */
+
+/* weight bf16 [N,K] -> packed [N,K/2], scales bf16 [N,K/G]; bit-exact with
+ * the reference encoder (absmax/7 scale stored as bf16, codes rounded half
+ * to even against the stored scale, clamped to [-7, 7]). */
+LK_API int lk_w4a16_quantise(const uint16_t* weight, uint8_t* packed, uint16_t* scales,
+                      int64_t n, int64_t k, int64_t group_size, void* stream);
+
+/* packed + scales -> out [N,K]: bf16(q * scale) as bf16 when out_f32 == 0,
+ * or the exact q * scale as float32 when out_f32 != 0. */
+LK_API int lk_w4a16_dequantise(const uint8_t* packed, const uint16_t* scales, void* out,
+                               int64_t n, int64_t k, int64_t group_size, int out_f32,
+                               void* stream);
+
+/* ---- op w4a16_dense: engine/kernels/__init__.py:82-125 (signature),
+ *      engine/kernels/w4a16_dense_gemv.py:312-336 (default variant)
+ * y bf16 [M,N] = x bf16 [M,K] . dequant(W)^T, fp32 accumulation. */
+LK_API int lk_w4a16_dense(const uint16_t* x, const uint8_t* packed, const uint16_t* scales,
+                   uint16_t* y, int64_t m, int64_t n, int64_t k, int64_t group_size,
+                   void* stream);
+
+/* Same op with the reference's rounding contract (weights rounded to bf16
+ * before the fp32 multiply-add, one thread per output); the registry's
+ * "reference" variant. engine/quant/triton_w4a16.py:151-188. */
+LK_API int lk_w4a16_dense_reference(const uint16_t* x, const uint8_t* packed,
+                             const uint16_t* scales, uint16_t* y, int64_t m, int64_t n,
+                             int64_t k, int64_t group_size, void* stream);
+
+/* ---- op w4a16_grouped: engine/kernels/__init__.py:26-79,
+ *      engine/kernels/w4a16_gemv.py:610-635
+ * out bf16 [T,R,N]: out[t,r] = x[t] . dequant(W[idx[t,r]])^T. */
+LK_API int lk_w4a16_grouped(const uint16_t* x, const int64_t* expert_indices,
+                     const uint8_t* packed, const uint16_t* scales, uint16_t* out,
+                     int64_t tokens, int64_t routes, int64_t experts, int64_t n,
+                     int64_t k, int64_t group_size, void* stream);
+
+/* Reference-rounding variant (engine/kernels/w4a16_grouped.py:121-194). */
+LK_API int lk_w4a16_grouped_reference(const uint16_t* x, const int64_t* expert_indices,
+                               const uint8_t* packed, const uint16_t* scales,
+                               uint16_t* out, int64_t tokens, int64_t routes,
+                               int64_t experts, int64_t n, int64_t k,
+                               int64_t group_size, void* stream);
+
+/* ---- op w4a16_swiglu: engine/kernels/__init__.py:164-218,
+ *      engine/kernels/w4a16_gemv.py:772-790
+ * act bf16 [T,R,N] = bf16(bf16(silu(bf16(x.W1^T))) * bf16(x.W3^T)). */
+LK_API int lk_w4a16_swiglu(const uint16_t* x, const int64_t* expert_indices,
+                    const uint8_t* w1_packed, const uint16_t* w1_scales,
+                    const uint8_t* w3_packed, const uint16_t* w3_scales, uint16_t* out,
+                    int64_t tokens, int64_t routes, int64_t experts, int64_t n, int64_t k,
+                    int64_t group_size, void* stream);
+
+/* Elementwise bf16(silu(gate)) * up on bf16 tensors, as the reference
+ * variant of w4a16_swiglu does after its two grouped calls
+ * (engine/kernels/__init__.py:195-197). */
+LK_API int lk_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t count,
+                void* stream);
+
+/* Route combine on precomputed expert outputs eo bf16 [T,R,H]:
+ * y = bf16(bf16(sum_{r<R-1} eo[t,r] * cw[t,r]) + eo[t,R-1]); the last route
+ * is the shared expert with weight 1 (engine/klinear/moe.py:327-334). */
+LK_API int lk_route_combine(const uint16_t* expert_outputs, const float* combine_weights,
+                            uint16_t* y, int64_t tokens, int64_t routes, int64_t h,
+                            void* stream);
+
+/* ---- fused W2 + route combine: engine/kernels/moe_combine.py:264-324
+ *      (semantics: fused_w2_combine_reference, :209-261; klinear/moe.py:317-334)
+ * y bf16 [T,H] = bf16(bf16(sum_{r<R-1} bf16(act[t,r].W2[idx]^T) * cw[t,r])
+ *                     + bf16(act[t,R-1].W2[idx]^T)); cw[:, R-1] is ignored. */
+LK_API int lk_w4a16_w2_combine(const uint16_t* activated, const int64_t* expert_indices,
+                        const float* combine_weights, const uint8_t* w2_packed,
+                        const uint16_t* w2_scales, uint16_t* y, int64_t tokens,
+                        int64_t routes, int64_t experts, int64_t h, int64_t i,
+                        int64_t group_size, void* stream);
+
+/* ---- router: engine/klinear/router.py:47-85 (on precomputed fp32 logits)
+ * idx int64 [T,top_k] in descending choice score (sigmoid + bias), ties to the
+ * lower id; weights fp32 [T,top_k] = sigmoid gathered, renormalised by
+ * (sum + 1e-20) when renormalize != 0 and top_k > 1, times scaling.
+ * bias may be NULL (zero). Requires experts <= 1024, top_k <= 32. */
+LK_API int lk_moe_router(const float* logits, const float* bias, int64_t* expert_indices,
+                  float* weights, int64_t tokens, int64_t experts, int64_t top_k,
+                  float routed_scaling_factor, int renormalize, void* stream);
+
+/* ---- first stage of the MoE block: router + gate/up + SwiGLU in one launch
+ *      (engine/klinear/router.py:47-85, engine/kernels/__init__.py:182-197)
+ * Writes expert_indices int64 [T,top_k], weights fp32 [T,top_k] and
+ * activated bf16 [T,top_k+1,I] (route top_k is the shared expert E-1). */
+LK_API int lk_w4a16_moe_gateup(const uint16_t* x, const float* logits, const float* bias,
+                               const uint8_t* w1_packed, const uint16_t* w1_scales,
+                               const uint8_t* w3_packed, const uint16_t* w3_scales,
+                               int64_t* expert_indices, float* weights, uint16_t* activated,
+                               int64_t tokens, int64_t experts, int64_t h, int64_t i,
+                               int64_t top_k, float routed_scaling_factor, int renormalize,
+                               int64_t group_size, void* stream);
+
+/* ---- the grouped W4A16 MoE block with its router, one decode step:
+ *      engine/klinear/moe.py:278-334 + engine/klinear/router.py:47-85
+ * Banks hold routed experts 0..E-2 and the shared expert at E-1.
+ * Writes y bf16 [T,H], expert_indices int64 [T,top_k], weights fp32
+ * [T,top_k] and the SwiGLU activations into activated bf16 [T,top_k+1,I]
+ * (caller-owned workspace). */
+LK_API int lk_w4a16_moe_decode(const uint16_t* x, const float* logits, const float* bias,
+                        const uint8_t* w1_packed, const uint16_t* w1_scales,
+                        const uint8_t* w3_packed, const uint16_t* w3_scales,
+                        const uint8_t* w2_packed, const uint16_t* w2_scales, uint16_t* y,
+                        int64_t* expert_indices, float* weights, uint16_t* activated,
+                        int64_t tokens, int64_t experts, int64_t h, int64_t i,
+                        int64_t top_k, float routed_scaling_factor, int renormalize,
+                        int64_t group_size, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LK_W4A16_H */

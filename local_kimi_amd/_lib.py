@@ -1,0 +1,89 @@
+"""ctypes binding of the in-tree HIP library (``liblkamd.so``).
+
+The library exposes the C ABI declared in ``include/lk_w4a16.h``. This module
+declares each entry point's argument types once, and :func:`call` turns a
+non-zero status into ``RuntimeError`` with the library's message. There is no
+fallback: if the library is missing, every kernel call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "liblkamd.so")
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_I = ctypes.c_int
+
+# name -> argument types (every entry point returns int status)
+SIGNATURES: dict[str, list] = {
+    "lk_w4a16_quantise": [_P, _P, _P, _I64, _I64, _I64, _P],
+    "lk_w4a16_dequantise": [_P, _P, _P, _I64, _I64, _I64, _I, _P],
+    "lk_w4a16_dense": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "lk_w4a16_dense_reference": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "lk_w4a16_grouped": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
+    "lk_w4a16_grouped_reference": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
+    "lk_w4a16_swiglu": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
+    "lk_silu_mul": [_P, _P, _P, _I64, _P],
+    "lk_route_combine": [_P, _P, _P, _I64, _I64, _I64, _P],
+    "lk_w4a16_w2_combine": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
+    "lk_moe_router": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _I, _P],
+    "lk_w4a16_moe_gateup": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                            _I64, _I64, _I64, _I64, _I64, _F, _I, _I64, _P],
+    "lk_w4a16_moe_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                            _I64, _I64, _I64, _I64, _I64, _F, _I, _I64, _P],
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def is_built() -> bool:
+    return os.path.exists(LIB_PATH)
+
+
+def load() -> ctypes.CDLL:
+    """Load the library once; raise RuntimeError when it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"the HIP library {LIB_PATH} is not built; run "
+                    "`python -m local_kimi_amd._build` (hipcc, gfx950) first"
+                )
+            lib = ctypes.CDLL(LIB_PATH)
+            lib.lk_last_error.restype = ctypes.c_char_p
+            lib.lk_last_error.argtypes = []
+            lib.lk_abi_version.restype = ctypes.c_int
+            lib.lk_abi_version.argtypes = []
+            for name, argtypes in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = ctypes.c_int
+                fn.argtypes = argtypes
+            _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    lib = load()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        message = lib.lk_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed (status {status}): {message}")
+
+
+def exported_symbols() -> list[str]:
+    """Entry points this binding expects the library to export."""
+    return ["lk_last_error", "lk_abi_version", *SIGNATURES]

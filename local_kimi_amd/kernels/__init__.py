@@ -1,0 +1,114 @@
+"""W4A16 / MXFP4 kernel ops for MI355X, registered behind the reference's registry.
+
+Importing this package registers every op and selects the shipped default,
+mirroring engine/kernels/__init__.py:19-223: op names ``w4a16_grouped``,
+``w4a16_dense`` and ``w4a16_swiglu`` keep the reference signatures; new ops
+(``w4a16_fused_qkv``, ``w4a16_w2_combine``, ``w4a16_moe_block``) follow the
+same style. Every op has two HIP variants:
+
+* ``reference`` -- one thread per output with the reference's rounding
+  contract (weights decoded to ``bf16(q * s)`` before the multiply-add);
+  simple and slow, used as the in-process equivalence baseline;
+* ``hip`` -- the gfx950 kernels, the shipped default.
+
+Both are ``requires_cuda=True``: on a machine without a GPU the registry
+refuses them instead of running anything on the CPU, and a missing HIP library
+raises on first call.
+"""
+
+from . import registry
+from .moe import (moe_router, shape_stable_expert_indices, w4a16_moe_block,
+                  w4a16_moe_block_reference, w4a16_moe_gateup)
+from .w4a16 import (fused_qkv_w4a16, fused_qkv_w4a16_reference, fused_w2_combine,
+                    fused_w2_combine_reference, grouped_w4a16_gemv, grouped_w4a16_reference,
+                    grouped_w4a16_swiglu_gemv, route_combine, silu_mul, w4a16_dense,
+                    w4a16_dense_reference)
+
+W4A16_GROUPED = "w4a16_grouped"
+W4A16_DENSE = "w4a16_dense"
+W4A16_SWIGLU = "w4a16_swiglu"
+W4A16_FUSED_QKV = "w4a16_fused_qkv"
+W4A16_W2_COMBINE = "w4a16_w2_combine"
+W4A16_MOE_BLOCK = "w4a16_moe_block"
+
+HIP = "hip"
+REFERENCE = "reference"
+
+
+def _register_grouped() -> None:
+    registry.register(W4A16_GROUPED, REFERENCE, reference=True, requires_cuda=True,
+                      description="One thread per output, weights rounded to bf16(q*s).")(
+        grouped_w4a16_reference)
+    registry.register(W4A16_GROUPED, HIP, requires_cuda=True,
+                      description="gfx950 grouped GEMV: 8 lanes per row, 16 B nibble loads, "
+                      "bf16 dot2 with per-chunk scales, DPP row reduction.")(grouped_w4a16_gemv)
+    registry.set_default(W4A16_GROUPED, HIP)
+
+
+def _register_dense() -> None:
+    registry.register(W4A16_DENSE, REFERENCE, reference=True, requires_cuda=True,
+                      description="One thread per output, weights rounded to bf16(q*s).")(
+        w4a16_dense_reference)
+    registry.register(W4A16_DENSE, HIP, requires_cuda=True,
+                      description="gfx950 dense GEMV with LDS-staged activations.")(w4a16_dense)
+    registry.set_default(W4A16_DENSE, HIP)
+
+
+def _register_swiglu() -> None:
+    cache: dict[str, object] = {}
+
+    def swiglu_reference(activations, expert_indices, w1_packed, w1_scales, w3_packed, w3_scales):
+        """Two grouped calls through the active grouped variant, then silu * up
+        (engine/kernels/__init__.py:182-197)."""
+        name = registry.active(W4A16_GROUPED)
+        kernel = cache.get(name)
+        if kernel is None:
+            kernel = registry.resolve(W4A16_GROUPED)
+            cache[name] = kernel
+        gate = kernel(activations, expert_indices, w1_packed, w1_scales)
+        up = kernel(activations, expert_indices, w3_packed, w3_scales)
+        return silu_mul(gate, up)
+
+    registry.register(W4A16_SWIGLU, REFERENCE, reference=True, requires_cuda=True,
+                      description="Two grouped calls plus silu and multiply.")(swiglu_reference)
+    registry.register(W4A16_SWIGLU, HIP, requires_cuda=True,
+                      description="One launch reading W1 and W3 together, writing only the "
+                      "activated result.")(grouped_w4a16_swiglu_gemv)
+    registry.set_default(W4A16_SWIGLU, HIP)
+
+
+def _register_others() -> None:
+    registry.register(W4A16_FUSED_QKV, REFERENCE, reference=True, requires_cuda=True,
+                      description="Three reference dense calls.")(fused_qkv_w4a16_reference)
+    registry.register(W4A16_FUSED_QKV, HIP, requires_cuda=True,
+                      description="Q, K, V through the gfx950 dense path.")(fused_qkv_w4a16)
+    registry.set_default(W4A16_FUSED_QKV, HIP)
+
+    registry.register(W4A16_W2_COMBINE, REFERENCE, reference=True, requires_cuda=True,
+                      description="Reference grouped W2 per route, then the combine kernel.")(
+        fused_w2_combine_reference)
+    registry.register(W4A16_W2_COMBINE, HIP, requires_cuda=True,
+                      description="W2 for all routes plus weighted combine and shared expert "
+                      "in one launch.")(fused_w2_combine)
+    registry.set_default(W4A16_W2_COMBINE, HIP)
+
+    registry.register(W4A16_MOE_BLOCK, REFERENCE, reference=True, requires_cuda=True,
+                      description="Router, reference gate/up, silu*up, reference W2 + combine.")(
+        w4a16_moe_block_reference)
+    registry.register(W4A16_MOE_BLOCK, HIP, requires_cuda=True,
+                      description="Router + gate/up + SwiGLU in one launch, W2 + combine in a "
+                      "second.")(w4a16_moe_block)
+    registry.set_default(W4A16_MOE_BLOCK, HIP)
+
+
+_register_grouped()
+_register_dense()
+_register_swiglu()
+_register_others()
+
+__all__ = [
+    "registry", "W4A16_GROUPED", "W4A16_DENSE", "W4A16_SWIGLU", "W4A16_FUSED_QKV",
+    "W4A16_W2_COMBINE", "W4A16_MOE_BLOCK", "moe_router", "shape_stable_expert_indices",
+    "w4a16_moe_block", "w4a16_moe_gateup", "w4a16_dense", "grouped_w4a16_gemv", "grouped_w4a16_swiglu_gemv",
+    "fused_w2_combine", "fused_qkv_w4a16", "route_combine", "silu_mul",
+]

@@ -1,0 +1,181 @@
+"""Router and the whole W4A16 MoE block on HIP.
+
+``moe_router`` restates engine/klinear/router.py:47-85 on precomputed fp32
+logits; ``w4a16_moe_block`` is the grouped branch of KLinearMoE.forward
+(engine/klinear/moe.py:278-334, 375-398): route, gate/up + SwiGLU over the
+top-k routes and the shared expert, W2, weighted combine plus shared expert.
+The fused HIP path runs it in two launches (router + gate/up + SwiGLU, then
+W2 + combine); the reference variant composes the reference ops.
+
+Expert banks hold the routed experts first and the shared expert last
+(``[E_routed + 1, ...]``), exactly as ``prepare_grouped_w4a16`` stacks them
+(engine/klinear/moe.py:253-267).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from . import w4a16 as _w
+
+
+def shape_stable_expert_indices(expert_indices: torch.Tensor, shared_expert_id: int) -> torch.Tensor:
+    """Append the shared expert as one fixed route for every token (moe.py:23-36)."""
+    if expert_indices.ndim != 2:
+        raise ValueError("expert_indices must have shape [tokens, routes]")
+    shared = torch.full((expert_indices.shape[0], 1), shared_expert_id,
+                        dtype=expert_indices.dtype, device=expert_indices.device)
+    return torch.cat((expert_indices, shared), dim=1)
+
+
+def _validate_router(logits: torch.Tensor, bias: torch.Tensor | None, top_k: int):
+    if logits.ndim != 2 or logits.dtype != torch.float32:
+        raise TypeError("router logits must be a float32 [tokens, experts] matrix")
+    if logits.device.type != "cuda":
+        raise ValueError("the HIP router requires CUDA")
+    tokens, experts = logits.shape
+    if experts == 0 or experts > 1024:
+        raise ValueError("the HIP router supports 1..1024 experts")
+    if not 0 < top_k <= min(32, experts):
+        raise ValueError(f"top_k must be in 1..{min(32, experts)}, got {top_k}")
+    if bias is not None:
+        if bias.dtype != torch.float32 or bias.shape != (experts,):
+            raise TypeError("router bias must be a float32 [experts] vector")
+        if bias.device != logits.device:
+            raise ValueError("router bias must share the logits device")
+    return tokens, experts
+
+
+def moe_router(logits: torch.Tensor, bias: torch.Tensor | None, top_k: int, *,
+               routed_scaling_factor: float = 1.0,
+               renormalize: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+    """Sigmoid top-k routing: ``(idx int64 [T, k], weights float32 [T, k])``.
+
+    Selections are ordered by descending ``sigmoid(logit) + bias``, ties to the
+    lower expert id; weights are the un-biased sigmoid scores, renormalised by
+    ``sum + 1e-20`` (when ``top_k > 1`` and ``renormalize``) and scaled.
+    """
+    tokens, experts = _validate_router(logits, bias, top_k)
+    idx = torch.empty((tokens, top_k), dtype=torch.long, device=logits.device)
+    w = torch.empty((tokens, top_k), dtype=torch.float32, device=logits.device)
+    if tokens == 0:
+        return idx, w
+    lg = _w._c(logits)
+    b = _w._c(bias) if bias is not None else None
+    with torch.cuda.device(logits.device):
+        _lib.call("lk_moe_router", lg.data_ptr(), b.data_ptr() if b is not None else None,
+                  idx.data_ptr(), w.data_ptr(), tokens, experts, top_k,
+                  float(routed_scaling_factor), int(bool(renormalize)), _w._stream(logits.device))
+    return idx, w
+
+
+def _validate_stage1(hidden, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales, top_k):
+    if hidden.ndim != 2 or hidden.dtype != torch.bfloat16:
+        raise TypeError("hidden states must be a BF16 [tokens, hidden] matrix")
+    tokens, h = hidden.shape
+    _validate_router(logits, bias, top_k)
+    if logits.shape[0] != tokens:
+        raise ValueError("router logits must have one row per token")
+    e1, inter, k1, g1 = _w.check_bank(w1_packed, w1_scales, "W1")
+    e3, inter3, k3, g3 = _w.check_bank(w3_packed, w3_scales, "W3")
+    if (e1, inter, k1, g1) != (e3, inter3, k3, g3):
+        raise ValueError("grouped W1 and W3 dimensions must match")
+    if k1 != h:
+        raise ValueError("W1/W3 reduction width must equal the hidden size")
+    if logits.shape[1] != e1 - 1:
+        raise ValueError("banks must hold every routed expert plus the shared expert last")
+    if w1_packed.device != hidden.device or w3_packed.device != hidden.device or \
+            logits.device != hidden.device:
+        raise ValueError("MoE inputs must share one device")
+    return tokens, e1, h, inter, g1
+
+
+def _validate_block(hidden, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
+                    w2_packed, w2_scales, top_k):
+    tokens, e_total, h, inter, g1 = _validate_stage1(hidden, logits, bias, w1_packed, w1_scales,
+                                                     w3_packed, w3_scales, top_k)
+    e2, h2, k2, g2 = _w.check_bank(w2_packed, w2_scales, "W2")
+    if e2 != e_total:
+        raise ValueError("W2 bank must have the same expert count as W1/W3")
+    if h2 != h or k2 != inter:
+        raise ValueError("W2 must map the intermediate size back to the hidden size")
+    if g1 != g2:
+        raise ValueError("W1/W3 and W2 must use the same group size")
+    if w2_packed.device != hidden.device:
+        raise ValueError("MoE inputs must share one device")
+    return tokens, e_total, h, inter, g1
+
+
+def w4a16_moe_block(hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor | None,
+                    w1_packed, w1_scales, w3_packed, w3_scales, w2_packed, w2_scales, top_k: int,
+                    routed_scaling_factor: float = 1.0, renormalize: bool = True):
+    """Router + SwiGLU experts + W2 + combine + shared expert in two HIP launches.
+
+    Returns ``(y bf16 [T, H], expert_indices int64 [T, k], weights float32 [T, k])``.
+    """
+    tokens, e_total, h, inter, g = _validate_block(hidden, logits, bias, w1_packed, w1_scales,
+                                                   w3_packed, w3_scales, w2_packed, w2_scales, top_k)
+    dev = hidden.device
+    y = torch.empty((tokens, h), dtype=torch.bfloat16, device=dev)
+    idx = torch.empty((tokens, top_k), dtype=torch.long, device=dev)
+    w = torch.empty((tokens, top_k), dtype=torch.float32, device=dev)
+    if tokens == 0:
+        return y, idx, w
+    act = torch.empty((tokens, top_k + 1, inter), dtype=torch.bfloat16, device=dev)
+    c = _w._c
+    x, lg = c(hidden), c(logits)
+    b = c(bias) if bias is not None else None
+    args = [c(t) for t in (w1_packed, w1_scales, w3_packed, w3_scales, w2_packed, w2_scales)]
+    with torch.cuda.device(dev):
+        _lib.call("lk_w4a16_moe_decode", x.data_ptr(), lg.data_ptr(),
+                  b.data_ptr() if b is not None else None, *(t.data_ptr() for t in args),
+                  y.data_ptr(), idx.data_ptr(), w.data_ptr(), act.data_ptr(), tokens, e_total, h,
+                  inter, top_k, float(routed_scaling_factor), int(bool(renormalize)), g,
+                  _w._stream(dev))
+    return y, idx, w
+
+
+def w4a16_moe_gateup(hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor | None,
+                     w1_packed, w1_scales, w3_packed, w3_scales, top_k: int,
+                     routed_scaling_factor: float = 1.0, renormalize: bool = True):
+    """First stage of the block in one launch: router + gate/up + SwiGLU.
+
+    Returns ``(activated bf16 [T, k+1, I], expert_indices [T, k], weights [T, k])``;
+    route ``k`` of ``activated`` is the shared expert.
+    """
+    tokens, e_total, h, inter, g = _validate_stage1(hidden, logits, bias, w1_packed, w1_scales,
+                                                    w3_packed, w3_scales, top_k)
+    dev = hidden.device
+    act = torch.empty((tokens, top_k + 1, inter), dtype=torch.bfloat16, device=dev)
+    idx = torch.empty((tokens, top_k), dtype=torch.long, device=dev)
+    w = torch.empty((tokens, top_k), dtype=torch.float32, device=dev)
+    if tokens == 0:
+        return act, idx, w
+    c = _w._c
+    x, lg = c(hidden), c(logits)
+    b = c(bias) if bias is not None else None
+    args = [c(t) for t in (w1_packed, w1_scales, w3_packed, w3_scales)]
+    with torch.cuda.device(dev):
+        _lib.call("lk_w4a16_moe_gateup", x.data_ptr(), lg.data_ptr(),
+                  b.data_ptr() if b is not None else None, *(t.data_ptr() for t in args),
+                  idx.data_ptr(), w.data_ptr(), act.data_ptr(), tokens, e_total, h, inter, top_k,
+                  float(routed_scaling_factor), int(bool(renormalize)), g, _w._stream(dev))
+    return act, idx, w
+
+
+def w4a16_moe_block_reference(hidden, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
+                              w2_packed, w2_scales, top_k: int, routed_scaling_factor: float = 1.0,
+                              renormalize: bool = True):
+    """The same block composed from the reference-rounding ops (moe.py:278-334)."""
+    tokens, e_total, h, inter, _ = _validate_block(hidden, logits, bias, w1_packed, w1_scales,
+                                                   w3_packed, w3_scales, w2_packed, w2_scales, top_k)
+    idx, w = moe_router(logits, bias, top_k, routed_scaling_factor=routed_scaling_factor,
+                        renormalize=renormalize)
+    stable = shape_stable_expert_indices(idx, e_total - 1)
+    gate = _w.grouped_w4a16_reference(hidden, stable, w1_packed, w1_scales)
+    up = _w.grouped_w4a16_reference(hidden, stable, w3_packed, w3_scales)
+    act = _w.silu_mul(gate, up)
+    cw = torch.cat((w, torch.ones((tokens, 1), dtype=torch.float32, device=w.device)), dim=1)
+    y = _w.fused_w2_combine_reference(act, stable, cw, w2_packed, w2_scales)
+    return y, idx, w

@@ -1,0 +1,56 @@
+"""The C-ABI library loads and exports every entry point include/lk_w4a16.h
+declares (no compute calls: this runs without a GPU)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from local_kimi_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared() -> list[str]:
+    names = []
+    for header in os.listdir(os.path.join(ROOT, "include")):
+        if header.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", header)).read()
+            names += re.findall(r"LK_API\s+[\w\s\*]+?\b(lk_\w+)\s*\(", text)
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.is_built():
+        pytest.skip("library not built; run python -m local_kimi_amd._build")
+    return _lib.load()
+
+
+def test_header_declares_the_entry_points_the_binding_uses():
+    declared = _declared()
+    assert declared, "no LK_API declarations found"
+    assert sorted(_lib.exported_symbols()) == declared
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
+
+
+def test_abi_version_and_error_string(lib):
+    assert lib.lk_abi_version() == 1
+    assert isinstance(lib.lk_last_error(), bytes)
+
+
+def test_argument_errors_are_reported_without_touching_the_gpu(lib):
+    # k=100 is not divisible by the group size: rejected on the host before any launch
+    with pytest.raises(RuntimeError, match="divisible"):
+        _lib.call("lk_w4a16_dense", 1, 1, 1, 1, 1, 8, 100, 32, None)
+    with pytest.raises(RuntimeError, match="power of two"):
+        _lib.call("lk_w4a16_dense", 1, 1, 1, 1, 1, 8, 192, 96, None)
+    with pytest.raises(RuntimeError, match="top_k"):
+        _lib.call("lk_moe_router", 1, None, 1, 1, 1, 4, 9, 1.0, 1, None)

@@ -1,0 +1,69 @@
+"""Host-side validation raises the reference's exception types before any GPU work."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from local_kimi_amd.kernels import (fused_w2_combine, grouped_w4a16_gemv, grouped_w4a16_swiglu_gemv,
+                                    moe_router, w4a16_dense)
+from local_kimi_amd.quant import W4A16Tensor, quantise
+
+
+def test_dense_rejects_wrong_dtypes_and_cpu_tensors():
+    x = torch.zeros((1, 64), dtype=torch.bfloat16)
+    p = torch.zeros((8, 32), dtype=torch.uint8)
+    s = torch.zeros((8, 2), dtype=torch.bfloat16)
+    with pytest.raises(TypeError):
+        w4a16_dense(x.float(), p, s)
+    with pytest.raises(TypeError):
+        w4a16_dense(x, p.to(torch.int8), s)
+    with pytest.raises(TypeError):
+        w4a16_dense(x, p, s.float())
+    with pytest.raises(ValueError, match="requires CUDA"):
+        w4a16_dense(x, p, s)
+
+
+def test_grouped_rejects_bad_indices_dtype_and_shapes():
+    x = torch.zeros((1, 64), dtype=torch.bfloat16)
+    p = torch.zeros((3, 8, 32), dtype=torch.uint8)
+    s = torch.zeros((3, 8, 2), dtype=torch.bfloat16)
+    with pytest.raises(TypeError, match="int64"):
+        grouped_w4a16_gemv(x, torch.zeros((1, 2), dtype=torch.int32), p, s)
+    with pytest.raises(ValueError, match="rank three"):
+        grouped_w4a16_gemv(x, torch.zeros((1, 2), dtype=torch.long), p[0], s[0])
+    with pytest.raises(ValueError, match="requires CUDA"):
+        grouped_w4a16_gemv(x, torch.zeros((1, 2), dtype=torch.long), p, s)
+
+
+def test_swiglu_and_combine_reject_mismatched_inputs():
+    x = torch.zeros((1, 64), dtype=torch.bfloat16)
+    idx = torch.zeros((1, 2), dtype=torch.long)
+    p = torch.zeros((3, 8, 32), dtype=torch.uint8)
+    s = torch.zeros((3, 8, 2), dtype=torch.bfloat16)
+    with pytest.raises(TypeError):
+        grouped_w4a16_swiglu_gemv(x, idx, p, s.float(), p, s)
+    act = torch.zeros((1, 2, 64), dtype=torch.bfloat16)
+    with pytest.raises(TypeError, match="float32"):
+        fused_w2_combine(act, idx, torch.zeros((1, 2), dtype=torch.float64), p, s)
+
+
+def test_router_rejects_bad_arguments():
+    with pytest.raises(TypeError):
+        moe_router(torch.zeros((1, 8), dtype=torch.float64), None, 2)
+    with pytest.raises(ValueError, match="requires CUDA"):
+        moe_router(torch.zeros((1, 8)), None, 2)
+
+
+def test_codec_validation():
+    with pytest.raises(TypeError):
+        quantise(torch.zeros((2, 64)))
+    with pytest.raises(ValueError, match="divisible"):
+        quantise(torch.zeros((2, 48), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="power-of-two"):
+        quantise(torch.zeros((2, 96), dtype=torch.bfloat16), group_size=96)
+    with pytest.raises(ValueError, match="requires a CUDA"):
+        quantise(torch.zeros((2, 64), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="scale shape"):
+        W4A16Tensor(torch.zeros((2, 64), dtype=torch.uint8), torch.zeros((2, 3), dtype=torch.bfloat16),
+                    (2, 128), group_size=32)
