@@ -34,11 +34,11 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // bf16 helpers
 
 __host__ __device__ inline float bf16_to_f32(uint16_t b) {
-  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+  return __builtin_bit_cast(float, static_cast<uint32_t>(b) << 16);
 }
 
 __host__ __device__ inline uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
   if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return 0x7FC0;  // NaN
   u += 0x7FFFu + ((u >> 16) & 1u);
   return static_cast<uint16_t>(u >> 16);

@@ -42,29 +42,70 @@ inline size_t stage_bytes(int ntok, int cpr) {
   return static_cast<size_t>(ntok) * cpr * (4 * sizeof(uint4) + sizeof(float));
 }
 
-// Stage nt activation rows (row stride `stride` elements) into LDS.
-__device__ inline void stage_x(const uint16_t* __restrict__ x, int64_t stride, int nt,
-                               const XStage st) {
-  const int cpr = st.cpr;
-  const int units = nt * cpr * 4;
-  for (int u = threadIdx.x; u < units; u += blockDim.x) {
-    const int j = u & 3;
-    const int rest = u >> 2;
-    const int tok = rest / cpr;
-    const int c = rest - tok * cpr;
-    const uint4 v = *reinterpret_cast<const uint4*>(x + tok * stride + c * 32 + j * 8);
-    uint32_t p[4];
-    pair_x8(v, p);
-    st.pair[(tok * 4 + j) * cpr + c] = make_uint4(p[0], p[1], p[2], p[3]);
-    const float s = sum4(sum_x8(v));
-    if (j == 0) st.off[tok * cpr + c] = kCodeOffset * s;
-  }
+// Write 8 activations (one dword j of chunk c of token tok) in pair order.
+__device__ inline void stage_unit(const uint4 v, int tok, int c, int j, const XStage& st) {
+  uint32_t p[4];
+  pair_x8(v, p);
+  st.pair[(tok * 4 + j) * st.cpr + c] = make_uint4(p[0], p[1], p[2], p[3]);
+  const float s = sum4(sum_x8(v));  // the 4 units of a chunk sit in one lane quad
+  if (j == 0) st.off[tok * st.cpr + c] = kCodeOffset * s;
 }
+
+// Activation staging in two phases so that every global load is in flight
+// before the first one is used: issue() loads up to UPT 16-byte units per
+// thread (addresses clamped in bounds, no branches), commit() writes them to
+// LDS. Units beyond UPT * blockDim (large multi-token stagings only) are
+// staged by a plain loop in commit().
+template <int UPT>
+struct XLoader {
+  uint4 v[UPT];
+
+  __device__ inline void issue(const uint16_t* __restrict__ x, int64_t stride, int nt,
+                               int cpr) {
+    const int units = nt * cpr * 4;
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      if (static_cast<int>(i * blockDim.x) < units) {  // uniform across the block
+        const int u = min(static_cast<int>(threadIdx.x + i * blockDim.x), units - 1);
+        const int j = u & 3;
+        const int rest = u >> 2;
+        const int tok = rest / cpr;
+        const int c = rest - tok * cpr;
+        v[i] = *reinterpret_cast<const uint4*>(x + tok * stride + c * 32 + j * 8);
+      }
+    }
+  }
+
+  __device__ inline void commit(const uint16_t* __restrict__ x, int64_t stride, int nt,
+                                const XStage& st) const {
+    const int cpr = st.cpr;
+    const int units = nt * cpr * 4;
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      const int u = threadIdx.x + i * blockDim.x;
+      if (u < units) {
+        const int rest = u >> 2;
+        const int tok = rest / cpr;
+        stage_unit(v[i], tok, rest - tok * cpr, u & 3, st);
+      }
+    }
+    for (int u = threadIdx.x + UPT * blockDim.x; u < units; u += blockDim.x) {
+      const int rest = u >> 2;
+      const int tok = rest / cpr;
+      const int c = rest - tok * cpr;
+      stage_unit(*reinterpret_cast<const uint4*>(x + tok * stride + c * 32 + (u & 3) * 8), tok,
+                 c, u & 3, st);
+    }
+  }
+};
+
+constexpr int kUpt = 8;
 
 // Geometry of one lane's share of a row block.
 template <int NR>
 struct Rows {
-  int64_t row[NR];
+  int64_t row[NR];   // this lane's weight rows
+  int64_t rowc[NR];  // the same, clamped into [0, n) for branch-free loads
   bool ok[NR];
   __device__ inline Rows(int64_t row_base, int64_t n) {
     const int lane = threadIdx.x & (kWave - 1);
@@ -72,6 +113,7 @@ struct Rows {
     for (int j = 0; j < NR; ++j) {
       row[j] = row_base + (lane >> 3) + 8 * j;
       ok[j] = row[j] < n;
+      rowc[j] = ok[j] ? row[j] : n - 1;
     }
   }
 };
@@ -92,36 +134,34 @@ __device__ inline Shape make_shape(int64_t k, int64_t group) {
   return s;
 }
 
-// Registers holding one batch of ITERS chunk columns for MATS matrices x NR rows.
+// Registers holding one batch of ITERS chunk columns for MATS matrices x NR
+// rows. load() issues every load of the batch without branches (addresses
+// clamped in bounds) and keeps the scales as raw bf16 bits, so no load result
+// is needed before the compute phase and all loads stay in flight together.
 template <int MATS, int NR, int ITERS>
 struct Batch {
   uint4 w[MATS][NR][ITERS];
-  float s[MATS][NR][ITERS];
+  uint16_t s[MATS][NR][ITERS];
 
   __device__ inline void load(const uint8_t* const (&wp)[MATS], const uint16_t* const (&ws)[MATS],
                               const Rows<NR>& rows, const Shape& sh, int cbase) {
     const int ph = threadIdx.x & 7;
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
-      const int c = cbase + ph + 8 * it;
+      const int c = min(cbase + ph + 8 * it, sh.cpr - 1);
 #pragma unroll
       for (int m = 0; m < MATS; ++m) {
 #pragma unroll
         for (int j = 0; j < NR; ++j) {
-          if (c < sh.cpr && rows.ok[j]) {
-            w[m][j][it] = load_stream_u4(wp[m] + rows.row[j] * sh.bytes_row + c * 16);
-            s[m][j][it] = bf16_to_f32(ws[m][rows.row[j] * sh.spr + (c >> sh.gshift)]);
-          } else {
-            w[m][j][it] = make_uint4(0, 0, 0, 0);
-            s[m][j][it] = 0.f;
-          }
+          w[m][j][it] = load_stream_u4(wp[m] + rows.rowc[j] * sh.bytes_row + c * 16);
+          s[m][j][it] = ws[m][rows.rowc[j] * sh.spr + (c >> sh.gshift)];
         }
       }
     }
   }
 
   template <int NTOK>
-  __device__ inline void compute(const XStage& st, int nt, int cbase,
+  __device__ inline void compute(const XStage& st, int nt, int cbase, const Rows<NR>& rows,
                                  float (&part)[MATS][NR][NTOK]) const {
     const int ph = threadIdx.x & 7;
 #pragma unroll
@@ -150,7 +190,8 @@ struct Batch {
                 acc = dot8_int4(w[m][j][it].y, xq[1], acc);
                 acc = dot8_int4(w[m][j][it].z, xq[2], acc);
                 acc = dot8_int4(w[m][j][it].w, xq[3], acc);
-                part[m][j][tok] = fmaf(s[m][j][it], acc - xo, part[m][j][tok]);
+                const float sc = rows.ok[j] ? bf16_to_f32(s[m][j][it]) : 0.f;
+                part[m][j][tok] = fmaf(sc, acc - xo, part[m][j][tok]);
               }
             }
           }
@@ -188,18 +229,230 @@ __device__ inline void gemv_block(const uint8_t* const (&wp)[MATS],
                                   const Shape& sh, const uint16_t* __restrict__ x,
                                   int64_t xstride, int nt, const XStage& st,
                                   float (&part)[MATS][NR][NTOK]) {
+  XLoader<kUpt> xl;
+  xl.issue(x, xstride, nt, sh.cpr);
   Batch<MATS, NR, ITERS> b;
   b.load(wp, ws, rows, sh, 0);
-  stage_x(x, xstride, nt, st);
+  xl.commit(x, xstride, nt, st);
   __syncthreads();
   zero_and(part);
   for (int cbase = 0;;) {
-    b.template compute<NTOK>(st, nt, cbase, part);
+    b.template compute<NTOK>(st, nt, cbase, rows, part);
     cbase += 8 * ITERS;
     if (cbase >= sh.cpr) break;
     b.load(wp, ws, rows, sh, cbase);
   }
   reduce8(part);
+}
+
+// ---------------------------------------------------------------------------
+// K-split GEMV core (decode shapes).
+//
+// A block of KW waves covers 8*NR weight rows; its waves split the reduction
+// axis. Lane (rg = lane >> 3, ph = lane & 7) of wave w owns the 32-wide chunk
+// columns c = w*8 + ph + 8*KW*i (i < CI) and the rows row0 + rg + 8*j (j < NR).
+// Each lane loads its own activation chunk(s) straight into registers (the 8
+// lanes sharing a chunk hit the same addresses, which the memory pipeline
+// merges), then every weight and scale load, all before first use. Partial
+// sums are reduced over the 8 chunk lanes with DPP and over the block's waves
+// through LDS in fixed wave order, so results are bit-reproducible.
+
+constexpr int kMaxKWaves = 16;
+
+template <int MATS, int NR, int NTOK, int CI>
+struct KSplit {
+  uint4 xv[NTOK][CI][4];
+  uint4 w[MATS][NR][CI];
+  uint16_t s[MATS][NR][CI];
+  float part[MATS][NR][NTOK];
+
+  __device__ inline static int chunk(int wave, int kw, int i) {
+    return wave * 8 + (threadIdx.x & 7) + 8 * kw * i;
+  }
+
+  // activation chunks of nt tokens (row stride xstride), clamped in bounds
+  __device__ inline void load_x(const uint16_t* __restrict__ x, int64_t xstride, int nt,
+                                int wave, int kw, int cpr) {
+#pragma unroll
+    for (int t = 0; t < NTOK; ++t) {
+      const int tc = min(t, nt - 1);
+#pragma unroll
+      for (int i = 0; i < CI; ++i) {
+        const int c = min(chunk(wave, kw, i), cpr - 1);
+        const uint4* src = reinterpret_cast<const uint4*>(x + tc * xstride + c * 32);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xv[t][i][q] = src[q];
+      }
+    }
+  }
+
+  __device__ inline void load_w(const uint8_t* const (&wp)[MATS], const uint16_t* const (&ws)[MATS],
+                                const Rows<NR>& rows, const Shape& sh, int wave, int kw) {
+#pragma unroll
+    for (int i = 0; i < CI; ++i) {
+      const int c = min(chunk(wave, kw, i), sh.cpr - 1);
+#pragma unroll
+      for (int m = 0; m < MATS; ++m)
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+          w[m][j][i] = load_stream_u4(wp[m] + rows.rowc[j] * sh.bytes_row + c * 16);
+          s[m][j][i] = ws[m][rows.rowc[j] * sh.spr + (c >> sh.gshift)];
+        }
+    }
+  }
+
+  __device__ inline void compute(const Rows<NR>& rows, int nt, int wave, int kw, int cpr) {
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int j = 0; j < NR; ++j)
+#pragma unroll
+        for (int t = 0; t < NTOK; ++t) part[m][j][t] = 0.f;
+#pragma unroll
+    for (int i = 0; i < CI; ++i) {
+      const bool cval = chunk(wave, kw, i) < cpr;
+#pragma unroll
+      for (int t = 0; t < NTOK; ++t) {
+        uint32_t xp[4][4];
+        float xs = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          pair_x8(xv[t][i][q], xp[q]);
+          xs += sum_x8(xv[t][i][q]);
+        }
+        const float xo = kCodeOffset * xs;
+#pragma unroll
+        for (int m = 0; m < MATS; ++m)
+#pragma unroll
+          for (int j = 0; j < NR; ++j) {
+            // two independent chains per chunk for more ILP
+            float a0 = dot8_int4(w[m][j][i].x, xp[0], 0.f);
+            float a1 = dot8_int4(w[m][j][i].y, xp[1], 0.f);
+            a0 = dot8_int4(w[m][j][i].z, xp[2], a0);
+            a1 = dot8_int4(w[m][j][i].w, xp[3], a1);
+            const float sc = (cval && rows.ok[j] && t < nt) ? bf16_to_f32(s[m][j][i]) : 0.f;
+            part[m][j][t] = fmaf(sc, (a0 + a1) - xo, part[m][j][t]);
+          }
+      }
+    }
+  }
+
+  // DPP over the 8 chunk lanes, then LDS over the block's waves. After the
+  // barrier, red[v][idx] holds wave v's partial for idx = ((m*NR + j)*NTOK + t)*8 + rg.
+  __device__ inline void reduce_to_lds(float (*red)[MATS * NR * NTOK * 8], int wave) {
+    const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int j = 0; j < NR; ++j)
+#pragma unroll
+        for (int t = 0; t < NTOK; ++t) {
+          const float v = sum8(part[m][j][t]);
+          if ((lane & 7) == 0) red[wave][((m * NR + j) * NTOK + t) * 8 + (lane >> 3)] = v;
+        }
+    __syncthreads();
+  }
+};
+
+// Sum of idx over the kw waves, fixed order.
+template <int W>
+__device__ inline float wave_total(const float (*red)[W], int kw, int idx) {
+  float acc = 0.f;
+  for (int v = 0; v < kw; ++v) acc += red[v][idx];
+  return acc;
+}
+
+struct KGeom {
+  int kw;  // waves per block along K
+  int ci;  // chunks per lane
+};
+
+inline KGeom kgeom(int64_t k) {
+  const int cpr = static_cast<int>(k / 32);
+  KGeom g;
+  g.kw = min(kMaxKWaves, (cpr + 7) / 8);
+  g.ci = (cpr + 8 * g.kw - 1) / (8 * g.kw);
+  return g;
+}
+
+// dense: y[tok, n] for NTOK tokens per block (blockIdx.y = token block)
+template <int NR, int NTOK, int CI>
+__global__ void __launch_bounds__(1024)
+dense_ksplit_kernel(const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
+                    const uint16_t* __restrict__ scales, uint16_t* __restrict__ y, int64_t m,
+                    int64_t n, int64_t k, int64_t group) {
+  __shared__ float red[kMaxKWaves][NR * NTOK * 8];
+  const int kw = blockDim.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const Shape sh = make_shape(k, group);
+  const int64_t tok0 = static_cast<int64_t>(blockIdx.y) * NTOK;
+  const int nt = static_cast<int>(min<int64_t>(NTOK, m - tok0));
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 8 * NR;
+  const Rows<NR> rows(row0, n);
+  const uint8_t* const wp[1] = {packed};
+  const uint16_t* const ws[1] = {scales};
+  KSplit<1, NR, NTOK, CI> ks;
+  ks.load_x(x + tok0 * k, k, nt, wave, kw, sh.cpr);
+  ks.load_w(wp, ws, rows, sh, wave, kw);
+  ks.compute(rows, nt, wave, kw, sh.cpr);
+  ks.reduce_to_lds(red, wave);
+  const int idx = threadIdx.x;
+  if (idx < NR * NTOK * 8) {
+    const int rg = idx & 7, t = (idx >> 3) % NTOK, j = (idx >> 3) / NTOK;
+    const int64_t row = row0 + rg + 8 * j;
+    if (t < nt && row < n) y[(tok0 + t) * n + row] = f32_to_bf16(wave_total(red, kw, idx));
+  }
+}
+
+// grouped (MATS=1) / fused gate-up SwiGLU (MATS=2): blockIdx.y = token-route
+template <int MATS, int NR, int CI>
+__global__ void __launch_bounds__(1024)
+grouped_ksplit_kernel(const uint16_t* __restrict__ x, const int64_t* __restrict__ idx,
+                      const uint8_t* __restrict__ p0, const uint16_t* __restrict__ s0,
+                      const uint8_t* __restrict__ p1, const uint16_t* __restrict__ s1,
+                      uint16_t* __restrict__ out, int64_t routes, int64_t experts, int64_t n,
+                      int64_t k, int64_t group) {
+  __shared__ float red[kMaxKWaves][MATS * NR * 8];
+  const int kw = blockDim.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const Shape sh = make_shape(k, group);
+  const int64_t pair = blockIdx.y;
+  const int64_t t = pair / routes;
+  KSplit<MATS, NR, 1, CI> ks;
+  ks.load_x(x + t * k, k, 1, wave, kw, sh.cpr);
+  // an index outside the bank is an empty route: read expert 0, write zeros
+  const int64_t e_raw = idx[pair];
+  const bool valid = e_raw >= 0 && e_raw < experts;
+  const int64_t e = valid ? e_raw : 0;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 8 * NR;
+  const Rows<NR> rows(row0, n);
+  const int64_t wstride = n * sh.bytes_row;
+  const int64_t sstride = n * sh.spr;
+  if constexpr (MATS == 1) {
+    const uint8_t* const wp[1] = {p0 + e * wstride};
+    const uint16_t* const ws[1] = {s0 + e * sstride};
+    ks.load_w(wp, ws, rows, sh, wave, kw);
+  } else {
+    const uint8_t* const wp[2] = {p0 + e * wstride, p1 + e * wstride};
+    const uint16_t* const ws[2] = {s0 + e * sstride, s1 + e * sstride};
+    ks.load_w(wp, ws, rows, sh, wave, kw);
+  }
+  ks.compute(rows, 1, wave, kw, sh.cpr);
+  ks.reduce_to_lds(red, wave);
+  const int o = threadIdx.x;
+  if (o < NR * 8) {
+    const int rg = o & 7, j = o >> 3;
+    const int64_t row = row0 + rg + 8 * j;
+    if (row < n) {
+      uint16_t v;
+      if constexpr (MATS == 1) {
+        v = f32_to_bf16(wave_total(red, kw, j * 8 + rg));
+      } else {
+        v = swiglu_bf16(wave_total(red, kw, j * 8 + rg), wave_total(red, kw, (NR + j) * 8 + rg));
+      }
+      out[pair * n + row] = valid ? v : static_cast<uint16_t>(0);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -288,18 +541,19 @@ __device__ int64_t route_token(const float* __restrict__ logits, const float* __
   const int lane = threadIdx.x & (kWave - 1);
   float s[EPL];
   uint32_t key[EPL];
+  bool live[EPL];  // not yet selected (every real expert is a candidate, whatever its key)
+  float lg[EPL], bs[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {  // all loads first, addresses clamped in bounds
+    const int id = min(lane * EPL + j, ne - 1);
+    lg[j] = logits[id];
+    bs[j] = bias ? bias[id] : 0.0f;
+  }
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
-    const int id = lane * EPL + j;
-    if (id < ne) {
-      const float l = logits[id];
-      s[j] = 1.0f / (1.0f + expf(-l));
-      const float c = s[j] + (bias ? bias[id] : 0.0f);
-      key[j] = orderable(c);
-    } else {
-      s[j] = 0.f;
-      key[j] = 0u;
-    }
+    live[j] = lane * EPL + j < ne;
+    s[j] = 1.0f / (1.0f + expf(-lg[j]));
+    key[j] = live[j] ? orderable(s[j] + bs[j]) : 0u;
   }
   float ssum = 0.f;
   int64_t mine = -1;
@@ -307,32 +561,35 @@ __device__ int64_t route_token(const float* __restrict__ logits, const float* __
   int64_t wanted = -1;
   for (int rr = 0; rr < top_k; ++rr) {
     uint32_t kb = 0u;
-    int jb = 0;
+    int jb = -1;
 #pragma unroll
     for (int j = 0; j < EPL; ++j)
-      if (key[j] > kb) {
+      if (live[j] && (jb < 0 || key[j] > kb)) {
         kb = key[j];
         jb = j;
       }
-    const uint32_t kmax = wave_max_u32(kb);
-    const uint32_t cand = (kb == kmax && kb != 0u) ? static_cast<uint32_t>(lane * EPL + jb) : 0xFFFFFFFFu;
+    const uint32_t kmax = wave_max_u32(jb >= 0 ? kb : 0u);
+    const uint32_t cand =
+        (jb >= 0 && kb == kmax) ? static_cast<uint32_t>(lane * EPL + jb) : 0xFFFFFFFFu;
     const uint32_t sel = wave_min_u32(cand);
-    const int owner = static_cast<int>(sel / EPL);
-    const int slot = static_cast<int>(sel % EPL);
+    // top_k <= ne guarantees a live candidate; stay in range regardless
+    const uint32_t safe = sel < static_cast<uint32_t>(ne) ? sel : 0u;
+    const int owner = static_cast<int>(safe / EPL);
+    const int slot = static_cast<int>(safe % EPL);
     float local = 0.f;
 #pragma unroll
     for (int j = 0; j < EPL; ++j)
       if (j == slot) {
         local = s[j];
-        if (lane == owner) key[j] = 0u;
+        if (lane == owner) live[j] = false;
       }
     const float score = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(local), owner));
     ssum += score;
     if (lane == rr) {
-      mine = sel;
+      mine = safe;
       my_score = score;
     }
-    if (rr == want) wanted = sel;
+    if (rr == want) wanted = safe;
   }
   if (idx_out != nullptr && lane < top_k) {
     const float denom = ssum + 1e-20f;
@@ -373,17 +630,21 @@ moe_gateup_kernel(const uint16_t* __restrict__ x, const float* __restrict__ logi
   const int64_t t = pair / routes;
   const int r = static_cast<int>(pair - t * routes);
   const int ne = static_cast<int>(experts - 1);
+  const Shape sh = make_shape(h, group);
+  const XStage st = make_stage(smem, 1, sh.cpr);
+  // the token's activations do not depend on routing: load them first
+  XLoader<kUpt> xl;
+  xl.issue(x + t * h, h, 1, sh.cpr);
   int64_t e;
   if (r < top_k) {
     const bool writer = (r == 0 && blockIdx.x == 0 && threadIdx.x < kWave);
     e = route_token<EPL>(logits + t * ne, bias, ne, top_k, r, scaling, renorm,
                          writer ? idx_out + t * top_k : nullptr,
                          writer ? w_out + t * top_k : nullptr);
+    if (e < 0 || e >= ne) e = 0;  // unreachable for top_k <= ne; keeps reads in the bank
   } else {
     e = experts - 1;
   }
-  const Shape sh = make_shape(h, group);
-  const XStage st = make_stage(smem, 1, sh.cpr);
   const int64_t row_base =
       (static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave) * 8;
   const Rows<1> rows(row_base, inter);
@@ -391,20 +652,97 @@ moe_gateup_kernel(const uint16_t* __restrict__ x, const float* __restrict__ logi
   const int64_t sstride = inter * sh.spr;
   const uint8_t* const wp[2] = {w1p + e * wstride, w3p + e * wstride};
   const uint16_t* const ws[2] = {w1s + e * sstride, w3s + e * sstride};
+  Batch<2, 1, ITERS> b;
+  b.load(wp, ws, rows, sh, 0);
+  xl.commit(x + t * h, h, 1, st);
+  __syncthreads();
   float part[2][1][1];
-  gemv_block<2, 1, 1, ITERS>(wp, ws, rows, sh, x + t * h, h, 1, st, part);
+  zero_and(part);
+  for (int cbase = 0;;) {
+    b.template compute<1>(st, 1, cbase, rows, part);
+    cbase += 8 * ITERS;
+    if (cbase >= sh.cpr) break;
+    b.load(wp, ws, rows, sh, cbase);
+  }
+  reduce8(part);
   if ((threadIdx.x & 7) == 0 && rows.ok[0])
     act[pair * inter + rows.row[0]] = swiglu_bf16(part[0][0][0], part[1][0][0]);
 }
 
-// ---------------------------------------------------------------------------
-// W2 + combine: blockIdx.y = token, rows of H from blockIdx.x. Routes are
-// processed in batches of RB with all of a batch's loads in flight at once.
-// Route r's expert is idx[t * idx_stride + r]; when shared_id >= 0 the last
-// route uses shared_id instead. Combine weight of route r < routes-1 is
-// cw[t * cw_stride + r]; the last route is added with weight 1.
+// decode gate/up + SwiGLU with the router, K-split form. blockIdx.y =
+// t * (top_k + 1) + r; route top_k is the shared expert (bank entry
+// experts - 1). Activations are loaded before routing (they do not depend on
+// it); every wave recomputes the token's routing so no extra launch or block
+// barrier is needed before the weight loads.
+template <int NR, int CI, int EPL>
+__global__ void __launch_bounds__(1024)
+moe_gateup_ksplit_kernel(const uint16_t* __restrict__ x, const float* __restrict__ logits,
+                         const float* __restrict__ bias, const uint8_t* __restrict__ w1p,
+                         const uint16_t* __restrict__ w1s, const uint8_t* __restrict__ w3p,
+                         const uint16_t* __restrict__ w3s, uint16_t* __restrict__ act,
+                         int64_t* __restrict__ idx_out, float* __restrict__ w_out,
+                         int64_t experts, int64_t h, int64_t inter, int top_k, float scaling,
+                         int renorm, int64_t group) {
+  __shared__ float red[kMaxKWaves][2 * NR * 8];
+  const int kw = blockDim.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int routes = top_k + 1;
+  const int64_t pair = blockIdx.y;
+  const int64_t t = pair / routes;
+  const int r = static_cast<int>(pair - t * routes);
+  const int ne = static_cast<int>(experts - 1);
+  const Shape sh = make_shape(h, group);
+  __shared__ int64_t routed_expert;
+  KSplit<2, NR, 1, CI> ks;
+  ks.load_x(x + t * h, h, 1, wave, kw, sh.cpr);
+  int64_t e;
+  if (r < top_k) {  // block-uniform
+    if (wave == 0) {  // one wave routes; the others wait at the barrier
+      const bool writer = (r == 0 && blockIdx.x == 0);
+      const int64_t sel = route_token<EPL>(logits + t * ne, bias, ne, top_k, r, scaling, renorm,
+                                           writer ? idx_out + t * top_k : nullptr,
+                                           writer ? w_out + t * top_k : nullptr);
+      if ((threadIdx.x & (kWave - 1)) == 0) routed_expert = sel;
+    }
+    __syncthreads();
+    e = routed_expert;
+    if (e < 0 || e >= ne) e = 0;  // unreachable for top_k <= ne; keeps reads in the bank
+  } else {
+    e = experts - 1;
+  }
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 8 * NR;
+  const Rows<NR> rows(row0, inter);
+  const int64_t wstride = inter * sh.bytes_row;
+  const int64_t sstride = inter * sh.spr;
+  const uint8_t* const wp[2] = {w1p + e * wstride, w3p + e * wstride};
+  const uint16_t* const ws[2] = {w1s + e * sstride, w3s + e * sstride};
+  ks.load_w(wp, ws, rows, sh, wave, kw);
+  ks.compute(rows, 1, wave, kw, sh.cpr);
+  ks.reduce_to_lds(red, wave);
+  const int o = threadIdx.x;
+  if (o < NR * 8) {
+    const int rg = o & 7, j = o >> 3;
+    const int64_t row = row0 + rg + 8 * j;
+    if (row < inter)
+      act[pair * inter + row] =
+          swiglu_bf16(wave_total(red, kw, j * 8 + rg), wave_total(red, kw, (NR + j) * 8 + rg));
+  }
+}
 
-template <int ITERS, int RB>
+// ---------------------------------------------------------------------------
+// W2 + combine: blockIdx.y = token, blockIdx.x = 8 rows of H. The block's
+// kW2Waves waves split the routes (wave w takes routes w, w + kW2Waves, ...),
+// so each wave keeps at most RPW routes of weight loads in flight; all waves
+// share the staged activations of every route. Route outputs are rounded to
+// bf16 and combined by one wave in route order: weighted fp32 sum of routes
+// 0..R-2, rounded to bf16, plus the last route (the shared expert) with
+// weight 1. Route r's expert is idx[t * idx_stride + r]; when shared_id >= 0
+// the last route uses shared_id. Indices outside the bank read expert 0 and
+// count as 0.
+
+constexpr int kW2Waves = 4;
+
+template <int ITERS, int RPW>
 __global__ void __launch_bounds__(256)
 w2_combine_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ idx,
                   int64_t idx_stride, int64_t shared_id, const float* __restrict__ cw,
@@ -413,68 +751,70 @@ w2_combine_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ 
                   int64_t experts, int64_t h, int64_t inter, int64_t group) {
   extern __shared__ uint4 smem[];
   const int64_t t = blockIdx.y;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const Shape sh = make_shape(inter, group);
   const XStage st = make_stage(smem, routes, sh.cpr);
-  const int64_t row_base =
-      (static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave) * 8;
+  // expert ids of this wave's routes: wave-uniform scalar loads, all issued
+  // before any weight load
+  int64_t e_of[RPW];
+#pragma unroll
+  for (int q = 0; q < RPW; ++q) {
+    const int r = min(wave + kW2Waves * q, routes - 1);
+    e_of[q] = (shared_id >= 0 && r == routes - 1) ? shared_id : idx[t * idx_stride + r];
+  }
+  float* eo_lds = reinterpret_cast<float*>(st.off + static_cast<size_t>(routes) * sh.cpr);
+  const uint16_t* xa = act + t * routes * inter;
+
+  XLoader<kUpt> xl;
+  xl.issue(xa, inter, routes, sh.cpr);
+
+  const int64_t row_base = static_cast<int64_t>(blockIdx.x) * 8;
   const Rows<1> rows(row_base, h);
   const int64_t wstride = h * sh.bytes_row;
   const int64_t sstride = h * sh.spr;
-  const uint16_t* xa = act + t * routes * inter;
-  // expert of route r; indices outside the bank read expert 0 and count as 0
-  auto expert_of = [&](int r, bool& valid) -> int64_t {
-    const int64_t e = (shared_id >= 0 && r == routes - 1) ? shared_id : idx[t * idx_stride + r];
-    valid = e >= 0 && e < experts;
-    return valid ? e : 0;
-  };
+  Batch<1, 1, ITERS> b[RPW];
+  bool valid[RPW];
+#pragma unroll
+  for (int q = 0; q < RPW; ++q) {
+    valid[q] = e_of[q] >= 0 && e_of[q] < experts;
+    const int64_t e = valid[q] ? e_of[q] : 0;
+    const uint8_t* const wp[1] = {w2p + e * wstride};
+    const uint16_t* const ws[1] = {w2s + e * sstride};
+    b[q].load(wp, ws, rows, sh, 0);
+  }
+  xl.commit(xa, inter, routes, st);
+  __syncthreads();
 
-  float routed = 0.f;
-  float last = 0.f;
-  bool staged = false;
-  for (int rb0 = 0; rb0 < routes; rb0 += RB) {
-    Batch<1, 1, ITERS> b[RB];
 #pragma unroll
-    for (int q = 0; q < RB; ++q) {
-      const int r = rb0 + q;
-      if (r < routes) {
-        bool valid;
-        const int64_t e = expert_of(r, valid);
-        const uint8_t* const wp[1] = {w2p + e * wstride};
-        const uint16_t* const ws[1] = {w2s + e * sstride};
-        b[q].load(wp, ws, rows, sh, 0);
+  for (int q = 0; q < RPW; ++q) {
+    const int r = wave + kW2Waves * q;
+    if (r < routes) {  // wave-uniform
+      const int64_t e = valid[q] ? e_of[q] : 0;
+      const uint8_t* const wp[1] = {w2p + e * wstride};
+      const uint16_t* const ws[1] = {w2s + e * sstride};
+      XStage sr = st;
+      sr.pair += static_cast<size_t>(r) * 4 * sh.cpr;
+      sr.off += static_cast<size_t>(r) * sh.cpr;
+      float part[1][1][1] = {{{0.f}}};
+      for (int cbase = 0;;) {
+        b[q].template compute<1>(sr, 1, cbase, rows, part);
+        cbase += 8 * ITERS;
+        if (cbase >= sh.cpr) break;
+        b[q].load(wp, ws, rows, sh, cbase);
       }
-    }
-    if (!staged) {
-      stage_x(xa, inter, routes, st);
-      __syncthreads();
-      staged = true;
-    }
-#pragma unroll
-    for (int q = 0; q < RB; ++q) {
-      const int r = rb0 + q;
-      if (r < routes) {
-        bool valid;
-        const int64_t e = expert_of(r, valid);
-        const uint8_t* const wp[1] = {w2p + e * wstride};
-        const uint16_t* const ws[1] = {w2s + e * sstride};
-        float part[1][1][1] = {{{0.f}}};
-        XStage sr = st;
-        sr.pair += static_cast<size_t>(r) * 4 * sh.cpr;
-        sr.off += static_cast<size_t>(r) * sh.cpr;
-        for (int cbase = 0;;) {
-          b[q].template compute<1>(sr, 1, cbase, part);
-          cbase += 8 * ITERS;
-          if (cbase >= sh.cpr) break;
-          b[q].load(wp, ws, rows, sh, cbase);
-        }
-        const float eo = valid ? round_bf16(sum8(part[0][0][0])) : 0.f;
-        if (r < routes - 1) routed += eo * cw[t * cw_stride + r];
-        else last = eo;
-      }
+      const float eo = valid[q] ? round_bf16(sum8(part[0][0][0])) : 0.f;
+      const int lane = threadIdx.x & (kWave - 1);
+      if ((lane & 7) == 0) eo_lds[r * 8 + (lane >> 3)] = eo;
     }
   }
-  if ((threadIdx.x & 7) == 0 && rows.ok[0])
-    y[t * h + rows.row[0]] = f32_to_bf16(round_bf16(routed) + last);
+  __syncthreads();
+  if (threadIdx.x < 8) {
+    const int rl = threadIdx.x;
+    float routed = 0.f;
+    for (int r = 0; r + 1 < routes; ++r) routed += eo_lds[r * 8 + rl] * cw[t * cw_stride + r];
+    const int64_t row = row_base + rl;
+    if (row < h) y[t * h + row] = f32_to_bf16(round_bf16(routed) + eo_lds[(routes - 1) * 8 + rl]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -527,6 +867,8 @@ using namespace lk;
 
 extern "C" {
 
+constexpr int kNR = 2;  // weight rows per lane in the K-split kernels
+
 int lk_w4a16_dense(const uint16_t* x, const uint8_t* packed, const uint16_t* scales, uint16_t* y,
                    int64_t m, int64_t n, int64_t k, int64_t group_size, void* stream) {
   LK_REQUIRE(packed && scales && y, "null pointer argument");
@@ -535,21 +877,38 @@ int lk_w4a16_dense(const uint16_t* x, const uint8_t* packed, const uint16_t* sca
   if (int rc = check_pow2_group(k, group_size)) return rc;
   if (m == 0) return LK_OK;
   LK_REQUIRE(x != nullptr, "null activation pointer");
-  const int cpr = static_cast<int>(k / 32);
-  int ntok = m >= 8 ? 8 : m >= 4 ? 4 : m >= 2 ? 2 : 1;
-  while (ntok > 1 && stage_bytes(ntok, cpr) > kMaxLds) ntok /= 2;
-  LK_REQUIRE(stage_bytes(ntok, cpr) <= kMaxLds, "reduction width %lld too large", (long long)k);
-  const int nw = waves_per_block();
-  const int64_t rows_per_block = nw * 8;
-  dim3 grid(static_cast<unsigned>((n + rows_per_block - 1) / rows_per_block),
-            static_cast<unsigned>((m + ntok - 1) / ntok));
-  const size_t lds = stage_bytes(ntok, cpr);
   hipStream_t s = as_stream(stream);
+  const KGeom g = kgeom(k);
+  const int ntok = m >= 4 ? 4 : m >= 2 ? 2 : 1;
+  LK_REQUIRE((m + ntok - 1) / ntok <= 65535, "too many tokens for one call");
+  if (g.ci <= 2) {
+    dim3 grid(static_cast<unsigned>((n + 8 * kNR - 1) / (8 * kNR)),
+              static_cast<unsigned>((m + ntok - 1) / ntok));
+    const int threads = g.kw * kWave;
+#define LK_DENSE_KS(NT, CIV) \
+  dense_ksplit_kernel<kNR, NT, CIV><<<grid, threads, 0, s>>>(x, packed, scales, y, m, n, k, group_size)
+    if (g.ci == 1) {
+      if (ntok == 1) LK_DENSE_KS(1, 1); else if (ntok == 2) LK_DENSE_KS(2, 1); else LK_DENSE_KS(4, 1);
+    } else {
+      if (ntok == 1) LK_DENSE_KS(1, 2); else if (ntok == 2) LK_DENSE_KS(2, 2); else LK_DENSE_KS(4, 2);
+    }
+#undef LK_DENSE_KS
+    return check_launch("lk_w4a16_dense");
+  }
+  // very wide reductions (K > 8192): LDS-staged kernel
+  const int cpr = static_cast<int>(k / 32);
+  int nt2 = m >= 8 ? 8 : m >= 4 ? 4 : m >= 2 ? 2 : 1;
+  while (nt2 > 1 && stage_bytes(nt2, cpr) > kMaxLds) nt2 /= 2;
+  LK_REQUIRE(stage_bytes(nt2, cpr) <= kMaxLds, "reduction width %lld too large", (long long)k);
+  const int nw = waves_per_block();
+  dim3 grid(static_cast<unsigned>((n + nw * 8 - 1) / (nw * 8)),
+            static_cast<unsigned>((m + nt2 - 1) / nt2));
+  const size_t lds = stage_bytes(nt2, cpr);
   const int iters = pick_iters(cpr);
 #define LK_DENSE_LAUNCH(NT)                                                                 \
   LK_ITERS_CASES(iters, (dense_gemv_kernel<1, NT, IT><<<grid, nw * kWave, lds, s>>>(        \
                             x, packed, scales, y, m, n, k, group_size)))
-  switch (ntok) {
+  switch (nt2) {
     case 1: LK_DENSE_LAUNCH(1); break;
     case 2: LK_DENSE_LAUNCH(2); break;
     case 4: LK_DENSE_LAUNCH(4); break;
@@ -573,6 +932,22 @@ static int grouped_common(const uint16_t* x, const int64_t* idx, const uint8_t* 
   const int64_t pairs = tokens * routes;
   LK_REQUIRE(pairs <= 65535, "%s: at most 65535 token-routes per call, got %lld", name,
              (long long)pairs);
+  hipStream_t s = as_stream(stream);
+  const KGeom g = kgeom(k);
+  if (g.ci <= 2) {
+    dim3 grid(static_cast<unsigned>((n + 8 * kNR - 1) / (8 * kNR)), static_cast<unsigned>(pairs));
+    const int threads = g.kw * kWave;
+#define LK_GROUPED_KS(MATS, CIV)                                                      \
+  grouped_ksplit_kernel<MATS, kNR, CIV><<<grid, threads, 0, s>>>(x, idx, p0, s0,      \
+      swiglu ? p1 : p0, swiglu ? s1 : s0, out, routes, experts, n, k, group)
+    if (swiglu) {
+      if (g.ci == 1) LK_GROUPED_KS(2, 1); else LK_GROUPED_KS(2, 2);
+    } else {
+      if (g.ci == 1) LK_GROUPED_KS(1, 1); else LK_GROUPED_KS(1, 2);
+    }
+#undef LK_GROUPED_KS
+    return check_launch(name);
+  }
   const int cpr = static_cast<int>(k / 32);
   LK_REQUIRE(stage_bytes(1, cpr) <= kMaxLds, "reduction width %lld too large", (long long)k);
   const int nw = waves_per_block();
@@ -580,7 +955,6 @@ static int grouped_common(const uint16_t* x, const int64_t* idx, const uint8_t* 
   dim3 grid(static_cast<unsigned>((n + rows_per_block - 1) / rows_per_block),
             static_cast<unsigned>(pairs));
   const size_t lds = stage_bytes(1, cpr);
-  hipStream_t s = as_stream(stream);
   const int iters = pick_iters(cpr);
   if (swiglu) {
     LK_ITERS_CASES(iters, (grouped_gemv_kernel<2, IT><<<grid, nw * kWave, lds, s>>>(
@@ -614,24 +988,22 @@ static int w2_combine_launch(const uint16_t* act, const int64_t* idx, int64_t id
                              int64_t tokens, int64_t routes, int64_t experts, int64_t h,
                              int64_t inter, int64_t group, hipStream_t s) {
   const int cpr = static_cast<int>(inter / 32);
-  LK_REQUIRE(stage_bytes(static_cast<int>(routes), cpr) <= kMaxLds,
-             "routes x reduction width too large for one block (%lld x %lld)",
+  const size_t lds = stage_bytes(static_cast<int>(routes), cpr) + routes * 8 * sizeof(float);
+  LK_REQUIRE(lds <= kMaxLds, "routes x reduction width too large for one block (%lld x %lld)",
              (long long)routes, (long long)inter);
+  LK_REQUIRE(routes <= 8 * kW2Waves, "at most %d routes per token", 8 * kW2Waves);
   LK_REQUIRE(tokens <= 65535, "at most 65535 tokens per call");
-  const int nw = waves_per_block();
-  const int64_t rows_per_block = nw * 8;
-  dim3 grid(static_cast<unsigned>((h + rows_per_block - 1) / rows_per_block),
-            static_cast<unsigned>(tokens));
-  const size_t lds = stage_bytes(static_cast<int>(routes), cpr);
+  dim3 grid(static_cast<unsigned>((h + 7) / 8), static_cast<unsigned>(tokens));
   const int iters = pick_iters(cpr);
-  if (iters <= 4) {
-    LK_ITERS_CASES(iters, (w2_combine_kernel<IT, 9><<<grid, nw * kWave, lds, s>>>(
-                              act, idx, idx_stride, shared_id, cw, cw_stride, w2p, w2s, y,
-                              static_cast<int>(routes), experts, h, inter, group)));
+  const int r = static_cast<int>(routes);
+  if (routes <= 3 * kW2Waves) {
+    LK_ITERS_CASES(iters, (w2_combine_kernel<IT, 3><<<grid, kW2Waves * kWave, lds, s>>>(
+                              act, idx, idx_stride, shared_id, cw, cw_stride, w2p, w2s, y, r,
+                              experts, h, inter, group)));
   } else {
-    LK_ITERS_CASES(iters, (w2_combine_kernel<IT, 3><<<grid, nw * kWave, lds, s>>>(
-                              act, idx, idx_stride, shared_id, cw, cw_stride, w2p, w2s, y,
-                              static_cast<int>(routes), experts, h, inter, group)));
+    LK_ITERS_CASES(iters, (w2_combine_kernel<IT, 8><<<grid, kW2Waves * kWave, lds, s>>>(
+                              act, idx, idx_stride, shared_id, cw, cw_stride, w2p, w2s, y, r,
+                              experts, h, inter, group)));
   }
   return check_launch("w2_combine");
 }
@@ -683,6 +1055,24 @@ static int moe_gateup_launch(const uint16_t* x, const float* logits, const float
                              int64_t group_size, hipStream_t s) {
   const int64_t routes = top_k + 1;
   LK_REQUIRE(tokens * routes <= 65535, "at most 65535 token-routes per call");
+  const KGeom g = kgeom(h);
+  if (g.ci <= 2) {
+    dim3 grid(static_cast<unsigned>((i + 8 * kNR - 1) / (8 * kNR)),
+              static_cast<unsigned>(tokens * routes));
+    const int threads = g.kw * kWave;
+    const int kk = static_cast<int>(top_k);
+#define LK_MOE_KS(CIV, EPLV)                                                              \
+  moe_gateup_ksplit_kernel<kNR, CIV, EPLV><<<grid, threads, 0, s>>>(                      \
+      x, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales, activated, expert_indices, \
+      weights, experts, h, i, kk, routed_scaling_factor, renormalize, group_size)
+    if (experts - 1 <= 256) {
+      if (g.ci == 1) LK_MOE_KS(1, 4); else LK_MOE_KS(2, 4);
+    } else {
+      if (g.ci == 1) LK_MOE_KS(1, 16); else LK_MOE_KS(2, 16);
+    }
+#undef LK_MOE_KS
+    return check_launch("moe gate/up");
+  }
   const int cpr = static_cast<int>(h / 32);
   LK_REQUIRE(stage_bytes(1, cpr) <= kMaxLds, "hidden size %lld too large", (long long)h);
   const int nw = waves_per_block();
