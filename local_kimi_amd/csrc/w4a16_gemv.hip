@@ -560,30 +560,31 @@ __device__ int64_t route_token(const float* __restrict__ logits, const float* __
   float my_score = 0.f;
   int64_t wanted = -1;
   for (int rr = 0; rr < top_k; ++rr) {
+    // this lane's best live candidate (strict > keeps the lowest id on ties)
     uint32_t kb = 0u;
     int jb = -1;
+    float sb = 0.f;
 #pragma unroll
     for (int j = 0; j < EPL; ++j)
       if (live[j] && (jb < 0 || key[j] > kb)) {
         kb = key[j];
         jb = j;
+        sb = s[j];
       }
     const uint32_t kmax = wave_max_u32(jb >= 0 ? kb : 0u);
-    const uint32_t cand =
-        (jb >= 0 && kb == kmax) ? static_cast<uint32_t>(lane * EPL + jb) : 0xFFFFFFFFu;
-    const uint32_t sel = wave_min_u32(cand);
+    // ids grow with the lane, so the lowest lane holding kmax holds the lowest id
+    const uint64_t holders = __builtin_amdgcn_ballot_w64(jb >= 0 && kb == kmax);
+    const int owner = holders ? static_cast<int>(__builtin_ctzll(holders)) : 0;
+    const int slot = __builtin_amdgcn_readlane(jb < 0 ? 0 : jb, owner);
+    const float score = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sb), owner));
+    const uint32_t sel = static_cast<uint32_t>(owner * EPL + slot);
     // top_k <= ne guarantees a live candidate; stay in range regardless
     const uint32_t safe = sel < static_cast<uint32_t>(ne) ? sel : 0u;
-    const int owner = static_cast<int>(safe / EPL);
-    const int slot = static_cast<int>(safe % EPL);
-    float local = 0.f;
+    if (lane == owner) {
 #pragma unroll
-    for (int j = 0; j < EPL; ++j)
-      if (j == slot) {
-        local = s[j];
-        if (lane == owner) live[j] = false;
-      }
-    const float score = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(local), owner));
+      for (int j = 0; j < EPL; ++j)
+        if (j == slot) live[j] = false;
+    }
     ssum += score;
     if (lane == rr) {
       mine = safe;
@@ -818,6 +819,54 @@ w2_combine_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
+// W2 + combine, K-split form for routes <= 16: wave r of the block handles
+// route r for the block's 8*NR rows of H; lane (rg, ph) owns chunks ph + 8*i
+// (i < CI) of the route's activations and rows rg + 8*j. Route sums go through
+// LDS once and are combined by the block in route order (bit-reproducible):
+// bf16 route outputs, fp32 weighted sum of routes 0..R-2, bf16, plus the last
+// route (the shared expert) with weight 1.
+
+template <int NR, int CI>
+__global__ void __launch_bounds__(1024)
+w2_ksplit_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ idx,
+                 int64_t idx_stride, int64_t shared_id, const float* __restrict__ cw,
+                 int64_t cw_stride, const uint8_t* __restrict__ w2p,
+                 const uint16_t* __restrict__ w2s, uint16_t* __restrict__ y, int routes,
+                 int64_t experts, int64_t h, int64_t inter, int64_t group) {
+  __shared__ float red[kMaxKWaves][NR * 8];
+  const int r = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // this wave's route
+  const int64_t t = blockIdx.y;
+  const Shape sh = make_shape(inter, group);
+  KSplit<1, NR, 1, CI> ks;
+  ks.load_x(act + (t * routes + r) * inter, inter, 1, /*wave=*/0, /*kw=*/1, sh.cpr);
+  const int64_t e_raw = (shared_id >= 0 && r == routes - 1) ? shared_id : idx[t * idx_stride + r];
+  const bool valid = e_raw >= 0 && e_raw < experts;
+  const int64_t e = valid ? e_raw : 0;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 8 * NR;
+  const Rows<NR> rows(row0, h);
+  const uint8_t* const wp[1] = {w2p + e * h * sh.bytes_row};
+  const uint16_t* const ws[1] = {w2s + e * h * sh.spr};
+  ks.load_w(wp, ws, rows, sh, 0, 1);
+  ks.compute(rows, 1, 0, 1, sh.cpr);
+  ks.reduce_to_lds(red, r);
+  const int o = threadIdx.x;
+  if (o < NR * 8) {
+    const int64_t row = row0 + (o & 7) + 8 * (o >> 3);
+    if (row < h) {
+      float routed = 0.f;
+      for (int q = 0; q + 1 < routes; ++q) {
+        const int64_t eq = idx[t * idx_stride + q];
+        const float eo = (eq >= 0 && eq < experts) ? round_bf16(red[q][o]) : 0.f;
+        routed += eo * cw[t * cw_stride + q];
+      }
+      const int64_t el = (shared_id >= 0) ? shared_id : idx[t * idx_stride + routes - 1];
+      const float last = (el >= 0 && el < experts) ? round_bf16(red[routes - 1][o]) : 0.f;
+      y[t * h + row] = f32_to_bf16(round_bf16(routed) + last);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host-side dispatch
 
 int waves_per_block() {
@@ -827,6 +876,25 @@ int waves_per_block() {
     return (n == 1 || n == 2 || n == 4) ? n : 1;
   }();
   return w;
+}
+
+// The route-per-wave W2 variant measured slower than the LDS-staged kernel at
+// the decode shape (11.5 / 9.3 us vs 8.8 us at 1 / 2 rows per lane); it stays
+// selectable for experiments with LK_W2_KSPLIT=1.
+bool w2_ksplit_enabled() {
+  static bool on = [] {
+    const char* v = getenv("LK_W2_KSPLIT");
+    return v && atoi(v) == 1;
+  }();
+  return on;
+}
+
+int w2_rows_per_lane() {
+  static int nr = [] {
+    const char* v = getenv("LK_W2_NR");
+    return (v && atoi(v) == 2) ? 2 : 1;
+  }();
+  return nr;
 }
 
 int pick_iters(int cpr) {
@@ -993,6 +1061,24 @@ static int w2_combine_launch(const uint16_t* act, const int64_t* idx, int64_t id
              (long long)routes, (long long)inter);
   LK_REQUIRE(routes <= 8 * kW2Waves, "at most %d routes per token", 8 * kW2Waves);
   LK_REQUIRE(tokens <= 65535, "at most 65535 tokens per call");
+  const int ci = (cpr + 7) / 8;
+  if (w2_ksplit_enabled() && routes <= kMaxKWaves && ci <= 4) {
+    const int nr = w2_rows_per_lane();
+    dim3 g2(static_cast<unsigned>((h + 8 * nr - 1) / (8 * nr)), static_cast<unsigned>(tokens));
+    const int threads = static_cast<int>(routes) * kWave;
+    const int rr = static_cast<int>(routes);
+#define LK_W2_KS(NRV, CIV)                                                                   \
+  w2_ksplit_kernel<NRV, CIV><<<g2, threads, 0, s>>>(act, idx, idx_stride, shared_id, cw,    \
+                                                    cw_stride, w2p, w2s, y, rr, experts, h, \
+                                                    inter, group)
+    if (nr == 1) {
+      if (ci == 1) LK_W2_KS(1, 1); else if (ci == 2) LK_W2_KS(1, 2); else LK_W2_KS(1, 4);
+    } else {
+      if (ci == 1) LK_W2_KS(2, 1); else if (ci == 2) LK_W2_KS(2, 2); else LK_W2_KS(2, 4);
+    }
+#undef LK_W2_KS
+    return check_launch("w2_combine");
+  }
   dim3 grid(static_cast<unsigned>((h + 7) / 8), static_cast<unsigned>(tokens));
   const int iters = pick_iters(cpr);
   const int r = static_cast<int>(routes);
