@@ -51,6 +51,18 @@ GATEUP_EXPERT_BYTES = 2 * w4a16_bytes(INTER, H)                         # 2,433,
 TOKEN_IO_BYTES = H * 2 + E_ROUTED * 4 + H * 2                           # x + logits + y
 
 
+def measured_traffic(kernel: str) -> tuple[int | None, str | None]:
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/traffic.json)."""
+    import json as _json
+
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        data = _json.load(open(path))
+        return int(data["kernels"][kernel]["traffic_bytes"]), "profiles/traffic.json"
+    except (OSError, KeyError, ValueError):
+        return None, None
+
+
 def make_bank(rows: int, cols: int, experts: int, gen: torch.Generator, dev):
     from local_kimi_amd.quant import quantise
 
@@ -193,11 +205,14 @@ def run_moe(args, dev) -> dict:
         "achieved_gbps": round(block_bytes / (us_per_token * 1e3), 1),
         "pct_hbm_peak": round(100.0 * block_bytes / (us_per_token * 1e3) / HBM_PEAK_GBPS, 2),
         "algorithmic_bytes_per_step": block_bytes,
-        "roofline": {"kernel": "moe_gateup_kernel (router + gate/up + SwiGLU)", "bound": "hbm",
+        "roofline": {"kernel": "moe_gateup_ksplit_kernel (router + gate/up + SwiGLU, 9 routes)",
+                     "bound": "hbm",
                      "achieved": round(gateup_bytes / (gateup_us * 1e3), 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s",
                      "frac": round(gateup_bytes / (gateup_us * 1e3) / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "bytes_per_launch": gateup_bytes,
+                     "traffic": measured_traffic("moe_gateup_ksplit_kernel")[0],
+                     "traffic_source": measured_traffic("moe_gateup_ksplit_kernel")[1],
+                     "bytes_per_launch": gateup_bytes,
                      "avg_launch_us": round(gateup_us, 3)},
     }
     if args.cpu_sample > 0:
@@ -240,9 +255,11 @@ def run_dense(args, dev) -> dict:
                    "weight_copies_rotated": copies},
         "achieved_gbps": round(nbytes / (us * 1e3), 1),
         "pct_hbm_peak": round(100.0 * nbytes / (us * 1e3) / HBM_PEAK_GBPS, 2),
-        "roofline": {"kernel": "dense_gemv_kernel", "bound": "hbm",
+        "roofline": {"kernel": "dense_ksplit_kernel", "bound": "hbm",
                      "achieved": round(nbytes / (us * 1e3), 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(nbytes / (us * 1e3) / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(nbytes / (us * 1e3) / HBM_PEAK_GBPS, 4),
+                     "traffic": measured_traffic("dense_ksplit_kernel")[0],
+                     "traffic_source": measured_traffic("dense_ksplit_kernel")[1],
                      "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3)},
     }
     if args.cpu_sample > 0:
@@ -250,12 +267,33 @@ def run_dense(args, dev) -> dict:
     return result
 
 
+def run_copy(args, dev) -> dict:
+    """Plain device copy of a known size: calibrates the HBM byte counters."""
+    nbytes = args.copy_mb << 20
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    reps = 10
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / reps
+    return {"metric": "device copy (counter calibration)", "value": round(us, 2), "unit": "us/copy",
+            "bytes_read": nbytes, "bytes_written": nbytes, "gbps": round(2 * nbytes / (us * 1e3), 1)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2600)
     ap.add_argument("--warmup", type=int, default=260)
-    ap.add_argument("--workload", choices=["moe_decode", "dense_decode"], default="moe_decode")
+    ap.add_argument("--workload", choices=["moe_decode", "dense_decode", "copy"], default="moe_decode")
+    ap.add_argument("--copy-mb", type=int, default=256, help="copy workload size (MiB)")
     ap.add_argument("--layers", type=int, default=26, help="MoE layer banks rotated")
     ap.add_argument("--copies", type=int, default=40, help="dense weight copies rotated")
     ap.add_argument("--cpu-sample", type=int, default=4, help="tokens for the CPU oracle baseline (0: skip)")
@@ -272,7 +310,8 @@ def main() -> int:
     _lib.load()
     dev = torch.device("cuda:0")
     log(f"[bench] device {torch.cuda.get_device_name(0)}, workload {args.workload}")
-    result = run_moe(args, dev) if args.workload == "moe_decode" else run_dense(args, dev)
+    runners = {"moe_decode": run_moe, "dense_decode": run_dense, "copy": run_copy}
+    result = runners[args.workload](args, dev)
     print(json.dumps(result), flush=True)
     return 0
 
