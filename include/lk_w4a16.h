@@ -156,6 +156,81 @@ LK_API int lk_w4a16_moe_decode(const uint16_t* x, const float* logits, const flo
                         int64_t top_k, float routed_scaling_factor, int renormalize,
                         int64_t group_size, void* stream);
 
+/* ---- expert-major schedule: engine/kernels/moe_grouped.py:77-95
+ *      (build_expert_schedule: sorted union of experts, occurrences in
+ *      row-major (token, slot) order), as counting-sort tables
+ * The route table has R = routes (+1 when shared_expert >= 0) entries per
+ * token: entry t*R + r is expert_indices[t*routes + r], and entry t*R + R-1
+ * is shared_expert when shared_expert >= 0. Writes
+ *   offsets int32 [E+2]: bucket b < E starts at offsets[b]; bucket E holds the
+ *                        routes outside [0, E); offsets[E+1] = T*R
+ *   perm int32 [T*R]:    sorted position -> entry, stable (row-major within
+ *                        a bucket)
+ *   tiles int32 [max_tiles,4]: (expert or -1, first position, rows <= 64, 0)
+ *   tile_count int32 [1]
+ * Requires experts <= 512. Sizes from lk_moe_schedule_sizes (R as above). */
+LK_API int lk_moe_schedule_sizes(int64_t tokens, int64_t routes, int64_t experts,
+                                 int64_t* max_tiles, int64_t* workspace_bytes);
+LK_API int lk_moe_schedule(const int64_t* expert_indices, int64_t tokens, int64_t routes,
+                           int64_t experts, int64_t shared_expert, int32_t* offsets,
+                           int32_t* perm, int32_t* tiles, int32_t* tile_count, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+
+/* ---- op w4a16_grouped / w4a16_swiglu for many token-routes (the same
+ *      contracts as lk_w4a16_grouped / lk_w4a16_swiglu above): expert-major
+ *      MFMA GEMM, each expert's weights read once per 64-row tile.
+ *      engine/kernels/moe_grouped.py:103-160 (expert-major evaluation).
+ * workspace: device memory of lk_w4a16_grouped_gemm_workspace() bytes
+ * (returns -1 for invalid dimensions). */
+LK_API int64_t lk_w4a16_grouped_gemm_workspace(int64_t tokens, int64_t routes, int64_t experts);
+LK_API int lk_w4a16_grouped_gemm(const uint16_t* x, const int64_t* expert_indices,
+                                 const uint8_t* packed, const uint16_t* scales, uint16_t* out,
+                                 int64_t tokens, int64_t routes, int64_t experts, int64_t n,
+                                 int64_t k, int64_t group_size, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
+LK_API int lk_w4a16_swiglu_gemm(const uint16_t* x, const int64_t* expert_indices,
+                                const uint8_t* w1_packed, const uint16_t* w1_scales,
+                                const uint8_t* w3_packed, const uint16_t* w3_scales,
+                                uint16_t* out, int64_t tokens, int64_t routes, int64_t experts,
+                                int64_t n, int64_t k, int64_t group_size, void* workspace,
+                                int64_t workspace_bytes, void* stream);
+
+/* ---- op w4a16_dense for many rows (prefill): MFMA GEMM, same contract as
+ *      lk_w4a16_dense. engine/quant/triton_w4a16.py:151-188 (tl.dot GEMM). */
+LK_API int lk_w4a16_dense_gemm(const uint16_t* x, const uint8_t* packed, const uint16_t* scales,
+                               uint16_t* y, int64_t m, int64_t n, int64_t k,
+                               int64_t group_size, void* stream);
+
+/* ---- fused QKV: engine/kernels/w4a16_fused_qkv.py:342-389
+ * (q, k, v) bf16 [M,N] each = x . dequant(Wq|Wk|Wv)^T. M >= 16: one MFMA GEMM
+ * launch over the three matrices; fewer rows: the decode GEMV per matrix. */
+LK_API int lk_w4a16_fused_qkv(const uint16_t* x, const uint8_t* q_packed,
+                              const uint16_t* q_scales, const uint8_t* k_packed,
+                              const uint16_t* k_scales, const uint8_t* v_packed,
+                              const uint16_t* v_scales, uint16_t* q, uint16_t* k_out,
+                              uint16_t* v, int64_t m, int64_t n, int64_t k, int64_t group_size,
+                              void* stream);
+
+/* ---- the grouped W4A16 MoE block with its router, expert-major (batched
+ *      decode and prefill): engine/klinear/moe.py:278-334 +
+ *      engine/klinear/router.py:47-85, evaluated per expert as in
+ *      engine/kernels/moe_grouped.py:103-160.
+ * Router, schedule, gate/up + SwiGLU GEMM over expert tiles, down GEMM
+ * scattered to (token, route) rows, combine. Same outputs as
+ * lk_w4a16_moe_decode. workspace: lk_w4a16_moe_forward_workspace() bytes
+ * (returns -1 for invalid dimensions). Requires experts <= 512, h % 8 == 0. */
+LK_API int64_t lk_w4a16_moe_forward_workspace(int64_t tokens, int64_t experts, int64_t h,
+                                              int64_t i, int64_t top_k);
+LK_API int lk_w4a16_moe_forward(const uint16_t* x, const float* logits, const float* bias,
+                                const uint8_t* w1_packed, const uint16_t* w1_scales,
+                                const uint8_t* w3_packed, const uint16_t* w3_scales,
+                                const uint8_t* w2_packed, const uint16_t* w2_scales, uint16_t* y,
+                                int64_t* expert_indices, float* weights, void* workspace,
+                                int64_t workspace_bytes, int64_t tokens, int64_t experts,
+                                int64_t h, int64_t i, int64_t top_k,
+                                float routed_scaling_factor, int renormalize, int64_t group_size,
+                                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,6 +37,22 @@ SIGNATURES: dict[str, list] = {
                             _I64, _I64, _I64, _I64, _I64, _F, _I, _I64, _P],
     "lk_w4a16_moe_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                             _I64, _I64, _I64, _I64, _I64, _F, _I, _I64, _P],
+    "lk_moe_schedule_sizes": [_I64, _I64, _I64, _P, _P],
+    "lk_moe_schedule": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P],
+    "lk_w4a16_grouped_gemm": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                              _P, _I64, _P],
+    "lk_w4a16_swiglu_gemm": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                             _P, _I64, _P],
+    "lk_w4a16_dense_gemm": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "lk_w4a16_fused_qkv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "lk_w4a16_moe_forward": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
+                             _I64, _I64, _I64, _I64, _I64, _F, _I, _I64, _P],
+}
+
+# name -> argument types of the size queries (they return int64, -1 on bad input)
+QUERIES: dict[str, list] = {
+    "lk_w4a16_grouped_gemm_workspace": [_I64, _I64, _I64],
+    "lk_w4a16_moe_forward_workspace": [_I64, _I64, _I64, _I64, _I64],
 }
 
 _lock = threading.Lock()
@@ -72,6 +88,10 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = ctypes.c_int
                 fn.argtypes = argtypes
+            for name, argtypes in QUERIES.items():
+                fn = getattr(lib, name)
+                fn.restype = ctypes.c_int64
+                fn.argtypes = argtypes
             _lib = lib
     return _lib
 
@@ -84,6 +104,22 @@ def call(name: str, *args) -> None:
         raise RuntimeError(f"{name} failed (status {status}): {message}")
 
 
+def query(name: str, *args) -> int:
+    """Call a size query; raise ValueError when it rejects the dimensions."""
+    value = int(getattr(load(), name)(*args))
+    if value < 0:
+        raise ValueError(f"{name}: invalid dimensions {args}")
+    return value
+
+
+def schedule_sizes(tokens: int, routes: int, experts: int) -> tuple[int, int]:
+    """``(max_tiles, workspace_bytes)`` of :c:func:`lk_moe_schedule`."""
+    max_tiles, ws = ctypes.c_int64(), ctypes.c_int64()
+    call("lk_moe_schedule_sizes", tokens, routes, experts, ctypes.addressof(max_tiles),
+         ctypes.addressof(ws))
+    return max_tiles.value, ws.value
+
+
 def exported_symbols() -> list[str]:
     """Entry points this binding expects the library to export."""
-    return ["lk_last_error", "lk_abi_version", *SIGNATURES]
+    return ["lk_last_error", "lk_abi_version", *SIGNATURES, *QUERIES]

@@ -20,6 +20,8 @@ int fail_arg(const char* fmt, ...);
 int check_launch(const char* what);
 // LK_OK when k > 0 and group is a positive multiple of 32 that divides k.
 int check_group(int64_t k, int64_t group);
+// check_group, and group is a power of two.
+int check_pow2_group(int64_t k, int64_t group);
 
 #define LK_REQUIRE(cond, ...)          \
   do {                                 \

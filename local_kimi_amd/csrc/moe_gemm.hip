@@ -1,0 +1,953 @@
+// Expert-major W4A16 kernels on the matrix cores (bf16 MFMA 16x16x32):
+//
+//  * the route schedule: a stable counting sort of the [T, R] route table by
+//    expert -- counts, offsets, the permutation (sorted position -> entry
+//    t * R + r, row-major within an expert) and a list of 64-row tiles. It is
+//    the table form of engine/kernels/moe_grouped.py:77-95 (sorted union of
+//    experts, occurrences in row-major order); routes outside [0, E) collect
+//    in a last bucket whose tiles write zeros;
+//  * one GEMM kernel family for every multi-token W4A16 product: grouped
+//    gate/up + SwiGLU over expert tiles (rows gathered through the
+//    permutation), the grouped down projection scattered back to (token,
+//    route) rows, and the dense / fused-QKV GEMM;
+//  * the route combine and the expert-major MoE block built from them.
+//
+// MFMA operand mapping (v_mfma_f32_16x16x32_bf16, wave64): lane l holds
+// A[m = l%16][8(l/16) + i] and B[8(l/16) + i][n = l%16] for i = 0..7 and
+// receives D[4(l/16) + i][l%16]. One packed weight dword (8 codes) unpacks
+// into exactly one B operand in the (k_p, k_{p+4}) pair order of
+// lk_common.hpp, and the activation fragments are staged in LDS in that
+// order. Decoded weights are q + 136 (exact in bf16); every group's partial
+// product comes from a fresh accumulator and is corrected and scaled once:
+//   y += s_g * (sum_{k in g} x * (q + 136) - 136 * sum_{k in g} x).
+// The positions of one MFMA must share a group: with G >= 128 a lane's 16
+// contiguous packed bytes (32 codes) feed the 4 MFMAs of one 128-wide k-step;
+// with G = 32 or 64 each MFMA covers 32 consecutive codes and a lane loads
+// one dword per MFMA.
+
+#include "lk_common.hpp"
+
+namespace lk {
+namespace {
+
+constexpr int kWave = 64;
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// route schedule
+
+constexpr int kSchedThreads = 512;
+constexpr int kSchedWaves = kSchedThreads / kWave;
+constexpr int kTileRows = 64;
+constexpr int kMaxBuckets = 513;  // experts + 1 (the last bucket collects invalid routes)
+
+struct RouteTable {
+  const int64_t* idx;  // [T, kcols]
+  int64_t kcols;
+  int64_t routes;   // entries per token (R)
+  int64_t experts;  // bank entries (E)
+  int64_t shared;   // when >= 0: expert of route R - 1 (not read from idx)
+
+  __device__ inline int bucket(int64_t entry) const {
+    const int64_t t = entry / routes;
+    const int64_t r = entry - t * routes;
+    const int64_t e = (shared >= 0 && r == routes - 1) ? shared : idx[t * kcols + r];
+    return (e >= 0 && e < experts) ? static_cast<int>(e) : static_cast<int>(experts);
+  }
+};
+
+struct Schedule {
+  int32_t* rank;        // [n] rank of an entry within its bucket and chunk
+  int32_t* hist;        // [chunks, E + 1] entries per bucket per chunk
+  int32_t* offsets;     // [E + 2] bucket starts; offsets[E + 1] = n
+  int32_t* perm;        // [n] sorted position -> entry
+  int32_t* tiles;       // [max_tiles, 4] (expert or -1, first row, rows, 0)
+  int32_t* tile_count;  // [1]
+};
+
+__device__ inline int wave_inclusive_scan(int v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(v, d, kWave);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// In-place exclusive prefix sum of vals[0, count) by one whole wave; every
+// lane of the wave gets the total.
+__device__ inline int wave_exclusive_scan(int* vals, int count) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int per = (count + kWave - 1) / kWave;
+  const int b = min(count, lane * per);
+  const int e = min(count, b + per);
+  int s = 0;
+  for (int i = b; i < e; ++i) s += vals[i];
+  const int incl = wave_inclusive_scan(s);
+  int run = incl - s;
+  for (int i = b; i < e; ++i) {
+    const int v = vals[i];
+    vals[i] = run;
+    run += v;
+  }
+  return __shfl(incl, kWave - 1, kWave);
+}
+
+// Places the entries of one chunk: tot[b] = entries of bucket b overall,
+// before[b] = entries of bucket b in earlier chunks. Block 0 also writes the
+// bucket offsets and the tile list (it reuses `before`, all zero there).
+__device__ void place_chunk(int64_t n, int nb, int* tot, int* before, int* start, bool valid,
+                            int64_t entry, int b, int rank, const Schedule& sc) {
+  for (int i = threadIdx.x; i < nb; i += blockDim.x) start[i] = tot[i];
+  __syncthreads();
+  if (threadIdx.x < kWave) wave_exclusive_scan(start, nb);
+  __syncthreads();
+  if (valid) sc.perm[start[b] + before[b] + rank] = static_cast<int32_t>(entry);
+  if (blockIdx.x != 0) return;
+  for (int i = threadIdx.x; i < nb; i += blockDim.x) sc.offsets[i] = start[i];
+  if (threadIdx.x == 0) sc.offsets[nb] = static_cast<int32_t>(n);
+  __syncthreads();
+  for (int i = threadIdx.x; i < nb; i += blockDim.x)
+    before[i] = (tot[i] + kTileRows - 1) / kTileRows;
+  __syncthreads();
+  int total_tiles = 0;
+  if (threadIdx.x < kWave) total_tiles = wave_exclusive_scan(before, nb);
+  __syncthreads();
+  for (int bb = threadIdx.x; bb < nb; bb += blockDim.x) {
+    const int cnt = tot[bb];
+    const int expert = bb < nb - 1 ? bb : -1;
+    int4* out = reinterpret_cast<int4*>(sc.tiles) + before[bb];
+    for (int row = 0; row < cnt; row += kTileRows, ++out)
+      *out = make_int4(expert, start[bb] + row, min(kTileRows, cnt - row), 0);
+  }
+  if (threadIdx.x == 0) *sc.tile_count = total_tiles;
+}
+
+// One chunk of kSchedThreads entries per block: per-wave bitmaps of the
+// lanes holding each bucket give every entry its rank among the equal
+// entries before it in the chunk (stable, row-major). With a single chunk
+// the placement follows in the same launch.
+__global__ void __launch_bounds__(kSchedThreads)
+schedule_count_kernel(const RouteTable rt, int64_t n, Schedule sc) {
+  __shared__ uint32_t bits[kSchedWaves * kMaxBuckets * 2];
+  __shared__ int pre[kSchedWaves * kMaxBuckets];
+  __shared__ int tot[kMaxBuckets], before[kMaxBuckets], start[kMaxBuckets];
+  const int nb = static_cast<int>(rt.experts) + 1;
+  for (int i = threadIdx.x; i < kSchedWaves * nb * 2; i += kSchedThreads) bits[i] = 0u;
+  __syncthreads();
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x / kWave;
+  const int64_t entry = static_cast<int64_t>(blockIdx.x) * kSchedThreads + threadIdx.x;
+  const bool valid = entry < n;
+  const int b = valid ? rt.bucket(entry) : 0;
+  if (valid) atomicOr(&bits[(w * nb + b) * 2 + (lane >> 5)], 1u << (lane & 31));
+  __syncthreads();
+  for (int bb = threadIdx.x; bb < nb; bb += kSchedThreads) {
+    int run = 0;
+    for (int ww = 0; ww < kSchedWaves; ++ww) {
+      pre[ww * nb + bb] = run;
+      run += __popc(bits[(ww * nb + bb) * 2]) + __popc(bits[(ww * nb + bb) * 2 + 1]);
+    }
+    tot[bb] = run;
+    before[bb] = 0;
+    if (gridDim.x > 1) sc.hist[static_cast<int64_t>(blockIdx.x) * nb + bb] = run;
+  }
+  __syncthreads();
+  int rank = 0;
+  if (valid) {
+    const uint32_t lo = bits[(w * nb + b) * 2];
+    const uint32_t hi = bits[(w * nb + b) * 2 + 1];
+    const int below = lane < 32 ? __popc(lo & ((1u << lane) - 1u))
+                                : __popc(lo) + __popc(hi & ((1u << (lane - 32)) - 1u));
+    rank = pre[w * nb + b] + below;
+  }
+  if (gridDim.x == 1) {
+    place_chunk(n, nb, tot, before, start, valid, entry, b, rank, sc);
+  } else if (valid) {
+    sc.rank[entry] = rank;
+  }
+}
+
+__global__ void __launch_bounds__(kSchedThreads)
+schedule_place_kernel(const RouteTable rt, int64_t n, int chunks, Schedule sc) {
+  __shared__ int tot[kMaxBuckets], before[kMaxBuckets], start[kMaxBuckets];
+  const int nb = static_cast<int>(rt.experts) + 1;
+  const int c = blockIdx.x;
+  for (int bb = threadIdx.x; bb < nb; bb += kSchedThreads) {
+    int pre = 0, all = 0;
+    for (int cc = 0; cc < chunks; ++cc) {
+      const int h = sc.hist[static_cast<int64_t>(cc) * nb + bb];
+      pre += cc < c ? h : 0;
+      all += h;
+    }
+    tot[bb] = all;
+    before[bb] = pre;
+  }
+  __syncthreads();
+  const int64_t entry = static_cast<int64_t>(c) * kSchedThreads + threadIdx.x;
+  const bool valid = entry < n;
+  const int b = valid ? rt.bucket(entry) : 0;
+  const int rank = valid ? sc.rank[entry] : 0;
+  place_chunk(n, nb, tot, before, start, valid, entry, b, rank, sc);
+}
+
+// ---------------------------------------------------------------------------
+// W4A16 GEMM on the matrix cores
+
+struct GemmArgs {
+  const uint16_t* a;         // activations bf16, rows of k
+  const int32_t* perm;       // sorted position -> entry (gather / scatter modes)
+  const int32_t* tiles;      // [*, 4] tile list (schedule modes)
+  const int32_t* tile_count;
+  const uint8_t* wp[3];      // packed weights per output matrix (SwiGLU: W1, W3)
+  const uint16_t* ws[3];
+  uint16_t* out[3];
+  int64_t n, k, group;
+  int64_t wstride;           // packed bytes per expert
+  int64_t sstride;           // scales per expert
+  int64_t routes;            // entries per token (gather: token = entry / routes)
+  int dense_rows;            // rows of a dense product
+  int col_blocks;            // column blocks per output matrix
+  int outputs;               // output matrices (3 for fused QKV, else 1)
+};
+
+template <typename T>
+__device__ inline T pick3(const T (&v)[3], int i) {
+  return i == 0 ? v[0] : (i == 1 ? v[1] : v[2]);
+}
+
+constexpr int kSub = 4;  // 16-row MFMA subtiles per 64-row tile
+
+__device__ inline bf16x8_t unpack_q8(uint32_t w) {
+  const uint32_t u = w ^ kNibbleFlip;
+  const u32x4_t v = {(u & kPairMask) | kBf16_128, ((u >> 4) & kPairMask) | kBf16_128,
+                     ((u >> 8) & kPairMask) | kBf16_128, ((u >> 12) & kPairMask) | kBf16_128};
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// One 128-wide k-step of a lane's weights: 4 packed dwords (one per MFMA) and
+// the scale bits of the group each MFMA belongs to, per matrix and column tile.
+template <int MATS, int NT, bool WIDE>
+struct WeightStep {
+  uint32_t w[MATS][NT][4];
+  uint16_t s[MATS][NT][4];
+
+  __device__ inline void load(const uint8_t* const (&wrow)[MATS][NT],
+                              const uint16_t* const (&srow)[MATS][NT], int step, int jq,
+                              int64_t k, int64_t group) {
+#pragma unroll
+    for (int mi = 0; mi < MATS; ++mi) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        if constexpr (WIDE) {
+          // G >= 128: k is a multiple of 128, the whole step lies in one group
+          const uint4 v =
+              *reinterpret_cast<const uint4*>(wrow[mi][nt] + static_cast<int64_t>(step) * 64 + jq * 16);
+          w[mi][nt][0] = v.x;
+          w[mi][nt][1] = v.y;
+          w[mi][nt][2] = v.z;
+          w[mi][nt][3] = v.w;
+          s[mi][nt][0] = srow[mi][nt][static_cast<int64_t>(step) * 128 / group];
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int64_t k0 = static_cast<int64_t>(step) * 128 + 32 * t;
+            const int64_t kk = k0 < k ? k0 : 0;  // sub-steps past k are skipped
+            w[mi][nt][t] = *reinterpret_cast<const uint32_t*>(wrow[mi][nt] + kk / 2 + jq * 4);
+            s[mi][nt][t] = srow[mi][nt][kk / group];
+          }
+        }
+      }
+    }
+  }
+};
+
+// Block = WAVES waves over one 64-row tile x (WAVES * NT * 16) columns; each
+// wave owns NT 16-column MFMA tiles of every matrix and all active 16-row
+// subtiles. Activations go through LDS (double buffered, one barrier per
+// 128-wide k-step); weights go straight from HBM into registers one k-step
+// ahead.
+template <int MATS, int NT, int WAVES, bool WIDE, bool GATHER, bool SCATTER, bool DENSE>
+__global__ void __launch_bounds__(WAVES * kWave)
+w4a16_gemm_kernel(const GemmArgs g) {
+  constexpr int kThreads = WAVES * kWave;
+  constexpr int kUPT = kTileRows * 16 / kThreads;  // 16-byte activation units per thread
+  constexpr int kBN = WAVES * NT * 16;
+  __shared__ uint4 a_lds[2][kSub * 4 * kWave];
+  __shared__ __attribute__((aligned(16))) float off_lds[2][4 * kTileRows];
+
+  // blocks of one tile sit on one XCD (block ids are dealt round robin to the 8 XCDs)
+  const int per_tile = g.col_blocks * g.outputs;
+  const int id = blockIdx.x;
+  const int grp = id / (8 * per_tile);
+  const int rem = id - grp * 8 * per_tile;
+  const int tile = grp * 8 + (rem & 7);
+  const int cb_all = rem >> 3;
+  const int osel = cb_all / g.col_blocks;
+  const int cb = cb_all - osel * g.col_blocks;
+  int expert, row0, rows;
+  if constexpr (DENSE) {
+    row0 = tile * kTileRows;
+    if (row0 >= g.dense_rows) return;
+    rows = min(kTileRows, g.dense_rows - row0);
+    expert = 0;
+  } else {
+    if (tile >= *g.tile_count) return;
+    const int4 d = reinterpret_cast<const int4*>(g.tiles)[tile];
+    expert = d.x;
+    row0 = d.y;
+    rows = d.z;
+  }
+  const int64_t N = g.n, K = g.k;
+  uint16_t* const out = pick3(g.out, osel);
+  const int tid = threadIdx.x;
+  if (expert < 0) {  // routes outside the bank produce zero rows
+    for (int i = tid; i < rows * kBN; i += kThreads) {
+      const int m = i / kBN;
+      const int64_t col = static_cast<int64_t>(cb) * kBN + (i - m * kBN);
+      if (col < N) {
+        const int64_t orow = SCATTER ? g.perm[row0 + m] : row0 + m;
+        out[orow * N + col] = 0;
+      }
+    }
+    return;
+  }
+
+  const int lane = tid & (kWave - 1);
+  const int wv = tid / kWave;
+  const int jq = lane >> 4;
+  const int ln = lane & 15;
+  const int64_t rowb = K / 2;
+  const int64_t spr = K / g.group;
+  const int ksteps = static_cast<int>((K + 127) / 128);
+  const int mt_act = (rows + 15) >> 4;
+
+  const uint8_t* wrow[MATS][NT];
+  const uint16_t* srow[MATS][NT];
+  int64_t col[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    col[nt] = static_cast<int64_t>(cb) * kBN + (wv * NT + nt) * 16 + ln;
+    const int64_t cc = col[nt] < N ? col[nt] : N - 1;
+#pragma unroll
+    for (int mi = 0; mi < MATS; ++mi) {
+      wrow[mi][nt] = pick3(g.wp, osel + mi) + expert * g.wstride + cc * rowb;
+      srow[mi][nt] = pick3(g.ws, osel + mi) + expert * g.sstride + cc * spr;
+    }
+  }
+
+  // activation rows this thread stages (unit u: row u / 16, 8-code unit u % 16)
+  const uint16_t* arow[kUPT];
+  uint32_t amask[kUPT];
+#pragma unroll
+  for (int i = 0; i < kUPT; ++i) {
+    const int m = (tid + i * kThreads) >> 4;
+    const bool ok = m < rows;
+    amask[i] = ok ? 0xFFFFFFFFu : 0u;
+    const int mm = ok ? m : 0;
+    int64_t r;
+    if constexpr (GATHER) r = g.perm[row0 + mm] / g.routes;
+    else r = row0 + mm;
+    arow[i] = g.a + r * K;
+  }
+  uint4 av[kUPT];
+  auto load_a = [&](int step) {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      const int c = (tid + i * kThreads) & 15;
+      const int64_t k0 = static_cast<int64_t>(step) * 128 + c * 8;
+      const uint32_t msk = k0 < K ? amask[i] : 0u;
+      const uint4 v = *reinterpret_cast<const uint4*>(arow[i] + (k0 < K ? k0 : 0));
+      av[i] = make_uint4(v.x & msk, v.y & msk, v.z & msk, v.w & msk);
+    }
+  };
+  // LDS fragment (subtile ms, MFMA t) is 64 x 16 bytes read by lane l at
+  // position (l/16) * 16 + ((l%16) ^ (4t + l/16)); the xor spreads one row's
+  // 16 writes over distinct banks.
+  auto commit_a = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kUPT; ++i) {
+      const int u = tid + i * kThreads;
+      const int m = u >> 4, c = u & 15;
+      const int t = WIDE ? (c & 3) : (c >> 2);
+      const int j = WIDE ? (c >> 2) : (c & 3);
+      uint32_t p[4];
+      pair_x8(av[i], p);
+      a_lds[buf][((m >> 4) * 4 + t) * kWave + j * 16 + ((m & 15) ^ (4 * t + j))] =
+          make_uint4(p[0], p[1], p[2], p[3]);
+      float sx = sum_x8(av[i]);
+      if constexpr (WIDE) {
+        sx = sum8(sx);
+        sx += dpp_f32<kRowMirror>(sx);  // the 16 units of a row sit in one 16-lane row
+        if (c == 0) off_lds[buf][m] = kCodeOffset * sx;
+      } else {
+        sx = sum4(sx);  // the 4 units of a 32-code sub-step sit in one lane quad
+        if (j == 0) off_lds[buf][t * kTileRows + m] = kCodeOffset * sx;
+      }
+    }
+  };
+
+  f32x4_t tot[MATS][NT][kSub], acc[MATS][NT][kSub];
+  const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int ms = 0; ms < kSub; ++ms) {
+        tot[mi][nt][ms] = zero4;
+        acc[mi][nt][ms] = zero4;
+      }
+  f32x4_t offacc[kSub];
+#pragma unroll
+  for (int ms = 0; ms < kSub; ++ms) offacc[ms] = zero4;
+
+  auto correct = [&](const f32x4_t (&o)[kSub], const WeightStep<MATS, NT, WIDE>& ws, int t) {
+#pragma unroll
+    for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const float sc = bf16_to_f32(ws.s[mi][nt][t]);
+#pragma unroll
+        for (int ms = 0; ms < kSub; ++ms)
+          if (ms < mt_act) {
+            tot[mi][nt][ms] += sc * (acc[mi][nt][ms] - o[ms]);
+            acc[mi][nt][ms] = zero4;
+          }
+      }
+  };
+
+  WeightStep<MATS, NT, WIDE> wcur, wnext;
+  wcur.load(wrow, srow, 0, jq, K, g.group);
+  load_a(0);
+  commit_a(0);
+  __syncthreads();
+  const int cg = static_cast<int>(g.group / 32);  // MFMAs per group (narrow groups)
+  for (int step = 0; step < ksteps; ++step) {
+    const int buf = step & 1;
+    const bool more = step + 1 < ksteps;
+    if (more) {
+      wnext.load(wrow, srow, step + 1, jq, K, g.group);
+      load_a(step + 1);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (!WIDE && static_cast<int64_t>(step) * 128 + 32 * t >= K) break;
+      bf16x8_t af[kSub];
+#pragma unroll
+      for (int ms = 0; ms < kSub; ++ms)
+        if (ms < mt_act)
+          af[ms] = __builtin_bit_cast(
+              bf16x8_t, a_lds[buf][(ms * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
+#pragma unroll
+      for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const bf16x8_t bv = unpack_q8(wcur.w[mi][nt][t]);
+#pragma unroll
+          for (int ms = 0; ms < kSub; ++ms)
+            if (ms < mt_act)
+              acc[mi][nt][ms] =
+                  __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ms], bv, acc[mi][nt][ms], 0, 0, 0);
+        }
+      if constexpr (!WIDE) {
+        if ((t + 1) % cg == 0) {
+          f32x4_t o[kSub];
+#pragma unroll
+          for (int ms = 0; ms < kSub; ++ms) {
+            o[ms] = zero4;
+            if (ms < mt_act)
+              for (int tt = t + 1 - cg; tt <= t; ++tt)
+                o[ms] += *reinterpret_cast<const f32x4_t*>(
+                    &off_lds[buf][tt * kTileRows + ms * 16 + jq * 4]);
+          }
+          correct(o, wcur, t);
+        }
+      }
+    }
+    if constexpr (WIDE) {
+#pragma unroll
+      for (int ms = 0; ms < kSub; ++ms)
+        if (ms < mt_act)
+          offacc[ms] += *reinterpret_cast<const f32x4_t*>(&off_lds[buf][ms * 16 + jq * 4]);
+      if ((static_cast<int64_t>(step + 1) * 128) % g.group == 0) {
+        correct(offacc, wcur, 0);
+#pragma unroll
+        for (int ms = 0; ms < kSub; ++ms) offacc[ms] = zero4;
+      }
+    }
+    if (more) {
+      commit_a(buf ^ 1);
+      wcur = wnext;
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int ms = 0; ms < kSub; ++ms) {
+    if (ms >= mt_act) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = ms * 16 + jq * 4 + i;
+      if (m >= rows) continue;
+      const int64_t orow = SCATTER ? static_cast<int64_t>(g.perm[row0 + m]) : row0 + m;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        if (col[nt] >= N) continue;
+        uint16_t v;
+        if constexpr (MATS == 2) v = swiglu_bf16(tot[0][nt][ms][i], tot[1][nt][ms][i]);
+        else v = f32_to_bf16(tot[0][nt][ms][i]);
+        out[orow * N + col[nt]] = v;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// route combine over entry-ordered expert outputs eo [T * (top_k + 1), H]:
+// y[t] = bf16(bf16(sum_{r < top_k} w[t, r] * eo[t, r]) + eo[t, top_k]),
+// 8 columns per thread.
+__global__ void __launch_bounds__(256)
+moe_combine_kernel(const uint16_t* __restrict__ eo, const float* __restrict__ w,
+                   uint16_t* __restrict__ y, int64_t tokens, int top_k, int64_t h) {
+  const int64_t per = h / 8;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gid >= tokens * per) return;
+  const int64_t t = gid / per;
+  const int64_t c8 = (gid - t * per) * 8;
+  const int64_t routes = top_k + 1;
+  const uint16_t* base = eo + t * routes * h + c8;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < top_k; ++r) {
+    const uint4 v = *reinterpret_cast<const uint4*>(base + r * h);
+    const float wr = w[t * top_k + r];
+    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[2 * j] += bf16_to_f32(q[j] & 0xFFFFu) * wr;
+      acc[2 * j + 1] += bf16_to_f32(q[j] >> 16) * wr;
+    }
+  }
+  const uint4 sv = *reinterpret_cast<const uint4*>(base + top_k * h);
+  const uint32_t sq[4] = {sv.x, sv.y, sv.z, sv.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t lo = f32_to_bf16(round_bf16(acc[2 * j]) + bf16_to_f32(sq[j] & 0xFFFFu));
+    const uint32_t hi = f32_to_bf16(round_bf16(acc[2 * j + 1]) + bf16_to_f32(sq[j] >> 16));
+    o[j] = lo | (hi << 16);
+  }
+  *reinterpret_cast<uint4*>(y + t * h + c8) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// offsets[0, n) = 0 and *count = 0 (an empty route table)
+__global__ void fill_i32_kernel(int32_t* offsets, int64_t n, int32_t* count) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) offsets[i] = 0;
+  if (i == 0) *count = 0;
+}
+
+// ---------------------------------------------------------------------------
+// host side
+
+inline size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+struct SchedLayout {
+  size_t rank, hist, total;
+  int chunks;
+  int64_t max_tiles;
+};
+
+int64_t max_tiles_for(int64_t entries, int64_t experts) {
+  return (experts + 1 < entries ? experts + 1 : entries) + entries / kTileRows + 1;
+}
+
+SchedLayout sched_layout(int64_t entries, int64_t experts) {
+  SchedLayout l;
+  l.chunks = static_cast<int>((entries + kSchedThreads - 1) / kSchedThreads);
+  l.max_tiles = max_tiles_for(entries, experts);
+  l.rank = 0;
+  l.hist = align_up(static_cast<size_t>(entries) * 4);
+  l.total = l.hist + align_up(static_cast<size_t>(l.chunks) * (experts + 1) * 4);
+  return l;
+}
+
+// Private buffers of one expert-major call, carved from the caller's workspace.
+struct MoeLayout {
+  SchedLayout sched;
+  size_t offsets, perm, tiles, count, act, eo, total;
+};
+
+MoeLayout moe_layout(int64_t entries, int64_t experts, int64_t act_cols, int64_t out_cols) {
+  MoeLayout l;
+  l.sched = sched_layout(entries, experts);
+  size_t at = l.sched.total;
+  l.offsets = at;
+  at += align_up(static_cast<size_t>(experts + 2) * 4);
+  l.perm = at;
+  at += align_up(static_cast<size_t>(entries) * 4);
+  l.tiles = at;
+  at += align_up(static_cast<size_t>(l.sched.max_tiles) * 16);
+  l.count = at;
+  at += 256;
+  l.act = at;
+  at += align_up(static_cast<size_t>(entries) * act_cols * 2);
+  l.eo = at;
+  at += align_up(static_cast<size_t>(entries) * out_cols * 2);
+  l.total = at;
+  return l;
+}
+
+int schedule_launch(const RouteTable& rt, int64_t entries, char* ws, const SchedLayout& sl,
+                    int32_t* offsets, int32_t* perm, int32_t* tiles, int32_t* tile_count,
+                    hipStream_t s) {
+  Schedule sc;
+  sc.rank = reinterpret_cast<int32_t*>(ws + sl.rank);
+  sc.hist = reinterpret_cast<int32_t*>(ws + sl.hist);
+  sc.offsets = offsets;
+  sc.perm = perm;
+  sc.tiles = tiles;
+  sc.tile_count = tile_count;
+  schedule_count_kernel<<<sl.chunks, kSchedThreads, 0, s>>>(rt, entries, sc);
+  if (sl.chunks > 1)
+    schedule_place_kernel<<<sl.chunks, kSchedThreads, 0, s>>>(rt, entries, sl.chunks, sc);
+  return check_launch("moe schedule");
+}
+
+enum class Mode { Gather, Scatter, GatherScatter, Dense };
+
+template <int MATS, int NT, bool WIDE>
+void gemm_dispatch_mode(const GemmArgs& g, Mode mode, unsigned blocks, hipStream_t s) {
+  constexpr int W = 4;
+  switch (mode) {
+    case Mode::Gather:
+      w4a16_gemm_kernel<MATS, NT, W, WIDE, true, false, false><<<blocks, W * kWave, 0, s>>>(g);
+      break;
+    case Mode::Scatter:
+      w4a16_gemm_kernel<MATS, NT, W, WIDE, false, true, false><<<blocks, W * kWave, 0, s>>>(g);
+      break;
+    case Mode::GatherScatter:
+      w4a16_gemm_kernel<MATS, NT, W, WIDE, true, true, false><<<blocks, W * kWave, 0, s>>>(g);
+      break;
+    case Mode::Dense:
+      w4a16_gemm_kernel<MATS, NT, W, WIDE, false, false, true><<<blocks, W * kWave, 0, s>>>(g);
+      break;
+  }
+}
+
+// Launches the GEMM over `tiles` row tiles (an upper bound in schedule
+// modes); `wide_cols` picks two 16-column tiles per wave.
+template <int MATS>
+int gemm_launch(GemmArgs g, Mode mode, int64_t tiles, bool wide_cols, hipStream_t s,
+                const char* what) {
+  LK_REQUIRE(g.k % 32 == 0 && g.group % 32 == 0 && (g.group & (g.group - 1)) == 0,
+             "%s: unsupported reduction width / group size", what);
+  const bool wide = g.group >= 128;
+  const int nt = wide_cols ? 2 : 1;
+  const int bn = 4 * nt * 16;
+  g.col_blocks = static_cast<int>((g.n + bn - 1) / bn);
+  const int64_t groups8 = (tiles + 7) / 8;
+  const int64_t blocks = groups8 * 8 * g.col_blocks * g.outputs;
+  LK_REQUIRE(blocks > 0 && blocks < (1LL << 31), "%s: too many blocks", what);
+  const unsigned nb = static_cast<unsigned>(blocks);
+  if (wide) {
+    if (wide_cols) gemm_dispatch_mode<MATS, 2, true>(g, mode, nb, s);
+    else gemm_dispatch_mode<MATS, 1, true>(g, mode, nb, s);
+  } else {
+    if (wide_cols) gemm_dispatch_mode<MATS, 2, false>(g, mode, nb, s);
+    else gemm_dispatch_mode<MATS, 1, false>(g, mode, nb, s);
+  }
+  return check_launch(what);
+}
+
+// Wider column blocks once there are enough tiles to fill the machine.
+bool wide_cols_for(int64_t tiles, int64_t n) { return tiles * ((n + 63) / 64) >= 2048; }
+
+int check_schedule_dims(int64_t tokens, int64_t routes, int64_t experts) {
+  LK_REQUIRE(experts > 0 && experts + 1 <= kMaxBuckets, "expert-major schedule supports 1..%d experts",
+             kMaxBuckets - 1);
+  LK_REQUIRE(tokens >= 0 && routes > 0, "invalid route table dimensions");
+  LK_REQUIRE(tokens * routes < (1LL << 30), "too many token-routes for one call");
+  return LK_OK;
+}
+
+}  // namespace
+}  // namespace lk
+
+using namespace lk;
+
+extern "C" {
+
+int lk_moe_schedule_sizes(int64_t tokens, int64_t routes, int64_t experts, int64_t* max_tiles,
+                          int64_t* workspace_bytes) {
+  if (int rc = check_schedule_dims(tokens, routes, experts)) return rc;
+  LK_REQUIRE(max_tiles && workspace_bytes, "null pointer argument");
+  const SchedLayout l = sched_layout(tokens * routes, experts);
+  *max_tiles = l.max_tiles;
+  *workspace_bytes = static_cast<int64_t>(l.total);
+  return LK_OK;
+}
+
+int lk_moe_schedule(const int64_t* expert_indices, int64_t tokens, int64_t routes,
+                    int64_t experts, int64_t shared_expert, int32_t* offsets, int32_t* perm,
+                    int32_t* tiles, int32_t* tile_count, void* workspace,
+                    int64_t workspace_bytes, void* stream) {
+  const int64_t r_total = routes + (shared_expert >= 0 ? 1 : 0);
+  if (int rc = check_schedule_dims(tokens, r_total, experts)) return rc;
+  LK_REQUIRE(shared_expert < experts, "shared expert id %lld outside the bank",
+             (long long)shared_expert);
+  LK_REQUIRE(offsets && perm && tiles && tile_count && workspace, "null pointer argument");
+  LK_REQUIRE(routes > 0 || shared_expert >= 0, "empty route table");
+  const int64_t entries = tokens * r_total;
+  const SchedLayout l = sched_layout(entries, experts);
+  LK_REQUIRE(workspace_bytes >= static_cast<int64_t>(l.total),
+             "schedule workspace too small: %lld < %lld bytes", (long long)workspace_bytes,
+             (long long)l.total);
+  if (entries == 0) {  // a fill kernel (no memset node when the call is captured)
+    hipStream_t s = as_stream(stream);
+    fill_i32_kernel<<<static_cast<unsigned>((experts + 2 + 255) / 256), 256, 0, s>>>(
+        offsets, experts + 2, tile_count);
+    return check_launch("lk_moe_schedule");
+  }
+  LK_REQUIRE(expert_indices != nullptr || routes == 0, "null pointer argument");
+  const RouteTable rt{expert_indices, routes, r_total, experts, shared_expert};
+  return schedule_launch(rt, entries, static_cast<char*>(workspace), l, offsets, perm, tiles,
+                         tile_count, as_stream(stream));
+}
+
+int64_t lk_w4a16_grouped_gemm_workspace(int64_t tokens, int64_t routes, int64_t experts) {
+  if (check_schedule_dims(tokens, routes, experts)) return -1;
+  return static_cast<int64_t>(moe_layout(tokens * routes, experts, 0, 0).total);
+}
+
+static int grouped_gemm_common(const uint16_t* x, const int64_t* idx, const uint8_t* p0,
+                               const uint16_t* s0, const uint8_t* p1, const uint16_t* s1,
+                               uint16_t* out, int64_t tokens, int64_t routes, int64_t experts,
+                               int64_t n, int64_t k, int64_t group, void* workspace,
+                               int64_t workspace_bytes, void* stream, bool swiglu,
+                               const char* name) {
+  LK_REQUIRE(p0 && s0 && out && (!swiglu || (p1 && s1)), "null pointer argument");
+  LK_REQUIRE(routes > 0 && experts > 0 && n > 0 && tokens >= 0,
+             "grouped W4A16 requires nonzero dimensions");
+  if (int rc = check_pow2_group(k, group)) return rc;
+  if (int rc = check_schedule_dims(tokens, routes, experts)) return rc;
+  if (tokens == 0) return LK_OK;
+  LK_REQUIRE(x && idx && workspace, "null pointer argument");
+  const int64_t entries = tokens * routes;
+  const MoeLayout l = moe_layout(entries, experts, 0, 0);
+  LK_REQUIRE(workspace_bytes >= static_cast<int64_t>(l.total),
+             "%s: workspace too small: %lld < %lld bytes", name, (long long)workspace_bytes,
+             (long long)l.total);
+  char* ws = static_cast<char*>(workspace);
+  hipStream_t s = as_stream(stream);
+  auto* offsets = reinterpret_cast<int32_t*>(ws + l.offsets);
+  auto* perm = reinterpret_cast<int32_t*>(ws + l.perm);
+  auto* tiles = reinterpret_cast<int32_t*>(ws + l.tiles);
+  auto* count = reinterpret_cast<int32_t*>(ws + l.count);
+  const RouteTable rt{idx, routes, routes, experts, -1};
+  if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, s)) return rc;
+  GemmArgs g{};
+  g.a = x;
+  g.perm = perm;
+  g.tiles = tiles;
+  g.tile_count = count;
+  g.wp[0] = p0;
+  g.ws[0] = s0;
+  g.wp[1] = swiglu ? p1 : p0;
+  g.ws[1] = swiglu ? s1 : s0;
+  g.wp[2] = p0;
+  g.ws[2] = s0;
+  g.out[0] = g.out[1] = g.out[2] = out;
+  g.n = n;
+  g.k = k;
+  g.group = group;
+  g.wstride = n * k / 2;
+  g.sstride = n * (k / group);
+  g.routes = routes;
+  g.outputs = 1;
+  const bool wc = wide_cols_for(l.sched.max_tiles, n);
+  if (swiglu)
+    return gemm_launch<2>(g, Mode::GatherScatter, l.sched.max_tiles, wc, s, name);
+  return gemm_launch<1>(g, Mode::GatherScatter, l.sched.max_tiles, wc, s, name);
+}
+
+int lk_w4a16_grouped_gemm(const uint16_t* x, const int64_t* expert_indices,
+                          const uint8_t* packed, const uint16_t* scales, uint16_t* out,
+                          int64_t tokens, int64_t routes, int64_t experts, int64_t n, int64_t k,
+                          int64_t group_size, void* workspace, int64_t workspace_bytes,
+                          void* stream) {
+  return grouped_gemm_common(x, expert_indices, packed, scales, nullptr, nullptr, out, tokens,
+                             routes, experts, n, k, group_size, workspace, workspace_bytes,
+                             stream, false, "lk_w4a16_grouped_gemm");
+}
+
+int lk_w4a16_swiglu_gemm(const uint16_t* x, const int64_t* expert_indices,
+                         const uint8_t* w1_packed, const uint16_t* w1_scales,
+                         const uint8_t* w3_packed, const uint16_t* w3_scales, uint16_t* out,
+                         int64_t tokens, int64_t routes, int64_t experts, int64_t n, int64_t k,
+                         int64_t group_size, void* workspace, int64_t workspace_bytes,
+                         void* stream) {
+  return grouped_gemm_common(x, expert_indices, w1_packed, w1_scales, w3_packed, w3_scales, out,
+                             tokens, routes, experts, n, k, group_size, workspace,
+                             workspace_bytes, stream, true, "lk_w4a16_swiglu_gemm");
+}
+
+int lk_w4a16_dense_gemm(const uint16_t* x, const uint8_t* packed, const uint16_t* scales,
+                        uint16_t* y, int64_t m, int64_t n, int64_t k, int64_t group_size,
+                        void* stream) {
+  LK_REQUIRE(packed && scales && y, "null pointer argument");
+  LK_REQUIRE(m >= 0 && n > 0, "invalid dense dimensions m=%lld n=%lld", (long long)m,
+             (long long)n);
+  if (int rc = check_pow2_group(k, group_size)) return rc;
+  if (m == 0) return LK_OK;
+  LK_REQUIRE(x != nullptr, "null activation pointer");
+  LK_REQUIRE(m < (1LL << 30), "too many rows");
+  GemmArgs g{};
+  g.a = x;
+  g.wp[0] = g.wp[1] = g.wp[2] = packed;
+  g.ws[0] = g.ws[1] = g.ws[2] = scales;
+  g.out[0] = g.out[1] = g.out[2] = y;
+  g.n = n;
+  g.k = k;
+  g.group = group_size;
+  g.routes = 1;
+  g.dense_rows = static_cast<int>(m);
+  g.outputs = 1;
+  const int64_t tiles = (m + kTileRows - 1) / kTileRows;
+  return gemm_launch<1>(g, Mode::Dense, tiles, wide_cols_for(tiles, n), as_stream(stream),
+                        "lk_w4a16_dense_gemm");
+}
+
+int lk_w4a16_fused_qkv(const uint16_t* x, const uint8_t* q_packed, const uint16_t* q_scales,
+                       const uint8_t* k_packed, const uint16_t* k_scales,
+                       const uint8_t* v_packed, const uint16_t* v_scales, uint16_t* q,
+                       uint16_t* k_out, uint16_t* v, int64_t m, int64_t n, int64_t k,
+                       int64_t group_size, void* stream) {
+  LK_REQUIRE(q_packed && q_scales && k_packed && k_scales && v_packed && v_scales && q && k_out &&
+                 v,
+             "null pointer argument");
+  LK_REQUIRE(m >= 0 && n > 0, "invalid QKV dimensions m=%lld n=%lld", (long long)m,
+             (long long)n);
+  if (int rc = check_pow2_group(k, group_size)) return rc;
+  if (m == 0) return LK_OK;
+  LK_REQUIRE(x != nullptr, "null activation pointer");
+  if (m < 16) {  // decode rows: the GEMV path, one launch per projection
+    if (int rc = lk_w4a16_dense(x, q_packed, q_scales, q, m, n, k, group_size, stream)) return rc;
+    if (int rc = lk_w4a16_dense(x, k_packed, k_scales, k_out, m, n, k, group_size, stream))
+      return rc;
+    return lk_w4a16_dense(x, v_packed, v_scales, v, m, n, k, group_size, stream);
+  }
+  LK_REQUIRE(m < (1LL << 30), "too many rows");
+  GemmArgs g{};
+  g.a = x;
+  g.wp[0] = q_packed;
+  g.wp[1] = k_packed;
+  g.wp[2] = v_packed;
+  g.ws[0] = q_scales;
+  g.ws[1] = k_scales;
+  g.ws[2] = v_scales;
+  g.out[0] = q;
+  g.out[1] = k_out;
+  g.out[2] = v;
+  g.n = n;
+  g.k = k;
+  g.group = group_size;
+  g.routes = 1;
+  g.dense_rows = static_cast<int>(m);
+  g.outputs = 3;
+  const int64_t tiles = (m + kTileRows - 1) / kTileRows;
+  return gemm_launch<1>(g, Mode::Dense, tiles, wide_cols_for(3 * tiles, n), as_stream(stream),
+                        "lk_w4a16_fused_qkv");
+}
+
+int64_t lk_w4a16_moe_forward_workspace(int64_t tokens, int64_t experts, int64_t h, int64_t i,
+                                       int64_t top_k) {
+  if (tokens < 0 || experts < 2 || h <= 0 || i <= 0 || top_k <= 0) return -1;
+  if (check_schedule_dims(tokens, top_k + 1, experts)) return -1;
+  return static_cast<int64_t>(moe_layout(tokens * (top_k + 1), experts, i, h).total);
+}
+
+int lk_w4a16_moe_forward(const uint16_t* x, const float* logits, const float* bias,
+                         const uint8_t* w1_packed, const uint16_t* w1_scales,
+                         const uint8_t* w3_packed, const uint16_t* w3_scales,
+                         const uint8_t* w2_packed, const uint16_t* w2_scales, uint16_t* y,
+                         int64_t* expert_indices, float* weights, void* workspace,
+                         int64_t workspace_bytes, int64_t tokens, int64_t experts, int64_t h,
+                         int64_t i, int64_t top_k, float routed_scaling_factor, int renormalize,
+                         int64_t group_size, void* stream) {
+  LK_REQUIRE(w1_packed && w1_scales && w3_packed && w3_scales && w2_packed && w2_scales && y &&
+                 expert_indices && weights,
+             "null pointer argument");
+  LK_REQUIRE(experts >= 2, "experts (routed + shared) must be at least 2");
+  LK_REQUIRE(top_k > 0 && top_k <= 32 && top_k <= experts - 1, "invalid top_k %lld",
+             (long long)top_k);
+  LK_REQUIRE(h > 0 && i > 0 && tokens >= 0, "invalid dimensions");
+  LK_REQUIRE(h % 8 == 0, "hidden size must be a multiple of 8, got %lld", (long long)h);
+  if (int rc = check_pow2_group(h, group_size)) return rc;
+  if (int rc = check_pow2_group(i, group_size)) return rc;
+  if (int rc = check_schedule_dims(tokens, top_k + 1, experts)) return rc;
+  if (tokens == 0) return LK_OK;
+  LK_REQUIRE(x && logits && workspace, "null pointer argument");
+  const int64_t routes = top_k + 1;
+  const int64_t entries = tokens * routes;
+  const MoeLayout l = moe_layout(entries, experts, i, h);
+  LK_REQUIRE(workspace_bytes >= static_cast<int64_t>(l.total),
+             "MoE workspace too small: %lld < %lld bytes", (long long)workspace_bytes,
+             (long long)l.total);
+  hipStream_t s = as_stream(stream);
+  if (int rc = lk_moe_router(logits, bias, expert_indices, weights, tokens, experts - 1, top_k,
+                             routed_scaling_factor, renormalize, stream))
+    return rc;
+  char* ws = static_cast<char*>(workspace);
+  auto* offsets = reinterpret_cast<int32_t*>(ws + l.offsets);
+  auto* perm = reinterpret_cast<int32_t*>(ws + l.perm);
+  auto* tiles = reinterpret_cast<int32_t*>(ws + l.tiles);
+  auto* count = reinterpret_cast<int32_t*>(ws + l.count);
+  auto* act = reinterpret_cast<uint16_t*>(ws + l.act);
+  auto* eo = reinterpret_cast<uint16_t*>(ws + l.eo);
+  const RouteTable rt{expert_indices, top_k, routes, experts, experts - 1};
+  if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, s)) return rc;
+
+  GemmArgs g{};
+  g.perm = perm;
+  g.tiles = tiles;
+  g.tile_count = count;
+  g.group = group_size;
+  g.routes = routes;
+  g.outputs = 1;
+  // gate/up + SwiGLU: rows gathered from x, activations written in sorted order
+  g.a = x;
+  g.wp[0] = w1_packed;
+  g.ws[0] = w1_scales;
+  g.wp[1] = w3_packed;
+  g.ws[1] = w3_scales;
+  g.wp[2] = w1_packed;
+  g.ws[2] = w1_scales;
+  g.out[0] = g.out[1] = g.out[2] = act;
+  g.n = i;
+  g.k = h;
+  g.wstride = i * h / 2;
+  g.sstride = i * (h / group_size);
+  const int64_t mt = l.sched.max_tiles;
+  if (int rc = gemm_launch<2>(g, Mode::Gather, mt, wide_cols_for(mt, i), s, "moe gate/up gemm"))
+    return rc;
+  // down projection: sorted activation rows, outputs scattered to (token, route) rows
+  g.a = act;
+  g.wp[0] = g.wp[1] = g.wp[2] = w2_packed;
+  g.ws[0] = g.ws[1] = g.ws[2] = w2_scales;
+  g.out[0] = g.out[1] = g.out[2] = eo;
+  g.n = h;
+  g.k = i;
+  g.wstride = h * i / 2;
+  g.sstride = h * (i / group_size);
+  if (int rc = gemm_launch<1>(g, Mode::Scatter, mt, wide_cols_for(mt, h), s, "moe down gemm"))
+    return rc;
+  const int64_t work = tokens * (h / 8);
+  moe_combine_kernel<<<static_cast<unsigned>((work + 255) / 256), 256, 0, s>>>(
+      eo, weights, y, tokens, static_cast<int>(top_k), h);
+  return check_launch("moe combine");
+}
+
+}  // extern "C"

@@ -222,6 +222,13 @@ int check_group(int64_t k, int64_t group) {
   return LK_OK;
 }
 
+int check_pow2_group(int64_t k, int64_t group) {
+  if (int rc = check_group(k, group)) return rc;
+  LK_REQUIRE((group & (group - 1)) == 0, "group size must be a power of two, got %lld",
+             (long long)group);
+  return LK_OK;
+}
+
 }  // namespace lk
 
 using namespace lk;

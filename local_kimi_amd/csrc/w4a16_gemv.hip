@@ -919,13 +919,6 @@ int pick_iters(int cpr) {
     default: { constexpr int IT = 16; BODY; } break; \
   }
 
-int check_pow2_group(int64_t k, int64_t group) {
-  if (int rc = check_group(k, group)) return rc;
-  LK_REQUIRE((group & (group - 1)) == 0, "group size must be a power of two, got %lld",
-             (long long)group);
-  return LK_OK;
-}
-
 constexpr size_t kMaxLds = 64 * 1024;
 
 }  // namespace

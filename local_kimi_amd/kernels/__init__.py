@@ -17,12 +17,14 @@ raises on first call.
 """
 
 from . import registry
-from .moe import (moe_router, shape_stable_expert_indices, w4a16_moe_block,
-                  w4a16_moe_block_reference, w4a16_moe_gateup)
+from .moe import (moe_router, moe_schedule, shape_stable_expert_indices, w4a16_moe_block,
+                  w4a16_moe_block_reference, w4a16_moe_decode, w4a16_moe_forward,
+                  w4a16_moe_gateup)
 from .w4a16 import (fused_qkv_w4a16, fused_qkv_w4a16_reference, fused_w2_combine,
-                    fused_w2_combine_reference, grouped_w4a16_gemv, grouped_w4a16_reference,
+                    fused_w2_combine_reference, grouped_w4a16_gemm, grouped_w4a16_gemv,
+                    grouped_w4a16_reference, grouped_w4a16_swiglu_gemm,
                     grouped_w4a16_swiglu_gemv, route_combine, silu_mul, w4a16_dense,
-                    w4a16_dense_reference)
+                    w4a16_dense_gemm, w4a16_dense_reference)
 
 W4A16_GROUPED = "w4a16_grouped"
 W4A16_DENSE = "w4a16_dense"
@@ -109,6 +111,8 @@ _register_others()
 __all__ = [
     "registry", "W4A16_GROUPED", "W4A16_DENSE", "W4A16_SWIGLU", "W4A16_FUSED_QKV",
     "W4A16_W2_COMBINE", "W4A16_MOE_BLOCK", "moe_router", "shape_stable_expert_indices",
-    "w4a16_moe_block", "w4a16_moe_gateup", "w4a16_dense", "grouped_w4a16_gemv", "grouped_w4a16_swiglu_gemv",
+    "w4a16_moe_block", "w4a16_moe_decode", "w4a16_moe_forward", "w4a16_moe_gateup",
+    "moe_schedule", "w4a16_dense", "w4a16_dense_gemm", "grouped_w4a16_gemv",
+    "grouped_w4a16_gemm", "grouped_w4a16_swiglu_gemv", "grouped_w4a16_swiglu_gemm",
     "fused_w2_combine", "fused_qkv_w4a16", "route_combine", "silu_mul",
 ]

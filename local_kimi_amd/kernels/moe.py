@@ -4,8 +4,12 @@
 logits; ``w4a16_moe_block`` is the grouped branch of KLinearMoE.forward
 (engine/klinear/moe.py:278-334, 375-398): route, gate/up + SwiGLU over the
 top-k routes and the shared expert, W2, weighted combine plus shared expert.
-The fused HIP path runs it in two launches (router + gate/up + SwiGLU, then
-W2 + combine); the reference variant composes the reference ops.
+Batch-1 decode runs in two launches (router + gate/up + SwiGLU, then W2 +
+combine). From ``MOE_EXPERT_MAJOR_MIN_TOKENS`` tokens the block runs
+expert-major: router, a counting-sort schedule of the routes by expert
+(engine/kernels/moe_grouped.py:77-160), an MFMA gate/up + SwiGLU GEMM over
+64-row expert tiles, the down GEMM scattered back to (token, route) rows and
+the combine. The reference variant composes the reference ops.
 
 Expert banks hold the routed experts first and the shared expert last
 (``[E_routed + 1, ...]``), exactly as ``prepare_grouped_w4a16`` stacks them
@@ -18,6 +22,40 @@ import torch
 
 from .. import _lib
 from . import w4a16 as _w
+
+
+# tokens from which the MoE block runs expert-major (each expert read once)
+MOE_EXPERT_MAJOR_MIN_TOKENS = 2
+# bank entries (routed + shared) the expert-major schedule supports
+MOE_EXPERT_MAJOR_MAX_EXPERTS = 512
+
+
+def moe_schedule(expert_indices: torch.Tensor, experts: int, shared_expert: int = -1):
+    """Expert-major schedule of a route table on the GPU.
+
+    Returns ``(offsets int32 [E+2], perm int32 [T*R], tiles int32 [n, 4],
+    tile_count int32 [1])`` with ``R = routes (+1 if shared_expert >= 0)``;
+    see ``lk_moe_schedule`` in include/lk_w4a16.h for the table contracts.
+    """
+    if expert_indices.ndim != 2 or expert_indices.dtype != torch.long:
+        raise TypeError("expert_indices must be an int64 [tokens, routes] matrix")
+    if expert_indices.device.type != "cuda":
+        raise ValueError("the HIP schedule requires CUDA")
+    tokens, routes = expert_indices.shape
+    r_total = routes + (1 if shared_expert >= 0 else 0)
+    max_tiles, ws_bytes = _lib.schedule_sizes(tokens, r_total, experts)
+    dev = expert_indices.device
+    offsets = torch.empty((experts + 2,), dtype=torch.int32, device=dev)
+    perm = torch.empty((tokens * r_total,), dtype=torch.int32, device=dev)
+    tiles = torch.empty((max_tiles, 4), dtype=torch.int32, device=dev)
+    count = torch.empty((1,), dtype=torch.int32, device=dev)
+    ws = _w.workspace(ws_bytes, dev)
+    idx = _w._c(expert_indices)
+    with torch.cuda.device(dev):
+        _lib.call("lk_moe_schedule", idx.data_ptr(), tokens, routes, experts, shared_expert,
+                  offsets.data_ptr(), perm.data_ptr(), tiles.data_ptr(), count.data_ptr(),
+                  ws.data_ptr(), ws.numel(), _w._stream(dev))
+    return offsets, perm, tiles, count
 
 
 def shape_stable_expert_indices(expert_indices: torch.Tensor, shared_expert_id: int) -> torch.Tensor:
@@ -110,10 +148,51 @@ def _validate_block(hidden, logits, bias, w1_packed, w1_scales, w3_packed, w3_sc
 def w4a16_moe_block(hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor | None,
                     w1_packed, w1_scales, w3_packed, w3_scales, w2_packed, w2_scales, top_k: int,
                     routed_scaling_factor: float = 1.0, renormalize: bool = True):
-    """Router + SwiGLU experts + W2 + combine + shared expert in two HIP launches.
+    """Router + SwiGLU experts + W2 + combine + shared expert on HIP.
 
+    One token: two launches (token-major decode). More tokens: the
+    expert-major path (:func:`w4a16_moe_forward`).
     Returns ``(y bf16 [T, H], expert_indices int64 [T, k], weights float32 [T, k])``.
     """
+    if hidden.ndim == 2 and hidden.shape[0] >= MOE_EXPERT_MAJOR_MIN_TOKENS and \
+            w1_packed.ndim == 3 and w1_packed.shape[0] <= MOE_EXPERT_MAJOR_MAX_EXPERTS:
+        return w4a16_moe_forward(hidden, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
+                                 w2_packed, w2_scales, top_k, routed_scaling_factor, renormalize)
+    return w4a16_moe_decode(hidden, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
+                            w2_packed, w2_scales, top_k, routed_scaling_factor, renormalize)
+
+
+def w4a16_moe_forward(hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor | None,
+                      w1_packed, w1_scales, w3_packed, w3_scales, w2_packed, w2_scales,
+                      top_k: int, routed_scaling_factor: float = 1.0, renormalize: bool = True):
+    """The expert-major block (router, schedule, two MFMA GEMMs, combine)."""
+    tokens, e_total, h, inter, g = _validate_block(hidden, logits, bias, w1_packed, w1_scales,
+                                                   w3_packed, w3_scales, w2_packed, w2_scales, top_k)
+    dev = hidden.device
+    y = torch.empty((tokens, h), dtype=torch.bfloat16, device=dev)
+    idx = torch.empty((tokens, top_k), dtype=torch.long, device=dev)
+    w = torch.empty((tokens, top_k), dtype=torch.float32, device=dev)
+    if tokens == 0:
+        return y, idx, w
+    ws = _w.workspace(_lib.query("lk_w4a16_moe_forward_workspace", tokens, e_total, h, inter,
+                                 top_k), dev)
+    c = _w._c
+    x, lg = c(hidden), c(logits)
+    b = c(bias) if bias is not None else None
+    args = [c(t) for t in (w1_packed, w1_scales, w3_packed, w3_scales, w2_packed, w2_scales)]
+    with torch.cuda.device(dev):
+        _lib.call("lk_w4a16_moe_forward", x.data_ptr(), lg.data_ptr(),
+                  b.data_ptr() if b is not None else None, *(t.data_ptr() for t in args),
+                  y.data_ptr(), idx.data_ptr(), w.data_ptr(), ws.data_ptr(), ws.numel(), tokens,
+                  e_total, h, inter, top_k, float(routed_scaling_factor), int(bool(renormalize)),
+                  g, _w._stream(dev))
+    return y, idx, w
+
+
+def w4a16_moe_decode(hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor | None,
+                     w1_packed, w1_scales, w3_packed, w3_scales, w2_packed, w2_scales, top_k: int,
+                     routed_scaling_factor: float = 1.0, renormalize: bool = True):
+    """The token-major block in two launches (any token count; fastest at one)."""
     tokens, e_total, h, inter, g = _validate_block(hidden, logits, bias, w1_packed, w1_scales,
                                                    w3_packed, w3_scales, w2_packed, w2_scales, top_k)
     dev = hidden.device

@@ -35,6 +35,17 @@ def _c(t: torch.Tensor) -> torch.Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
 
+# Row counts from which the expert-major / MFMA GEMM paths replace the
+# per-route GEMV kernels (token-routes for the grouped ops, rows for dense).
+GROUPED_GEMM_MIN_ROUTES = 32
+DENSE_GEMM_MIN_ROWS = 16
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Scratch device memory from the torch caching allocator."""
+    return torch.empty((max(int(nbytes), 1),), dtype=torch.uint8, device=device)
+
+
 def check_bank(packed: torch.Tensor, scales: torch.Tensor, what: str) -> tuple[int, int, int, int]:
     """Validate one grouped bank without touching its data: ``(E, N, K, G)``."""
     if packed.ndim != 3 or scales.ndim != 3:
@@ -96,8 +107,20 @@ def _dense(entry: str, activations, packed_weights, scales):
 
 def w4a16_dense(activations: torch.Tensor, packed_weights: torch.Tensor,
                 scales: torch.Tensor) -> torch.Tensor:
-    """``y[M, N] = x @ dequant(W).T`` with the gfx950 GEMV (registered as ``hip``)."""
+    """``y[M, N] = x @ dequant(W).T`` (registered as ``hip``).
+
+    Decode rows use the K-split GEMV; from ``DENSE_GEMM_MIN_ROWS`` rows the
+    MFMA GEMM (weights read once per 64-row tile).
+    """
+    if activations.ndim == 2 and activations.shape[0] >= DENSE_GEMM_MIN_ROWS:
+        return _dense("lk_w4a16_dense_gemm", activations, packed_weights, scales)
     return _dense("lk_w4a16_dense", activations, packed_weights, scales)
+
+
+def w4a16_dense_gemm(activations: torch.Tensor, packed_weights: torch.Tensor,
+                     scales: torch.Tensor) -> torch.Tensor:
+    """The MFMA GEMM form of :func:`w4a16_dense` at any row count."""
+    return _dense("lk_w4a16_dense_gemm", activations, packed_weights, scales)
 
 
 def w4a16_dense_reference(activations: torch.Tensor, packed_weights: torch.Tensor,
@@ -147,9 +170,20 @@ def _grouped(entry: str, activations, expert_indices, packed_weights, scales):
         return out
     x, idx, p, s = _c(activations), _c(expert_indices), _c(packed_weights), _c(scales)
     with torch.cuda.device(activations.device):
-        _lib.call(entry, x.data_ptr(), idx.data_ptr(), p.data_ptr(), s.data_ptr(), out.data_ptr(),
-                  t, r, e, n, k, g, _stream(activations.device))
+        if entry.endswith("_gemm"):
+            ws = workspace(_lib.query("lk_w4a16_grouped_gemm_workspace", t, r, e), x.device)
+            _lib.call(entry, x.data_ptr(), idx.data_ptr(), p.data_ptr(), s.data_ptr(),
+                      out.data_ptr(), t, r, e, n, k, g, ws.data_ptr(), ws.numel(),
+                      _stream(activations.device))
+        else:
+            _lib.call(entry, x.data_ptr(), idx.data_ptr(), p.data_ptr(), s.data_ptr(),
+                      out.data_ptr(), t, r, e, n, k, g, _stream(activations.device))
     return out
+
+
+def _use_grouped_gemm(activations, expert_indices) -> bool:
+    return (expert_indices.ndim == 2 and activations.ndim == 2
+            and expert_indices.shape[0] * expert_indices.shape[1] >= GROUPED_GEMM_MIN_ROUTES)
 
 
 def grouped_w4a16_gemv(activations: torch.Tensor, expert_indices: torch.Tensor,
@@ -157,9 +191,17 @@ def grouped_w4a16_gemv(activations: torch.Tensor, expert_indices: torch.Tensor,
     """``out[t, r] = x[t] @ dequant(W[idx[t, r]]).T`` -> ``[T, R, N]`` bf16.
 
     Expert indices outside ``[0, E)`` are treated as empty routes (zeros) so a
-    bad index cannot read past the bank.
+    bad index cannot read past the bank. From ``GROUPED_GEMM_MIN_ROUTES``
+    token-routes the routes are sorted by expert and run as an MFMA GEMM.
     """
-    return _grouped("lk_w4a16_grouped", activations, expert_indices, packed_weights, scales)
+    entry = "lk_w4a16_grouped_gemm" if _use_grouped_gemm(activations, expert_indices) \
+        else "lk_w4a16_grouped"
+    return _grouped(entry, activations, expert_indices, packed_weights, scales)
+
+
+def grouped_w4a16_gemm(activations, expert_indices, packed_weights, scales):
+    """The expert-major MFMA form of :func:`grouped_w4a16_gemv` at any size."""
+    return _grouped("lk_w4a16_grouped_gemm", activations, expert_indices, packed_weights, scales)
 
 
 def grouped_w4a16_reference(activations, expert_indices, packed_weights, scales):
@@ -183,9 +225,8 @@ def _validate_swiglu(activations, expert_indices, w1_packed, w1_scales, w3_packe
     return dims
 
 
-def grouped_w4a16_swiglu_gemv(activations, expert_indices, w1_packed, w1_scales, w3_packed,
-                              w3_scales) -> torch.Tensor:
-    """One launch: ``bf16(bf16(silu(bf16(x W1^T))) * bf16(x W3^T))`` per route."""
+def _swiglu(gemm: bool, activations, expert_indices, w1_packed, w1_scales, w3_packed,
+            w3_scales) -> torch.Tensor:
     t, r, e, n, k, g = _validate_swiglu(activations, expert_indices, w1_packed, w1_scales,
                                         w3_packed, w3_scales)
     out = torch.empty((t, r, n), dtype=torch.bfloat16, device=activations.device)
@@ -193,11 +234,32 @@ def grouped_w4a16_swiglu_gemv(activations, expert_indices, w1_packed, w1_scales,
         return out
     x, idx = _c(activations), _c(expert_indices)
     p1, s1, p3, s3 = _c(w1_packed), _c(w1_scales), _c(w3_packed), _c(w3_scales)
+    args = [x.data_ptr(), idx.data_ptr(), p1.data_ptr(), s1.data_ptr(), p3.data_ptr(),
+            s3.data_ptr(), out.data_ptr(), t, r, e, n, k, g]
     with torch.cuda.device(activations.device):
-        _lib.call("lk_w4a16_swiglu", x.data_ptr(), idx.data_ptr(), p1.data_ptr(), s1.data_ptr(),
-                  p3.data_ptr(), s3.data_ptr(), out.data_ptr(), t, r, e, n, k, g,
-                  _stream(activations.device))
+        if gemm:
+            ws = workspace(_lib.query("lk_w4a16_grouped_gemm_workspace", t, r, e), x.device)
+            _lib.call("lk_w4a16_swiglu_gemm", *args, ws.data_ptr(), ws.numel(),
+                      _stream(activations.device))
+        else:
+            _lib.call("lk_w4a16_swiglu", *args, _stream(activations.device))
     return out
+
+
+def grouped_w4a16_swiglu_gemv(activations, expert_indices, w1_packed, w1_scales, w3_packed,
+                              w3_scales) -> torch.Tensor:
+    """One launch: ``bf16(bf16(silu(bf16(x W1^T))) * bf16(x W3^T))`` per route.
+
+    From ``GROUPED_GEMM_MIN_ROUTES`` token-routes: the expert-major MFMA GEMM.
+    """
+    return _swiglu(_use_grouped_gemm(activations, expert_indices), activations, expert_indices,
+                   w1_packed, w1_scales, w3_packed, w3_scales)
+
+
+def grouped_w4a16_swiglu_gemm(activations, expert_indices, w1_packed, w1_scales, w3_packed,
+                              w3_scales) -> torch.Tensor:
+    """The expert-major MFMA form of :func:`grouped_w4a16_swiglu_gemv`."""
+    return _swiglu(True, activations, expert_indices, w1_packed, w1_scales, w3_packed, w3_scales)
 
 
 def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
@@ -329,11 +391,27 @@ def _validate_qkv(activations, q_packed, q_scales, k_packed, k_scales, v_packed,
 
 
 def fused_qkv_w4a16(activations, q_packed, q_scales, k_packed, k_scales, v_packed, v_scales):
-    """Q, K and V projections of one activation matrix -> ``(q, k, v)``."""
+    """Q, K and V projections of one activation matrix -> ``(q, k, v)``.
+
+    From 16 rows one MFMA GEMM launch covers all three matrices; decode rows
+    run the GEMV once per matrix.
+    """
     _validate_qkv(activations, q_packed, q_scales, k_packed, k_scales, v_packed, v_scales)
-    return (w4a16_dense(activations, q_packed, q_scales),
-            w4a16_dense(activations, k_packed, k_scales),
-            w4a16_dense(activations, v_packed, v_scales))
+    m, k = activations.shape
+    n = q_packed.shape[0]
+    g = _group_size(k, q_scales.shape[1], "q")
+    if _group_size(k, k_scales.shape[1], "k") != g or _group_size(k, v_scales.shape[1], "v") != g:
+        raise ValueError("fused QKV projections must share one group size")
+    dev = activations.device
+    outs = [torch.empty((m, n), dtype=torch.bfloat16, device=dev) for _ in range(3)]
+    if m == 0:
+        return tuple(outs)
+    x = _c(activations)
+    w = [_c(t) for t in (q_packed, q_scales, k_packed, k_scales, v_packed, v_scales)]
+    with torch.cuda.device(dev):
+        _lib.call("lk_w4a16_fused_qkv", x.data_ptr(), *(t.data_ptr() for t in w),
+                  *(o.data_ptr() for o in outs), m, n, k, g, _stream(dev))
+    return tuple(outs)
 
 
 def fused_qkv_w4a16_reference(activations, q_packed, q_scales, k_packed, k_scales, v_packed,

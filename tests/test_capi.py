@@ -54,3 +54,19 @@ def test_argument_errors_are_reported_without_touching_the_gpu(lib):
         _lib.call("lk_w4a16_dense", 1, 1, 1, 1, 1, 8, 192, 96, None)
     with pytest.raises(RuntimeError, match="top_k"):
         _lib.call("lk_moe_router", 1, None, 1, 1, 1, 4, 9, 1.0, 1, None)
+
+
+def test_expert_major_sizes_and_argument_errors(lib):
+    max_tiles, ws = _lib.schedule_sizes(2048, 9, 257)
+    # prefill bound: min(E + 1, n) + n / 64 + 1 tiles of 64 rows
+    assert max_tiles == 258 + 18432 // 64 + 1
+    assert ws >= 18432 * 4
+    assert _lib.query("lk_w4a16_moe_forward_workspace", 64, 257, 2304, 1024, 8) > 0
+    assert lib.lk_w4a16_moe_forward_workspace(64, 1000, 2304, 1024, 8) == -1
+    assert lib.lk_w4a16_grouped_gemm_workspace(4, 0, 8) == -1
+    with pytest.raises(RuntimeError, match="experts"):
+        _lib.schedule_sizes(4, 8, 600)
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        _lib.call("lk_moe_schedule", 1, 4, 8, 16, -1, 1, 1, 1, 1, 1, 8, None)
+    with pytest.raises(RuntimeError, match="divisible"):
+        _lib.call("lk_w4a16_dense_gemm", 1, 1, 1, 1, 16, 8, 100, 32, None)

@@ -1,0 +1,301 @@
+"""GPU parity of the expert-major path: route schedule and MFMA GEMMs.
+
+Bit-exact: the schedule tables (offsets, permutation, tiles) against
+oracle.moe.schedule_tables and an independent tile walk. Tolerance (stated
+here, from the quantized-matmul contract): bf16 outputs within 1e-2 relative
+/ 2e-2 absolute of the oracle. Full-size cases compare against the oracle on
+the experts the sampled tokens use, and against the token-major GPU path on
+every token.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as OM
+from oracle import w4a16 as OW
+
+from ._helpers import assert_close_bf16, from_bits, random_bf16_bits, to_bits
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _require_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    from local_kimi_amd import _lib
+
+    _lib.load()
+
+
+def _dev(a):
+    if a.dtype == np.uint16:
+        return from_bits(a, DEV)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _bank(rng, e, n, k, g):
+    ps, ss = [], []
+    for _ in range(e):
+        p, s = OW.quantise(random_bf16_bits(rng, (n, k), 0.02), g)
+        ps.append(p)
+        ss.append(s)
+    return np.stack(ps), np.stack(ss)
+
+
+# ---------------------------------------------------------------------------
+# schedule
+
+
+def _expected_tiles(offsets, experts):
+    tiles = []
+    for b in range(experts + 1):
+        cnt = int(offsets[b + 1] - offsets[b])
+        for row in range(0, cnt, 64):
+            tiles.append((b if b < experts else -1, int(offsets[b]) + row, min(64, cnt - row), 0))
+    return np.array(tiles, dtype=np.int32).reshape(-1, 4)
+
+
+@pytest.mark.parametrize("tokens,routes,experts,shared,invalid", [
+    (1, 8, 257, 256, False),      # batch-1 decode
+    (7, 8, 16, -1, True),         # sentinel and out-of-range routes
+    (64, 8, 257, 256, False),     # batched decode, two chunks
+    (300, 9, 64, -1, True),       # six chunks with invalid routes
+    (2048, 8, 257, 256, False),   # prefill: 18432 entries
+    (5, 3, 512, -1, False),       # largest bank
+    (700, 1, 3, -1, False),       # one hot expert split over many tiles
+])
+def test_schedule_matches_oracle(rng, tokens, routes, experts, shared, invalid):
+    from local_kimi_amd.kernels import moe_schedule
+
+    high = experts - 1 if shared >= 0 else experts
+    idx = rng.integers(0, high, (tokens, routes)).astype(np.int64)
+    if invalid:
+        flat = idx.reshape(-1)
+        pick = rng.choice(flat.size, size=max(1, flat.size // 7), replace=False)
+        flat[pick] = rng.choice(np.array([-1, experts, experts + 5, -7]), size=pick.size)
+    offsets, perm, tiles, count = moe_schedule(_dev(idx), experts, shared)
+    full = idx if shared < 0 else np.concatenate(
+        (idx, np.full((tokens, 1), shared, dtype=np.int64)), axis=1)
+    flat = full.reshape(-1)
+    valid = (flat >= 0) & (flat < experts)
+    counts, eoff, eperm = OM.schedule_tables(np.where(valid, flat, -1).reshape(full.shape), experts)
+    off = offsets.cpu().numpy()
+    assert np.array_equal(off[: experts + 1], eoff)
+    assert off[experts + 1] == flat.size
+    p = perm.cpu().numpy()
+    assert np.array_equal(p[: eoff[-1]], eperm)
+    assert np.array_equal(p[eoff[-1]:], np.nonzero(~valid)[0])
+    want = _expected_tiles(off, experts)
+    n_tiles = int(count.item())
+    assert n_tiles == len(want)
+    assert np.array_equal(tiles.cpu().numpy()[:n_tiles], want)
+    # rerun: identical tables
+    again = moe_schedule(_dev(idx), experts, shared)
+    assert torch.equal(again[1], perm) and torch.equal(again[0], offsets)
+
+
+# ---------------------------------------------------------------------------
+# dense GEMM and fused QKV
+
+
+@pytest.mark.parametrize("m,n,k,g", [
+    (16, 96, 256, 32), (64, 128, 512, 64), (100, 2304, 2304, 128), (130, 200, 384, 128),
+    (17, 48, 96, 32), (64, 64, 512, 256), (70, 80, 320, 64),
+])
+def test_dense_gemm_matches_oracle(rng, m, n, k, g):
+    from local_kimi_amd.kernels import w4a16_dense_gemm
+
+    p, s = OW.quantise(random_bf16_bits(rng, (n, k), 0.02), g)
+    x = random_bf16_bits(rng, (m, k))
+    y = w4a16_dense_gemm(_dev(x), _dev(p), _dev(s))
+    assert_close_bf16(to_bits(y), OW.dense(x, p, s, g), what=f"dense gemm {m}x{n}x{k} G{g}")
+    assert torch.equal(y, w4a16_dense_gemm(_dev(x), _dev(p), _dev(s)))
+
+
+@pytest.mark.parametrize("m", [4, 64, 100])
+def test_fused_qkv_matches_oracle(rng, m):
+    from local_kimi_amd.kernels import fused_qkv_w4a16
+
+    n, k, g = 256, 512, 128
+    mats = [OW.quantise(random_bf16_bits(rng, (n, k), 0.02), g) for _ in range(3)]
+    x = random_bf16_bits(rng, (m, k))
+    flat = [a for pair in mats for a in pair]
+    got = fused_qkv_w4a16(_dev(x), *(_dev(a) for a in flat))
+    want = OW.fused_qkv(x, *flat, g)
+    for name, a, e in zip("qkv", got, want):
+        assert_close_bf16(to_bits(a), e, what=f"fused qkv {name} m={m}")
+
+
+# ---------------------------------------------------------------------------
+# grouped GEMMs
+
+
+@pytest.mark.parametrize("g", [32, 128])
+def test_grouped_gemm_matches_oracle(rng, g):
+    from local_kimi_amd.kernels import grouped_w4a16_gemm, grouped_w4a16_swiglu_gemm
+
+    t, r, e, n, k = 40, 3, 6, 96, 256
+    x = random_bf16_bits(rng, (t, k))
+    idx = rng.integers(0, e, (t, r)).astype(np.int64)
+    idx[3, 1] = -1
+    idx[7, 0] = e + 2
+    bad = (idx < 0) | (idx >= e)
+    safe = np.where(bad, 0, idx)
+    p, s = _bank(rng, e, n, k, g)
+    out = to_bits(grouped_w4a16_gemm(_dev(x), _dev(idx), _dev(p), _dev(s)))
+    want = OW.grouped(x, safe, p, s, g)
+    want[bad] = 0
+    assert_close_bf16(out, want, what="grouped gemm")
+    assert not out[bad].any()
+    p3, s3 = _bank(rng, e, n, k, g)
+    act = to_bits(grouped_w4a16_swiglu_gemm(_dev(x), _dev(idx), _dev(p), _dev(s), _dev(p3),
+                                            _dev(s3)))
+    want = OW.swiglu(x, safe, p, s, p3, s3, g)
+    want[bad] = 0
+    assert_close_bf16(act, want, what="swiglu gemm")
+
+
+def test_grouped_dispatch_uses_gemm_for_many_routes(rng):
+    """The registered op switches to the expert-major GEMM; same results."""
+    from local_kimi_amd.kernels import grouped_w4a16_gemv
+    from local_kimi_amd.kernels import w4a16 as W
+
+    t, r, e, n, k, g = 20, 4, 5, 64, 256, 128
+    assert t * r >= W.GROUPED_GEMM_MIN_ROUTES
+    x = random_bf16_bits(rng, (t, k))
+    idx = rng.integers(0, e, (t, r)).astype(np.int64)
+    p, s = _bank(rng, e, n, k, g)
+    out = to_bits(grouped_w4a16_gemv(_dev(x), _dev(idx), _dev(p), _dev(s)))
+    assert_close_bf16(out, OW.grouped(x, idx, p, s, g), what="grouped dispatch")
+
+
+# ---------------------------------------------------------------------------
+# expert-major MoE block
+
+
+def _moe_inputs(rng, e_routed, h, i, g, tokens, zipf=False):
+    from local_kimi_amd.workloads import normal_router_logits, zipf_router_logits
+
+    banks = (*_bank(rng, e_routed + 1, i, h, g), *_bank(rng, e_routed + 1, i, h, g),
+             *_bank(rng, e_routed + 1, h, i, g))
+    x = random_bf16_bits(rng, (tokens, h))
+    logits = (zipf_router_logits if zipf else normal_router_logits)(rng, tokens, e_routed)
+    return x, logits, banks
+
+
+@pytest.mark.parametrize("tokens,g,zipf", [(2, 128, False), (5, 128, True), (37, 32, False),
+                                           (64, 128, True)])
+def test_moe_forward_matches_oracle_small_bank(rng, tokens, g, zipf):
+    from local_kimi_amd.kernels import w4a16_moe_decode, w4a16_moe_forward
+
+    h, i = (512, 256) if g == 128 else (256, 128)
+    x, logits, banks = _moe_inputs(rng, 16, h, i, g, tokens, zipf)
+    ey, eidx, ew = OM.moe_block(x, logits, None, *banks, top_k=4, routed_scaling_factor=2.446,
+                                group_size=g)
+    args = (_dev(x), _dev(logits), None, *(_dev(b) for b in banks), 4, 2.446)
+    y, idx, w = w4a16_moe_forward(*args)
+    assert np.array_equal(idx.cpu().numpy(), eidx)
+    np.testing.assert_allclose(w.cpu().numpy(), ew, rtol=2e-6)
+    assert_close_bf16(to_bits(y), ey, what=f"moe forward T={tokens}")
+    assert torch.equal(y, w4a16_moe_forward(*args)[0])
+    yd, _, _ = w4a16_moe_decode(*args)
+    assert_close_bf16(to_bits(y), to_bits(yd), what="expert-major vs token-major")
+
+
+def test_moe_forward_with_bias_and_grouped_router_inputs(rng):
+    from local_kimi_amd.kernels import w4a16_moe_forward
+
+    x, logits, banks = _moe_inputs(rng, 32, 256, 128, 128, 9)
+    bias = rng.normal(0, 0.5, 32).astype(np.float32)
+    ey, eidx, _ = OM.moe_block(x, logits, bias, *banks, top_k=6, routed_scaling_factor=1.0,
+                               group_size=128, renormalize=False)
+    y, idx, _ = w4a16_moe_forward(_dev(x), _dev(logits), _dev(bias), *(_dev(b) for b in banks),
+                                  6, 1.0, False)
+    assert np.array_equal(idx.cpu().numpy(), eidx)
+    assert_close_bf16(to_bits(y), ey, what="moe forward with bias")
+
+
+@pytest.fixture(scope="module")
+def kimi_banks():
+    """Kimi-Linear MoE banks: hidden 2304, 256 routed + 1 shared experts,
+    intermediate 1024, G=128, weights N(0, 0.02) quantised on the GPU."""
+    from local_kimi_amd.quant import quantise
+
+    e_total, h, i, g = 257, 2304, 1024, 128
+    gen = torch.Generator(device=DEV).manual_seed(20260731)
+
+    def bank(n, k):
+        packed = torch.empty((e_total, n, k // 2), dtype=torch.uint8, device=DEV)
+        scales = torch.empty((e_total, n, k // g), dtype=torch.bfloat16, device=DEV)
+        for e in range(e_total):
+            w = (torch.randn(n, k, device=DEV, generator=gen) * 0.02).to(torch.bfloat16)
+            enc = quantise(w, group_size=g)
+            packed[e].copy_(enc.packed)
+            scales[e].copy_(enc.scales)
+        return packed, scales
+
+    return (*bank(i, h), *bank(i, h), *bank(h, i))
+
+
+def _oracle_tokens(x, logits, banks, tokens_sel, top_k=8, scaling=2.446, g=128):
+    """Oracle block output of selected tokens, using only the experts they route to."""
+    eidx, ew = OM.route(logits[tokens_sel], None, top_k, routed_scaling_factor=scaling)
+    e_total = banks[0].shape[0]
+    used = sorted(set(eidx.reshape(-1).tolist()) | {e_total - 1})
+    remap = {e: j for j, e in enumerate(used)}
+    sub = [b[used].cpu().numpy() if b.dtype == torch.uint8 else to_bits(b[used]) for b in banks]
+    stable = np.array([[remap[e] for e in row] + [remap[e_total - 1]] for row in eidx.tolist()])
+    xs = x[tokens_sel]
+    act = OW.swiglu(xs, stable, sub[0], sub[1], sub[2], sub[3], g)
+    cw = np.concatenate((ew, np.ones((len(tokens_sel), 1), np.float32)), 1)
+    return OM.w2_combine(act, stable, cw, sub[4], sub[5], g), eidx
+
+
+@pytest.mark.parametrize("tokens,zipf", [(4, True), (16, True), (64, True), (2048, False)])
+def test_moe_forward_full_size(rng, kimi_banks, tokens, zipf):
+    """Batched decode (Zipf routing) and prefill (N(0,1) logits) at the Kimi shape."""
+    from local_kimi_amd.kernels import w4a16_moe_decode, w4a16_moe_forward
+    from local_kimi_amd.workloads import normal_router_logits, zipf_router_logits
+
+    x = random_bf16_bits(rng, (tokens, 2304))
+    logits = (zipf_router_logits if zipf else normal_router_logits)(rng, tokens, 256)
+    args = (_dev(x), _dev(logits), None, *kimi_banks, 8, 2.446)
+    y, idx, _ = w4a16_moe_forward(*args)
+    yd, idxd, _ = w4a16_moe_decode(*args)
+    assert torch.equal(idx, idxd)
+    assert_close_bf16(to_bits(y), to_bits(yd), what="expert-major vs token-major")
+    sel = np.unique(rng.choice(tokens, size=min(tokens, 6), replace=False))
+    ey, eidx = _oracle_tokens(x, logits, kimi_banks, sel)
+    assert np.array_equal(idx.cpu().numpy()[sel], eidx)
+    worst = assert_close_bf16(to_bits(y)[sel], ey, what=f"moe forward T={tokens}")
+    assert worst < 0.75
+
+
+def test_moe_forward_under_graph_replay(rng):
+    from local_kimi_amd.kernels import w4a16_moe_forward
+
+    x, logits, banks = _moe_inputs(rng, 8, 256, 128, 128, 6)
+    dev = [_dev(b) for b in banks]
+    xd, ld = _dev(x), _dev(logits)
+    eager, eidx, _ = w4a16_moe_forward(xd, ld, None, *dev, 2, 2.446)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        w4a16_moe_forward(xd, ld, None, *dev, 2, 2.446)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gy, gidx, _ = w4a16_moe_forward(xd, ld, None, *dev, 2, 2.446)
+    for _ in range(4):
+        gy.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gy, eager) and torch.equal(gidx, eidx)
+        _ = (xd.float() * 2).sum().item()
