@@ -267,6 +267,163 @@ def run_dense(args, dev) -> dict:
     return result
 
 
+def _layer_banks(layers: int, gen: torch.Generator, dev):
+    master = (*make_bank(INTER, H, E_ROUTED + 1, gen, dev), *make_bank(INTER, H, E_ROUTED + 1, gen, dev),
+              *make_bank(H, INTER, E_ROUTED + 1, gen, dev))
+    return [master] + [tuple(t.clone() for t in master) for _ in range(layers - 1)]
+
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+EXPERT_FLOPS = 2 * 3 * INTER * H  # gate, up and down projections per routed row
+
+
+def run_moe_batched(args, dev) -> dict:
+    """Batched decode: M tokens per step, Zipf(1.1)-skewed routing, expert-major path."""
+    from local_kimi_amd.kernels import w4a16_moe_decode, w4a16_moe_forward
+    from local_kimi_amd.workloads import zipf_router_logits
+    from oracle import moe as OM
+
+    block = w4a16_moe_forward if args.moe_path == "expert" else w4a16_moe_decode
+
+    m, layers = args.tokens, args.layers
+    gen = torch.Generator(device=dev).manual_seed(20260729)
+    rng = np.random.default_rng(20260729)
+    t0 = time.time()
+    banks = _layer_banks(layers, gen, dev)
+    xs = [(torch.randn((m, H), device=dev, generator=gen)).to(torch.bfloat16) for _ in range(layers)]
+    host_logits = [zipf_router_logits(rng, m, E_ROUTED) for _ in range(layers)]
+    logits = [torch.from_numpy(lg).to(dev) for lg in host_logits]
+    unions = [len(np.unique(OM.route(lg, None, TOP_K)[0])) for lg in host_logits]
+    torch.cuda.synchronize()
+    log(f"[bench] {layers} layer banks ready in {time.time() - t0:.1f}s; distinct routed "
+        f"experts per layer: mean {np.mean(unions):.1f} (min {min(unions)}, max {max(unions)})")
+    stream = torch.cuda.Stream(device=dev)
+
+    def all_layers():
+        for l in range(layers):
+            block(xs[l], logits[l], None, *banks[l], TOP_K, SCALING)
+
+    graph = capture(all_layers, stream)
+    reps = max(1, args.steps // layers)
+    warm = max(1, args.warmup // layers)
+    for _ in range(warm):
+        graph.replay()
+    ms = time_graph(graph, reps, stream)
+    steps = reps * layers
+    us_step = ms * 1000.0 / steps
+    step_bytes = float(np.mean([(u + 1) * EXPERT_BYTES for u in unions])) + m * TOKEN_IO_BYTES
+    step_flops = m * (TOP_K + 1) * EXPERT_FLOPS
+    gbps = step_bytes / (us_step * 1e3)
+    return {
+        "metric": "Batched MoE decode us/step + achieved HBM GB/s (% of peak) at W4A16",
+        "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": steps,
+        "warmup": warm * layers, "ms_per_step": round(ms / steps, 6), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x, "
+                "Zipf(1.1) router logits (log p + Gumbel)",
+        "config": {"workload": f"moe_batched_decode_m{m}", "path": f"{args.moe_path}-major",
+                   "tokens_per_step": m, "hidden": H,
+                   "routed_experts": E_ROUTED, "shared_experts": 1, "moe_intermediate": INTER,
+                   "top_k": TOP_K, "group_size": G, "layer_banks_rotated": layers,
+                   "mean_distinct_routed_experts": round(float(np.mean(unions)), 2)},
+        "us_per_token": round(us_step / m, 3),
+        "achieved_gbps": round(gbps, 1),
+        "pct_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
+        "algorithmic_bytes_per_step": int(step_bytes),
+        "roofline": {"kernel": "whole block (router, schedule, gate/up GEMM, down GEMM, combine)",
+                     "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "mfma_tflops": round(step_flops / (us_step * 1e6), 2)},
+    }
+
+
+def run_moe_prefill(args, dev) -> dict:
+    """Prefill: 2048 tokens x top-8 (+ shared) through one layer, N(0,1) logits."""
+    from local_kimi_amd.kernels import w4a16_moe_forward
+
+    m = args.prefill_tokens
+    gen = torch.Generator(device=dev).manual_seed(20260729)
+    banks = _layer_banks(2, gen, dev)
+    xs = [(torch.randn((m, H), device=dev, generator=gen)).to(torch.bfloat16) for _ in range(2)]
+    logits = [torch.randn((m, E_ROUTED), device=dev, generator=gen) for _ in range(2)]
+    stream = torch.cuda.Stream(device=dev)
+
+    def both():
+        for l in range(2):
+            w4a16_moe_forward(xs[l], logits[l], None, *banks[l], TOP_K, SCALING)
+
+    graph = capture(both, stream)
+    reps = max(1, args.prefill_steps // 2)
+    for _ in range(3):
+        graph.replay()
+    ms = time_graph(graph, reps, stream)
+    steps = 2 * reps
+    us = ms * 1000.0 / steps
+    nbytes = (E_ROUTED + 1) * EXPERT_BYTES + m * TOKEN_IO_BYTES
+    flops = m * (TOP_K + 1) * EXPERT_FLOPS
+    tflops = flops / (us * 1e6)
+    gbps = nbytes / (us * 1e3)
+    return {
+        "metric": "MoE prefill us/layer + MFMA TFLOP/s and HBM GB/s at W4A16",
+        "value": round(us, 2), "unit": "us/layer", "n_gpus": 1, "steps": steps, "warmup": 6,
+        "ms_per_step": round(ms / steps, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x and logits",
+        "config": {"workload": f"moe_prefill_{m}", "tokens": m, "hidden": H, "routed_experts": E_ROUTED,
+                   "shared_experts": 1, "moe_intermediate": INTER, "top_k": TOP_K, "group_size": G},
+        "tokens_per_s": round(m / (us * 1e-6), 1),
+        "achieved_gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+        "achieved_tflops": round(tflops, 1),
+        "pct_mfma_peak": round(100 * tflops / MFMA_BF16_PEAK_TFLOPS, 2),
+        "algorithmic_bytes_per_step": nbytes, "flops_per_step": flops,
+        "roofline": {"kernel": "whole block (router, schedule, gate/up GEMM, down GEMM, combine)",
+                     "bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": None, "hbm_gbps": round(gbps, 1)},
+    }
+
+
+def run_qkv_prefill(args, dev) -> dict:
+    """Fused QKV projection of 2048 tokens: [2048, 2304] x [2304, 3 x 4096] at W4A16."""
+    from local_kimi_amd.kernels import fused_qkv_w4a16
+    from local_kimi_amd.quant import quantise
+
+    m, n = args.prefill_tokens, 4096
+    gen = torch.Generator(device=dev).manual_seed(20260729)
+    mats = []
+    for _ in range(3):
+        enc = quantise((torch.randn((n, H), device=dev, generator=gen) * 0.02).to(torch.bfloat16),
+                       group_size=G)
+        mats += [enc.packed, enc.scales]
+    x = torch.randn((m, H), device=dev, generator=gen).to(torch.bfloat16)
+    stream = torch.cuda.Stream(device=dev)
+    graph = capture(lambda: fused_qkv_w4a16(x, *mats), stream)
+    reps = max(1, args.prefill_steps)
+    for _ in range(3):
+        graph.replay()
+    ms = time_graph(graph, reps, stream)
+    us = ms * 1000.0 / reps
+    nbytes = 3 * w4a16_bytes(n, H) + m * H * 2 + 3 * m * n * 2
+    flops = 2 * m * H * 3 * n
+    tflops = flops / (us * 1e6)
+    return {
+        "metric": "Fused QKV prefill GEMM us + MFMA TFLOP/s at W4A16",
+        "value": round(us, 2), "unit": "us/call", "n_gpus": 1, "steps": reps, "warmup": 3,
+        "ms_per_step": round(ms / reps, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x",
+        "config": {"workload": f"qkv_prefill_{m}", "m": m, "n_per_projection": n, "k": H,
+                   "group_size": G},
+        "achieved_tflops": round(tflops, 1),
+        "pct_mfma_peak": round(100 * tflops / MFMA_BF16_PEAK_TFLOPS, 2),
+        "achieved_gbps": round(nbytes / (us * 1e3), 1),
+        "algorithmic_bytes_per_step": nbytes, "flops_per_step": flops,
+        "roofline": {"kernel": "w4a16_gemm_kernel (dense, 3 outputs)", "bound": "mfma",
+                     "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None},
+    }
+
+
 def run_copy(args, dev) -> dict:
     """Plain device copy of a known size: calibrates the HBM byte counters."""
     nbytes = args.copy_mb << 20
@@ -292,7 +449,14 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2600)
     ap.add_argument("--warmup", type=int, default=260)
-    ap.add_argument("--workload", choices=["moe_decode", "dense_decode", "copy"], default="moe_decode")
+    ap.add_argument("--workload", default="moe_decode",
+                    choices=["moe_decode", "dense_decode", "moe_batched", "moe_prefill",
+                             "qkv_prefill", "copy"])
+    ap.add_argument("--tokens", type=int, default=64, help="moe_batched tokens per step")
+    ap.add_argument("--moe-path", choices=["expert", "token"], default="expert",
+                    help="moe_batched: expert-major GEMMs or the token-major GEMV kernels")
+    ap.add_argument("--prefill-tokens", type=int, default=2048)
+    ap.add_argument("--prefill-steps", type=int, default=40)
     ap.add_argument("--copy-mb", type=int, default=256, help="copy workload size (MiB)")
     ap.add_argument("--layers", type=int, default=26, help="MoE layer banks rotated")
     ap.add_argument("--copies", type=int, default=40, help="dense weight copies rotated")
@@ -310,7 +474,8 @@ def main() -> int:
     _lib.load()
     dev = torch.device("cuda:0")
     log(f"[bench] device {torch.cuda.get_device_name(0)}, workload {args.workload}")
-    runners = {"moe_decode": run_moe, "dense_decode": run_dense, "copy": run_copy}
+    runners = {"moe_decode": run_moe, "dense_decode": run_dense, "moe_batched": run_moe_batched,
+               "moe_prefill": run_moe_prefill, "qkv_prefill": run_qkv_prefill, "copy": run_copy}
     result = runners[args.workload](args, dev)
     print(json.dumps(result), flush=True)
     return 0

@@ -231,6 +231,74 @@ LK_API int lk_w4a16_moe_forward(const uint16_t* x, const float* logits, const fl
                                 float routed_scaling_factor, int renormalize, int64_t group_size,
                                 void* stream);
 
+/* ---- MXFP4 (OCP MX): E2M1 codes low nibble first, one E8M0 exponent per
+ *      32 values along K; value = e2m1 * 2**(e8m0 - 127).
+ *      engine/k3ref/dequant.py:18-73 (codec), engine/kernels/reference.py:29-80
+ *      (dequantize + linear), engine/kernels/mxfp4_gemm.py:191-235 (GEMM op). */
+
+/* weight bf16 [N,K] -> packed [N,K/2], scale uint8 [N,K/32]. The reference has
+ * no encoder: shared exponent floor(log2(amax)) - 2 (bias 127, clamped to
+ * [0, 254], 127 for an all-zero block), elements rounded to the E2M1 grid
+ * with ties to the even code and saturation at +-6 (OCP MX v1.0). */
+LK_API int lk_mxfp4_quantise(const uint16_t* weight, uint8_t* packed, uint8_t* scale, int64_t n,
+                             int64_t k, void* stream);
+
+/* packed + scale -> out [N,K]: float32 values when out_f32 != 0, else bf16
+ * (one rounding of the exact value; -0.0 kept). */
+LK_API int lk_mxfp4_dequantise(const uint8_t* packed, const uint8_t* scale, void* out, int64_t n,
+                               int64_t k, int out_f32, void* stream);
+
+/* y [M,N] = x [M,K] . dequant(W)^T, fp32 accumulation, output in the
+ * activation type: bf16 (act_f16 == 0) or fp16 (act_f16 != 0).
+ * engine/kernels/mxfp4_gemm.py:191-226. */
+LK_API int lk_mxfp4_gemm(const uint16_t* x, const uint8_t* packed, const uint8_t* scale,
+                         uint16_t* y, int64_t m, int64_t n, int64_t k, int act_f16, void* stream);
+
+/* The same op as the reference variant: each weight decoded to the activation
+ * type, then an fp32 dot, one thread per output
+ * (engine/kernels/reference.py:67-80). */
+LK_API int lk_mxfp4_gemm_reference(const uint16_t* x, const uint8_t* packed, const uint8_t* scale,
+                                   uint16_t* y, int64_t m, int64_t n, int64_t k, int act_f16,
+                                   void* stream);
+
+/* Grouped MXFP4 banks packed [E,N,K/2], scale [E,N,K/32]; the contracts of
+ * lk_w4a16_grouped_gemm / lk_w4a16_swiglu_gemm (bf16 activations; workspace
+ * from lk_w4a16_grouped_gemm_workspace). */
+LK_API int lk_mxfp4_grouped_gemm(const uint16_t* x, const int64_t* expert_indices,
+                                 const uint8_t* packed, const uint8_t* scale, uint16_t* out,
+                                 int64_t tokens, int64_t routes, int64_t experts, int64_t n,
+                                 int64_t k, void* workspace, int64_t workspace_bytes,
+                                 void* stream);
+LK_API int lk_mxfp4_swiglu_gemm(const uint16_t* x, const int64_t* expert_indices,
+                                const uint8_t* w1_packed, const uint8_t* w1_scale,
+                                const uint8_t* w3_packed, const uint8_t* w3_scale, uint16_t* out,
+                                int64_t tokens, int64_t routes, int64_t experts, int64_t n,
+                                int64_t k, void* workspace, int64_t workspace_bytes,
+                                void* stream);
+
+/* The MoE block of lk_w4a16_moe_forward with MXFP4 expert banks (the
+ * Kimi-Linear SwiGLU block; workspace from lk_w4a16_moe_forward_workspace). */
+LK_API int lk_mxfp4_moe_forward(const uint16_t* x, const float* logits, const float* bias,
+                                const uint8_t* w1_packed, const uint8_t* w1_scale,
+                                const uint8_t* w3_packed, const uint8_t* w3_scale,
+                                const uint8_t* w2_packed, const uint8_t* w2_scale, uint16_t* y,
+                                int64_t* expert_indices, float* weights, void* workspace,
+                                int64_t workspace_bytes, int64_t tokens, int64_t experts,
+                                int64_t h, int64_t i, int64_t top_k,
+                                float routed_scaling_factor, int renormalize, void* stream);
+
+/* One packed expert MLP with K3's SiTU activation:
+ * engine/kernels/moe_grouped.py:163-194 (mxfp4_expert_mlp, situ_and_mul).
+ * activated bf16 [M,I] = bf16(beta*tanh(g/beta)*sigmoid(g) * lb*tanh(u/lb))
+ * with g, u the bf16 gate / up projections (no lb term when
+ * situ_linear_beta <= 0); y bf16 [M,H] = activated . dequant(W2)^T. */
+LK_API int lk_mxfp4_expert_mlp(const uint16_t* x, const uint8_t* w1_packed,
+                               const uint8_t* w1_scale, const uint8_t* w3_packed,
+                               const uint8_t* w3_scale, const uint8_t* w2_packed,
+                               const uint8_t* w2_scale, uint16_t* y, uint16_t* activated,
+                               int64_t m, int64_t h, int64_t i, float situ_beta,
+                               float situ_linear_beta, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,6 +47,16 @@ SIGNATURES: dict[str, list] = {
     "lk_w4a16_fused_qkv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "lk_w4a16_moe_forward": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                              _I64, _I64, _I64, _I64, _I64, _F, _I, _I64, _P],
+    "lk_mxfp4_quantise": [_P, _P, _P, _I64, _I64, _P],
+    "lk_mxfp4_dequantise": [_P, _P, _P, _I64, _I64, _I, _P],
+    "lk_mxfp4_gemm": [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P],
+    "lk_mxfp4_gemm_reference": [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P],
+    "lk_mxfp4_grouped_gemm": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P],
+    "lk_mxfp4_swiglu_gemm": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
+                             _P, _I64, _P],
+    "lk_mxfp4_moe_forward": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
+                             _I64, _I64, _I64, _I64, _I64, _F, _I, _P],
+    "lk_mxfp4_expert_mlp": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _P],
 }
 
 # name -> argument types of the size queries (they return int64, -1 on bad input)

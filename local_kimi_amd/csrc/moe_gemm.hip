@@ -196,21 +196,26 @@ schedule_place_kernel(const RouteTable rt, int64_t n, int chunks, Schedule sc) {
 // ---------------------------------------------------------------------------
 // W4A16 GEMM on the matrix cores
 
+enum : int { kFmtW4A16 = 0, kFmtMxBf16 = 1, kFmtMxF16 = 2 };  // weight format x activation type
+enum : int { kActSwiglu = 0, kActSitu = 1 };                   // two-matrix epilogues
+
 struct GemmArgs {
-  const uint16_t* a;         // activations bf16, rows of k
+  const uint16_t* a;         // activations (bf16, or fp16 for kFmtMxF16), rows of k
   const int32_t* perm;       // sorted position -> entry (gather / scatter modes)
   const int32_t* tiles;      // [*, 4] tile list (schedule modes)
   const int32_t* tile_count;
-  const uint8_t* wp[3];      // packed weights per output matrix (SwiGLU: W1, W3)
-  const uint16_t* ws[3];
+  const uint8_t* wp[3];      // packed weights per output matrix (two-matrix: gate, up)
+  const void* ws[3];         // scales: bf16 (W4A16) or E8M0 bytes (MXFP4)
   uint16_t* out[3];
   int64_t n, k, group;
   int64_t wstride;           // packed bytes per expert
-  int64_t sstride;           // scales per expert
+  int64_t sstride;           // scale elements per expert
   int64_t routes;            // entries per token (gather: token = entry / routes)
   int dense_rows;            // rows of a dense product
   int col_blocks;            // column blocks per output matrix
   int outputs;               // output matrices (3 for fused QKV, else 1)
+  int act;                   // two-matrix epilogue (kActSwiglu / kActSitu)
+  float situ_beta, situ_linear_beta;  // SiTU parameters; linear_beta <= 0: none
 };
 
 template <typename T>
@@ -218,7 +223,11 @@ __device__ inline T pick3(const T (&v)[3], int i) {
   return i == 0 ? v[0] : (i == 1 ? v[1] : v[2]);
 }
 
-constexpr int kSub = 4;  // 16-row MFMA subtiles per 64-row tile
+constexpr int kSub = 4;       // 16-row MFMA subtiles per 64-row tile
+constexpr int kGemmWaves = 4;
+constexpr uint32_t kOnesBf16x2 = 0x3F803F80u;  // (1.0, 1.0) in bf16
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 
 __device__ inline bf16x8_t unpack_q8(uint32_t w) {
   const uint32_t u = w ^ kNibbleFlip;
@@ -227,36 +236,83 @@ __device__ inline bf16x8_t unpack_q8(uint32_t w) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
+// 2**(e - 127) as fp32 for an E8M0 byte (e = 0: the subnormal 2**-127, 255: inf)
+__device__ inline float e8m0_to_f32(uint32_t e) {
+  return __builtin_bit_cast(float, e == 0u ? 0x00400000u : e << 23);
+}
+
+// 8 E2M1 codes (natural order, low nibble first) times 2**(e - 127), exact in
+// bf16 / fp16 within range: the gfx950 scaled convert, two codes per byte.
+__device__ inline u32x4_t unpack_fp4x8_bf16(uint32_t w, float scale) {
+  const u32x4_t v = {
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3))};
+  return v;
+}
+__device__ inline u32x4_t unpack_fp4x8_f16(uint32_t w, float scale) {
+  const u32x4_t v = {
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 0)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 1)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 2)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 3))};
+  return v;
+}
+
+// K3's SiTU (engine/kernels/moe_grouped.py:163-178): gate and up rounded to
+// bf16 first (they are linear outputs), fp32 math, one rounding at the end.
+__device__ inline uint16_t situ_bf16(float gate_acc, float up_acc, float beta, float lbeta) {
+  const float g = round_bf16(gate_acc);
+  float u = round_bf16(up_acc);
+  const float ag = beta * tanhf(g / beta) * (1.0f / (1.0f + expf(-g)));
+  if (lbeta > 0.f) u = lbeta * tanhf(u / lbeta);
+  return f32_to_bf16(ag * u);
+}
+
+// fp32 sum of 8 bf16 activations: four dot2 against (1, 1), exact products
+__device__ inline float sum_x8_dot(const uint4 v) {
+  float s = dot2_bf16(v.x, kOnesBf16x2, 0.f);
+  s = dot2_bf16(v.y, kOnesBf16x2, s);
+  s = dot2_bf16(v.z, kOnesBf16x2, s);
+  return dot2_bf16(v.w, kOnesBf16x2, s);
+}
+
 // One 128-wide k-step of a lane's weights: 4 packed dwords (one per MFMA) and
-// the scale bits of the group each MFMA belongs to, per matrix and column tile.
-template <int MATS, int NT, bool WIDE>
+// the scale of the group each MFMA belongs to, per matrix and column tile.
+// W4A16 with G >= 128 (WIDE): one 16-byte load, one group per step.
+// Otherwise each MFMA covers 32 consecutive codes (one dword per lane).
+template <int FMT, int MATS, int NT, bool WIDE>
 struct WeightStep {
   uint32_t w[MATS][NT][4];
-  uint16_t s[MATS][NT][4];
+  uint32_t s[MATS][NT][4];  // bf16 bits (W4A16) or E8M0 byte (MXFP4)
 
   __device__ inline void load(const uint8_t* const (&wrow)[MATS][NT],
-                              const uint16_t* const (&srow)[MATS][NT], int step, int jq,
-                              int64_t k, int64_t group) {
+                              const void* const (&srow)[MATS][NT], int step, int jq, int64_t k,
+                              int64_t group) {
 #pragma unroll
     for (int mi = 0; mi < MATS; ++mi) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         if constexpr (WIDE) {
-          // G >= 128: k is a multiple of 128, the whole step lies in one group
-          const uint4 v =
-              *reinterpret_cast<const uint4*>(wrow[mi][nt] + static_cast<int64_t>(step) * 64 + jq * 16);
+          const uint4 v = *reinterpret_cast<const uint4*>(
+              wrow[mi][nt] + static_cast<int64_t>(step) * 64 + jq * 16);
           w[mi][nt][0] = v.x;
           w[mi][nt][1] = v.y;
           w[mi][nt][2] = v.z;
           w[mi][nt][3] = v.w;
-          s[mi][nt][0] = srow[mi][nt][static_cast<int64_t>(step) * 128 / group];
+          s[mi][nt][0] = static_cast<const uint16_t*>(
+              srow[mi][nt])[static_cast<int64_t>(step) * 128 / group];
         } else {
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const int64_t k0 = static_cast<int64_t>(step) * 128 + 32 * t;
             const int64_t kk = k0 < k ? k0 : 0;  // sub-steps past k are skipped
             w[mi][nt][t] = *reinterpret_cast<const uint32_t*>(wrow[mi][nt] + kk / 2 + jq * 4);
-            s[mi][nt][t] = srow[mi][nt][kk / group];
+            if constexpr (FMT == kFmtW4A16)
+              s[mi][nt][t] = static_cast<const uint16_t*>(srow[mi][nt])[kk / group];
+            else
+              s[mi][nt][t] = static_cast<const uint8_t*>(srow[mi][nt])[kk / 32];
           }
         }
       }
@@ -264,18 +320,24 @@ struct WeightStep {
   }
 };
 
-// Block = WAVES waves over one 64-row tile x (WAVES * NT * 16) columns; each
-// wave owns NT 16-column MFMA tiles of every matrix and all active 16-row
-// subtiles. Activations go through LDS (double buffered, one barrier per
-// 128-wide k-step); weights go straight from HBM into registers one k-step
-// ahead.
-template <int MATS, int NT, int WAVES, bool WIDE, bool GATHER, bool SCATTER, bool DENSE>
-__global__ void __launch_bounds__(WAVES * kWave)
+// Block = 4 waves over one 64-row tile x (64 * NT) columns; each wave owns NT
+// 16-column MFMA tiles of every matrix and all active 16-row subtiles.
+// Activations go through LDS (double buffered, one barrier per 128-wide
+// k-step; only the tile's real rows are staged); weights go straight from HBM
+// into registers two k-steps ahead.
+// W4A16: a group's MFMA chain starts from C = -136 * sum(x) (staged with the
+// activations), so closing the group is one FMA per output: tot += s_g * acc.
+// MXFP4: the scale is applied by the decode, one chain over all of k.
+template <int FMT, int MATS, int NT, bool WIDE, bool GATHER, bool SCATTER, bool DENSE>
+__global__ void __launch_bounds__(kGemmWaves * kWave, 2)
 w4a16_gemm_kernel(const GemmArgs g) {
-  constexpr int kThreads = WAVES * kWave;
+  constexpr bool kMx = FMT != kFmtW4A16;
+  static_assert(!(kMx && WIDE), "MXFP4 groups are 32 wide");
+  constexpr int kThreads = kGemmWaves * kWave;
   constexpr int kUPT = kTileRows * 16 / kThreads;  // 16-byte activation units per thread
-  constexpr int kBN = WAVES * NT * 16;
+  constexpr int kBN = kGemmWaves * NT * 16;
   __shared__ uint4 a_lds[2][kSub * 4 * kWave];
+  // W4A16: -136 * sum(x) per (row, group-in-step); WIDE: one group part per step
   __shared__ __attribute__((aligned(16))) float off_lds[2][4 * kTileRows];
 
   // blocks of one tile sit on one XCD (block ids are dealt round robin to the 8 XCDs)
@@ -323,9 +385,10 @@ w4a16_gemm_kernel(const GemmArgs g) {
   const int64_t spr = K / g.group;
   const int ksteps = static_cast<int>((K + 127) / 128);
   const int mt_act = (rows + 15) >> 4;
+  const int cg = static_cast<int>(g.group / 32);  // narrow W4A16 groups: MFMAs per group
 
   const uint8_t* wrow[MATS][NT];
-  const uint16_t* srow[MATS][NT];
+  const void* srow[MATS][NT];
   int64_t col[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -334,19 +397,25 @@ w4a16_gemm_kernel(const GemmArgs g) {
 #pragma unroll
     for (int mi = 0; mi < MATS; ++mi) {
       wrow[mi][nt] = pick3(g.wp, osel + mi) + expert * g.wstride + cc * rowb;
-      srow[mi][nt] = pick3(g.ws, osel + mi) + expert * g.sstride + cc * spr;
+      if constexpr (kMx)
+        srow[mi][nt] = static_cast<const uint8_t*>(pick3(g.ws, osel + mi)) + expert * g.sstride +
+                       cc * spr;
+      else
+        srow[mi][nt] = static_cast<const uint16_t*>(pick3(g.ws, osel + mi)) +
+                       expert * g.sstride + cc * spr;
     }
   }
 
-  // activation rows this thread stages (unit u: row u / 16, 8-code unit u % 16)
+  // activation rows this thread stages (unit u: row u / 16, 8-code unit u % 16);
+  // rows past the tile's end are neither loaded nor staged (their outputs are
+  // never stored and MFMA rows are independent)
   const uint16_t* arow[kUPT];
-  uint32_t amask[kUPT];
+  bool aok[kUPT];
 #pragma unroll
   for (int i = 0; i < kUPT; ++i) {
     const int m = (tid + i * kThreads) >> 4;
-    const bool ok = m < rows;
-    amask[i] = ok ? 0xFFFFFFFFu : 0u;
-    const int mm = ok ? m : 0;
+    aok[i] = m < rows;
+    const int mm = aok[i] ? m : 0;
     int64_t r;
     if constexpr (GATHER) r = g.perm[row0 + mm] / g.routes;
     else r = row0 + mm;
@@ -356,11 +425,13 @@ w4a16_gemm_kernel(const GemmArgs g) {
   auto load_a = [&](int step) {
 #pragma unroll
     for (int i = 0; i < kUPT; ++i) {
-      const int c = (tid + i * kThreads) & 15;
-      const int64_t k0 = static_cast<int64_t>(step) * 128 + c * 8;
-      const uint32_t msk = k0 < K ? amask[i] : 0u;
-      const uint4 v = *reinterpret_cast<const uint4*>(arow[i] + (k0 < K ? k0 : 0));
-      av[i] = make_uint4(v.x & msk, v.y & msk, v.z & msk, v.w & msk);
+      if (aok[i]) {
+        const int c = (tid + i * kThreads) & 15;
+        const int64_t k0 = static_cast<int64_t>(step) * 128 + c * 8;
+        const uint4 v = *reinterpret_cast<const uint4*>(arow[i] + (k0 < K ? k0 : 0));
+        const uint32_t msk = k0 < K ? 0xFFFFFFFFu : 0u;
+        av[i] = make_uint4(v.x & msk, v.y & msk, v.z & msk, v.w & msk);
+      }
     }
   };
   // LDS fragment (subtile ms, MFMA t) is 64 x 16 bytes read by lane l at
@@ -369,22 +440,31 @@ w4a16_gemm_kernel(const GemmArgs g) {
   auto commit_a = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < kUPT; ++i) {
-      const int u = tid + i * kThreads;
-      const int m = u >> 4, c = u & 15;
-      const int t = WIDE ? (c & 3) : (c >> 2);
-      const int j = WIDE ? (c >> 2) : (c & 3);
-      uint32_t p[4];
-      pair_x8(av[i], p);
-      a_lds[buf][((m >> 4) * 4 + t) * kWave + j * 16 + ((m & 15) ^ (4 * t + j))] =
-          make_uint4(p[0], p[1], p[2], p[3]);
-      float sx = sum_x8(av[i]);
-      if constexpr (WIDE) {
-        sx = sum8(sx);
-        sx += dpp_f32<kRowMirror>(sx);  // the 16 units of a row sit in one 16-lane row
-        if (c == 0) off_lds[buf][m] = kCodeOffset * sx;
-      } else {
-        sx = sum4(sx);  // the 4 units of a 32-code sub-step sit in one lane quad
-        if (j == 0) off_lds[buf][t * kTileRows + m] = kCodeOffset * sx;
+      if (aok[i]) {  // uniform over the 16 lanes of one row (the DPP row)
+        const int u = tid + i * kThreads;
+        const int m = u >> 4, c = u & 15;
+        const int t = WIDE ? (c & 3) : (c >> 2);
+        const int j = WIDE ? (c >> 2) : (c & 3);
+        uint4* dst = &a_lds[buf][((m >> 4) * 4 + t) * kWave + j * 16 + ((m & 15) ^ (4 * t + j))];
+        if constexpr (kMx) {
+          *dst = av[i];  // natural order: the fp4 decode keeps codes in order
+        } else {
+          uint32_t p[4];
+          pair_x8(av[i], p);
+          *dst = make_uint4(p[0], p[1], p[2], p[3]);
+          float sx = sum_x8_dot(av[i]);
+          if constexpr (WIDE) {
+            sx = sum8(sx);
+            sx += dpp_f32<kRowMirror>(sx);  // the 16 units of a row sit in one 16-lane row
+            if (c == 0) off_lds[buf][m] = -kCodeOffset * sx;
+          } else {
+            // a group is cg consecutive sub-steps = 4 * cg consecutive units
+            sx = sum4(sx);
+            if (cg == 2) sx += dpp_f32<kRowHalfMirror>(sx);
+            if ((c & (4 * cg - 1)) == 0)
+              off_lds[buf][(t / cg) * kTileRows + m] = -kCodeOffset * sx;
+          }
+        }
       }
     }
   };
@@ -400,88 +480,134 @@ w4a16_gemm_kernel(const GemmArgs g) {
         tot[mi][nt][ms] = zero4;
         acc[mi][nt][ms] = zero4;
       }
-  f32x4_t offacc[kSub];
-#pragma unroll
-  for (int ms = 0; ms < kSub; ++ms) offacc[ms] = zero4;
 
-  auto correct = [&](const f32x4_t (&o)[kSub], const WeightStep<MATS, NT, WIDE>& ws, int t) {
-#pragma unroll
-    for (int mi = 0; mi < MATS; ++mi)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const float sc = bf16_to_f32(ws.s[mi][nt][t]);
-#pragma unroll
-        for (int ms = 0; ms < kSub; ++ms)
-          if (ms < mt_act) {
-            tot[mi][nt][ms] += sc * (acc[mi][nt][ms] - o[ms]);
-            acc[mi][nt][ms] = zero4;
-          }
-      }
-  };
-
-  WeightStep<MATS, NT, WIDE> wcur, wnext;
-  wcur.load(wrow, srow, 0, jq, K, g.group);
+  WeightStep<FMT, MATS, NT, WIDE> w0, w1, w2;
+  w0.load(wrow, srow, 0, jq, K, g.group);
+  if (ksteps > 1) w1.load(wrow, srow, 1, jq, K, g.group);
   load_a(0);
   commit_a(0);
   __syncthreads();
-  const int cg = static_cast<int>(g.group / 32);  // MFMAs per group (narrow groups)
   for (int step = 0; step < ksteps; ++step) {
     const int buf = step & 1;
     const bool more = step + 1 < ksteps;
-    if (more) {
-      wnext.load(wrow, srow, step + 1, jq, K, g.group);
-      load_a(step + 1);
-    }
+    if (step + 2 < ksteps) w2.load(wrow, srow, step + 2, jq, K, g.group);
+    if (more) load_a(step + 1);
+
+    if constexpr (kMx) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      if (!WIDE && static_cast<int64_t>(step) * 128 + 32 * t >= K) break;
-      bf16x8_t af[kSub];
+      for (int t = 0; t < 4; ++t) {
+        if (static_cast<int64_t>(step) * 128 + 32 * t >= K) break;
+        u32x4_t af[kSub];
 #pragma unroll
-      for (int ms = 0; ms < kSub; ++ms)
-        if (ms < mt_act)
-          af[ms] = __builtin_bit_cast(
-              bf16x8_t, a_lds[buf][(ms * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
-#pragma unroll
-      for (int mi = 0; mi < MATS; ++mi)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const bf16x8_t bv = unpack_q8(wcur.w[mi][nt][t]);
-#pragma unroll
-          for (int ms = 0; ms < kSub; ++ms)
-            if (ms < mt_act)
-              acc[mi][nt][ms] =
-                  __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ms], bv, acc[mi][nt][ms], 0, 0, 0);
-        }
-      if constexpr (!WIDE) {
-        if ((t + 1) % cg == 0) {
-          f32x4_t o[kSub];
-#pragma unroll
-          for (int ms = 0; ms < kSub; ++ms) {
-            o[ms] = zero4;
-            if (ms < mt_act)
-              for (int tt = t + 1 - cg; tt <= t; ++tt)
-                o[ms] += *reinterpret_cast<const f32x4_t*>(
-                    &off_lds[buf][tt * kTileRows + ms * 16 + jq * 4]);
+        for (int ms = 0; ms < kSub; ++ms)
+          if (ms < mt_act) {
+            const uint4 q = a_lds[buf][(ms * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))];
+            af[ms] = u32x4_t{q.x, q.y, q.z, q.w};
           }
-          correct(o, wcur, t);
-        }
+#pragma unroll
+        for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            const float sc = e8m0_to_f32(w0.s[mi][nt][t]);
+            if constexpr (FMT == kFmtMxBf16) {
+              const bf16x8_t bv =
+                  __builtin_bit_cast(bf16x8_t, unpack_fp4x8_bf16(w0.w[mi][nt][t], sc));
+#pragma unroll
+              for (int ms = 0; ms < kSub; ++ms)
+                if (ms < mt_act)
+                  tot[mi][nt][ms] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                      __builtin_bit_cast(bf16x8_t, af[ms]), bv, tot[mi][nt][ms], 0, 0, 0);
+            } else {
+              const f16x8_t bv =
+                  __builtin_bit_cast(f16x8_t, unpack_fp4x8_f16(w0.w[mi][nt][t], sc));
+#pragma unroll
+              for (int ms = 0; ms < kSub; ++ms)
+                if (ms < mt_act)
+                  tot[mi][nt][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                      __builtin_bit_cast(f16x8_t, af[ms]), bv, tot[mi][nt][ms], 0, 0, 0);
+            }
+          }
       }
-    }
-    if constexpr (WIDE) {
+    } else if constexpr (WIDE) {
+      const bool first = (static_cast<int64_t>(step) * 128) % g.group == 0;
+      const bool last = (static_cast<int64_t>(step + 1) * 128) % g.group == 0;
+      f32x4_t neg[kSub];
 #pragma unroll
       for (int ms = 0; ms < kSub; ++ms)
-        if (ms < mt_act)
-          offacc[ms] += *reinterpret_cast<const f32x4_t*>(&off_lds[buf][ms * 16 + jq * 4]);
-      if ((static_cast<int64_t>(step + 1) * 128) % g.group == 0) {
-        correct(offacc, wcur, 0);
+        neg[ms] = ms < mt_act ? *reinterpret_cast<const f32x4_t*>(&off_lds[buf][ms * 16 + jq * 4])
+                              : zero4;
 #pragma unroll
-        for (int ms = 0; ms < kSub; ++ms) offacc[ms] = zero4;
+      for (int t = 0; t < 4; ++t) {
+        bf16x8_t af[kSub];
+#pragma unroll
+        for (int ms = 0; ms < kSub; ++ms)
+          if (ms < mt_act)
+            af[ms] = __builtin_bit_cast(
+                bf16x8_t, a_lds[buf][(ms * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
+#pragma unroll
+        for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            const bf16x8_t bv = unpack_q8(w0.w[mi][nt][t]);
+#pragma unroll
+            for (int ms = 0; ms < kSub; ++ms)
+              if (ms < mt_act) {
+                // G > 128: later steps of a group continue its chain plus their offset
+                const f32x4_t c = t > 0 ? acc[mi][nt][ms]
+                                        : (first ? neg[ms] : acc[mi][nt][ms] + neg[ms]);
+                acc[mi][nt][ms] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ms], bv, c, 0, 0, 0);
+              }
+          }
+      }
+      if (last) {
+#pragma unroll
+        for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            const float sc = bf16_to_f32(static_cast<uint16_t>(w0.s[mi][nt][0]));
+#pragma unroll
+            for (int ms = 0; ms < kSub; ++ms)
+              if (ms < mt_act) tot[mi][nt][ms] += sc * acc[mi][nt][ms];
+          }
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (static_cast<int64_t>(step) * 128 + 32 * t >= K) break;
+        const bool first = (t % cg) == 0;
+        const bool last = ((t + 1) % cg) == 0;
+        bf16x8_t af[kSub];
+        f32x4_t neg[kSub];
+#pragma unroll
+        for (int ms = 0; ms < kSub; ++ms) {
+          neg[ms] = zero4;
+          if (ms < mt_act) {
+            af[ms] = __builtin_bit_cast(
+                bf16x8_t, a_lds[buf][(ms * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
+            if (first)
+              neg[ms] = *reinterpret_cast<const f32x4_t*>(
+                  &off_lds[buf][(t / cg) * kTileRows + ms * 16 + jq * 4]);
+          }
+        }
+#pragma unroll
+        for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            const bf16x8_t bv = unpack_q8(w0.w[mi][nt][t]);
+            const float sc = bf16_to_f32(static_cast<uint16_t>(w0.s[mi][nt][t]));
+#pragma unroll
+            for (int ms = 0; ms < kSub; ++ms)
+              if (ms < mt_act) {
+                const f32x4_t c = first ? neg[ms] : acc[mi][nt][ms];
+                acc[mi][nt][ms] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ms], bv, c, 0, 0, 0);
+                if (last) tot[mi][nt][ms] += sc * acc[mi][nt][ms];
+              }
+          }
       }
     }
-    if (more) {
-      commit_a(buf ^ 1);
-      wcur = wnext;
-    }
+    if (more) commit_a(buf ^ 1);
+    w0 = w1;
+    w1 = w2;
     __syncthreads();
   }
 
@@ -497,8 +623,16 @@ w4a16_gemm_kernel(const GemmArgs g) {
       for (int nt = 0; nt < NT; ++nt) {
         if (col[nt] >= N) continue;
         uint16_t v;
-        if constexpr (MATS == 2) v = swiglu_bf16(tot[0][nt][ms][i], tot[1][nt][ms][i]);
-        else v = f32_to_bf16(tot[0][nt][ms][i]);
+        if constexpr (MATS == 2) {
+          v = g.act == kActSitu
+                  ? situ_bf16(tot[0][nt][ms][i], tot[1][nt][ms][i], g.situ_beta,
+                              g.situ_linear_beta)
+                  : swiglu_bf16(tot[0][nt][ms][i], tot[1][nt][ms][i]);
+        } else if constexpr (FMT == kFmtMxF16) {
+          v = __builtin_bit_cast(uint16_t, static_cast<_Float16>(tot[0][nt][ms][i]));
+        } else {
+          v = f32_to_bf16(tot[0][nt][ms][i]);
+        }
         out[orow * N + col[nt]] = v;
       }
     }
@@ -618,46 +752,63 @@ int schedule_launch(const RouteTable& rt, int64_t entries, char* ws, const Sched
 
 enum class Mode { Gather, Scatter, GatherScatter, Dense };
 
-template <int MATS, int NT, bool WIDE>
+template <int FMT, int MATS, int NT, bool WIDE>
 void gemm_dispatch_mode(const GemmArgs& g, Mode mode, unsigned blocks, hipStream_t s) {
-  constexpr int W = 4;
-  switch (mode) {
-    case Mode::Gather:
-      w4a16_gemm_kernel<MATS, NT, W, WIDE, true, false, false><<<blocks, W * kWave, 0, s>>>(g);
-      break;
-    case Mode::Scatter:
-      w4a16_gemm_kernel<MATS, NT, W, WIDE, false, true, false><<<blocks, W * kWave, 0, s>>>(g);
-      break;
-    case Mode::GatherScatter:
-      w4a16_gemm_kernel<MATS, NT, W, WIDE, true, true, false><<<blocks, W * kWave, 0, s>>>(g);
-      break;
-    case Mode::Dense:
-      w4a16_gemm_kernel<MATS, NT, W, WIDE, false, false, true><<<blocks, W * kWave, 0, s>>>(g);
-      break;
+  constexpr int T = kGemmWaves * kWave;
+  if constexpr (FMT == kFmtMxF16) {  // fp16 activations: the plain MXFP4 GEMM only
+    w4a16_gemm_kernel<FMT, MATS, NT, false, false, false, true><<<blocks, T, 0, s>>>(g);
+    return;
+  } else {
+    switch (mode) {
+      case Mode::Gather:
+        w4a16_gemm_kernel<FMT, MATS, NT, WIDE, true, false, false><<<blocks, T, 0, s>>>(g);
+        break;
+      case Mode::Scatter:
+        w4a16_gemm_kernel<FMT, MATS, NT, WIDE, false, true, false><<<blocks, T, 0, s>>>(g);
+        break;
+      case Mode::GatherScatter:
+        w4a16_gemm_kernel<FMT, MATS, NT, WIDE, true, true, false><<<blocks, T, 0, s>>>(g);
+        break;
+      case Mode::Dense:
+        w4a16_gemm_kernel<FMT, MATS, NT, WIDE, false, false, true><<<blocks, T, 0, s>>>(g);
+        break;
+    }
   }
 }
 
 // Launches the GEMM over `tiles` row tiles (an upper bound in schedule
 // modes); `wide_cols` picks two 16-column tiles per wave.
-template <int MATS>
+template <int FMT, int MATS>
 int gemm_launch(GemmArgs g, Mode mode, int64_t tiles, bool wide_cols, hipStream_t s,
                 const char* what) {
-  LK_REQUIRE(g.k % 32 == 0 && g.group % 32 == 0 && (g.group & (g.group - 1)) == 0,
-             "%s: unsupported reduction width / group size", what);
-  const bool wide = g.group >= 128;
+  if constexpr (FMT == kFmtW4A16) {
+    LK_REQUIRE(g.k % 32 == 0 && g.group % 32 == 0 && (g.group & (g.group - 1)) == 0,
+               "%s: unsupported reduction width / group size", what);
+  } else {
+    LK_REQUIRE(g.k % 32 == 0 && g.group == 32, "%s: MXFP4 needs k %% 32 == 0", what);
+    LK_REQUIRE(FMT != kFmtMxF16 || (mode == Mode::Dense && MATS == 1),
+               "%s: fp16 activations are supported by the plain MXFP4 GEMM only", what);
+  }
+  const bool wide = FMT == kFmtW4A16 && g.group >= 128;
+  wide_cols = wide_cols && MATS == 1;  // two matrices x two column tiles exceed 256 VGPRs
   const int nt = wide_cols ? 2 : 1;
-  const int bn = 4 * nt * 16;
+  const int bn = kGemmWaves * nt * 16;
   g.col_blocks = static_cast<int>((g.n + bn - 1) / bn);
   const int64_t groups8 = (tiles + 7) / 8;
   const int64_t blocks = groups8 * 8 * g.col_blocks * g.outputs;
   LK_REQUIRE(blocks > 0 && blocks < (1LL << 31), "%s: too many blocks", what);
   const unsigned nb = static_cast<unsigned>(blocks);
-  if (wide) {
-    if (wide_cols) gemm_dispatch_mode<MATS, 2, true>(g, mode, nb, s);
-    else gemm_dispatch_mode<MATS, 1, true>(g, mode, nb, s);
+  if constexpr (MATS == 1) {
+    if (wide) {
+      if (wide_cols) gemm_dispatch_mode<FMT, 1, 2, FMT == kFmtW4A16>(g, mode, nb, s);
+      else gemm_dispatch_mode<FMT, 1, 1, FMT == kFmtW4A16>(g, mode, nb, s);
+    } else {
+      if (wide_cols) gemm_dispatch_mode<FMT, 1, 2, false>(g, mode, nb, s);
+      else gemm_dispatch_mode<FMT, 1, 1, false>(g, mode, nb, s);
+    }
   } else {
-    if (wide_cols) gemm_dispatch_mode<MATS, 2, false>(g, mode, nb, s);
-    else gemm_dispatch_mode<MATS, 1, false>(g, mode, nb, s);
+    if (wide) gemm_dispatch_mode<FMT, MATS, 1, FMT == kFmtW4A16>(g, mode, nb, s);
+    else gemm_dispatch_mode<FMT, MATS, 1, false>(g, mode, nb, s);
   }
   return check_launch(what);
 }
@@ -671,6 +822,34 @@ int check_schedule_dims(int64_t tokens, int64_t routes, int64_t experts) {
   LK_REQUIRE(tokens >= 0 && routes > 0, "invalid route table dimensions");
   LK_REQUIRE(tokens * routes < (1LL << 30), "too many token-routes for one call");
   return LK_OK;
+}
+
+template <int MATS>
+int launch_fmt(bool mx, const GemmArgs& g, Mode mode, int64_t tiles, bool wide_cols,
+                      hipStream_t s, const char* what) {
+  if (mx) return gemm_launch<kFmtMxBf16, MATS>(g, mode, tiles, wide_cols, s, what);
+  return gemm_launch<kFmtW4A16, MATS>(g, mode, tiles, wide_cols, s, what);
+}
+
+// W4A16: a power-of-two group (multiple of 32) dividing k; MXFP4: 32.
+int check_format(bool mx, int64_t k, int64_t group) {
+  if (mx) {
+    LK_REQUIRE(k > 0 && k % 32 == 0, "MXFP4 reduction dimension must be divisible by 32");
+    return LK_OK;
+  }
+  return check_pow2_group(k, group);
+}
+
+void dense_args(GemmArgs& g, const uint16_t* x, int64_t m, int64_t n, int64_t k,
+                       int64_t group) {
+  g.a = x;
+  g.n = n;
+  g.k = k;
+  g.group = group;
+  g.routes = 1;
+  g.dense_rows = static_cast<int>(m);
+  g.outputs = 1;
+  g.act = kActSwiglu;
 }
 
 }  // namespace
@@ -722,16 +901,16 @@ int64_t lk_w4a16_grouped_gemm_workspace(int64_t tokens, int64_t routes, int64_t 
   return static_cast<int64_t>(moe_layout(tokens * routes, experts, 0, 0).total);
 }
 
-static int grouped_gemm_common(const uint16_t* x, const int64_t* idx, const uint8_t* p0,
-                               const uint16_t* s0, const uint8_t* p1, const uint16_t* s1,
-                               uint16_t* out, int64_t tokens, int64_t routes, int64_t experts,
-                               int64_t n, int64_t k, int64_t group, void* workspace,
+static int grouped_gemm_common(bool mx, const uint16_t* x, const int64_t* idx, const uint8_t* p0,
+                               const void* s0, const uint8_t* p1, const void* s1, uint16_t* out,
+                               int64_t tokens, int64_t routes, int64_t experts, int64_t n,
+                               int64_t k, int64_t group, void* workspace,
                                int64_t workspace_bytes, void* stream, bool swiglu,
                                const char* name) {
   LK_REQUIRE(p0 && s0 && out && (!swiglu || (p1 && s1)), "null pointer argument");
   LK_REQUIRE(routes > 0 && experts > 0 && n > 0 && tokens >= 0,
-             "grouped W4A16 requires nonzero dimensions");
-  if (int rc = check_pow2_group(k, group)) return rc;
+             "%s requires nonzero dimensions", name);
+  if (int rc = check_format(mx, k, group)) return rc;
   if (int rc = check_schedule_dims(tokens, routes, experts)) return rc;
   if (tokens == 0) return LK_OK;
   LK_REQUIRE(x && idx && workspace, "null pointer argument");
@@ -762,15 +941,15 @@ static int grouped_gemm_common(const uint16_t* x, const int64_t* idx, const uint
   g.out[0] = g.out[1] = g.out[2] = out;
   g.n = n;
   g.k = k;
-  g.group = group;
+  g.group = mx ? 32 : group;
   g.wstride = n * k / 2;
-  g.sstride = n * (k / group);
+  g.sstride = n * (k / g.group);
   g.routes = routes;
   g.outputs = 1;
+  g.act = kActSwiglu;
   const bool wc = wide_cols_for(l.sched.max_tiles, n);
-  if (swiglu)
-    return gemm_launch<2>(g, Mode::GatherScatter, l.sched.max_tiles, wc, s, name);
-  return gemm_launch<1>(g, Mode::GatherScatter, l.sched.max_tiles, wc, s, name);
+  if (swiglu) return launch_fmt<2>(mx, g, Mode::GatherScatter, l.sched.max_tiles, wc, s, name);
+  return launch_fmt<1>(mx, g, Mode::GatherScatter, l.sched.max_tiles, wc, s, name);
 }
 
 int lk_w4a16_grouped_gemm(const uint16_t* x, const int64_t* expert_indices,
@@ -778,9 +957,9 @@ int lk_w4a16_grouped_gemm(const uint16_t* x, const int64_t* expert_indices,
                           int64_t tokens, int64_t routes, int64_t experts, int64_t n, int64_t k,
                           int64_t group_size, void* workspace, int64_t workspace_bytes,
                           void* stream) {
-  return grouped_gemm_common(x, expert_indices, packed, scales, nullptr, nullptr, out, tokens,
-                             routes, experts, n, k, group_size, workspace, workspace_bytes,
-                             stream, false, "lk_w4a16_grouped_gemm");
+  return grouped_gemm_common(false, x, expert_indices, packed, scales, nullptr, nullptr, out,
+                             tokens, routes, experts, n, k, group_size, workspace,
+                             workspace_bytes, stream, false, "lk_w4a16_grouped_gemm");
 }
 
 int lk_w4a16_swiglu_gemm(const uint16_t* x, const int64_t* expert_indices,
@@ -789,9 +968,28 @@ int lk_w4a16_swiglu_gemm(const uint16_t* x, const int64_t* expert_indices,
                          int64_t tokens, int64_t routes, int64_t experts, int64_t n, int64_t k,
                          int64_t group_size, void* workspace, int64_t workspace_bytes,
                          void* stream) {
-  return grouped_gemm_common(x, expert_indices, w1_packed, w1_scales, w3_packed, w3_scales, out,
-                             tokens, routes, experts, n, k, group_size, workspace,
+  return grouped_gemm_common(false, x, expert_indices, w1_packed, w1_scales, w3_packed,
+                             w3_scales, out, tokens, routes, experts, n, k, group_size, workspace,
                              workspace_bytes, stream, true, "lk_w4a16_swiglu_gemm");
+}
+
+int lk_mxfp4_grouped_gemm(const uint16_t* x, const int64_t* expert_indices,
+                          const uint8_t* packed, const uint8_t* scale, uint16_t* out,
+                          int64_t tokens, int64_t routes, int64_t experts, int64_t n, int64_t k,
+                          void* workspace, int64_t workspace_bytes, void* stream) {
+  return grouped_gemm_common(true, x, expert_indices, packed, scale, nullptr, nullptr, out,
+                             tokens, routes, experts, n, k, 32, workspace, workspace_bytes,
+                             stream, false, "lk_mxfp4_grouped_gemm");
+}
+
+int lk_mxfp4_swiglu_gemm(const uint16_t* x, const int64_t* expert_indices,
+                         const uint8_t* w1_packed, const uint8_t* w1_scale,
+                         const uint8_t* w3_packed, const uint8_t* w3_scale, uint16_t* out,
+                         int64_t tokens, int64_t routes, int64_t experts, int64_t n, int64_t k,
+                         void* workspace, int64_t workspace_bytes, void* stream) {
+  return grouped_gemm_common(true, x, expert_indices, w1_packed, w1_scale, w3_packed, w3_scale,
+                             out, tokens, routes, experts, n, k, 32, workspace, workspace_bytes,
+                             stream, true, "lk_mxfp4_swiglu_gemm");
 }
 
 int lk_w4a16_dense_gemm(const uint16_t* x, const uint8_t* packed, const uint16_t* scales,
@@ -805,19 +1003,74 @@ int lk_w4a16_dense_gemm(const uint16_t* x, const uint8_t* packed, const uint16_t
   LK_REQUIRE(x != nullptr, "null activation pointer");
   LK_REQUIRE(m < (1LL << 30), "too many rows");
   GemmArgs g{};
-  g.a = x;
+  dense_args(g, x, m, n, k, group_size);
   g.wp[0] = g.wp[1] = g.wp[2] = packed;
   g.ws[0] = g.ws[1] = g.ws[2] = scales;
   g.out[0] = g.out[1] = g.out[2] = y;
-  g.n = n;
-  g.k = k;
-  g.group = group_size;
-  g.routes = 1;
-  g.dense_rows = static_cast<int>(m);
-  g.outputs = 1;
   const int64_t tiles = (m + kTileRows - 1) / kTileRows;
-  return gemm_launch<1>(g, Mode::Dense, tiles, wide_cols_for(tiles, n), as_stream(stream),
-                        "lk_w4a16_dense_gemm");
+  return gemm_launch<kFmtW4A16, 1>(g, Mode::Dense, tiles, wide_cols_for(tiles, n),
+                                   as_stream(stream), "lk_w4a16_dense_gemm");
+}
+
+int lk_mxfp4_gemm(const uint16_t* x, const uint8_t* packed, const uint8_t* scale, uint16_t* y,
+                  int64_t m, int64_t n, int64_t k, int act_f16, void* stream) {
+  LK_REQUIRE(packed && scale && y, "null pointer argument");
+  LK_REQUIRE(m >= 0 && n > 0, "reduction and output dimensions must be nonzero");
+  if (int rc = check_format(true, k, 32)) return rc;
+  if (m == 0) return LK_OK;
+  LK_REQUIRE(x != nullptr, "null activation pointer");
+  LK_REQUIRE(m < (1LL << 30), "too many rows");
+  GemmArgs g{};
+  dense_args(g, x, m, n, k, 32);
+  g.wp[0] = g.wp[1] = g.wp[2] = packed;
+  g.ws[0] = g.ws[1] = g.ws[2] = scale;
+  g.out[0] = g.out[1] = g.out[2] = y;
+  const int64_t tiles = (m + kTileRows - 1) / kTileRows;
+  if (act_f16)
+    return gemm_launch<kFmtMxF16, 1>(g, Mode::Dense, tiles, wide_cols_for(tiles, n),
+                                     as_stream(stream), "lk_mxfp4_gemm");
+  return gemm_launch<kFmtMxBf16, 1>(g, Mode::Dense, tiles, wide_cols_for(tiles, n),
+                                    as_stream(stream), "lk_mxfp4_gemm");
+}
+
+int lk_mxfp4_expert_mlp(const uint16_t* x, const uint8_t* w1_packed, const uint8_t* w1_scale,
+                        const uint8_t* w3_packed, const uint8_t* w3_scale,
+                        const uint8_t* w2_packed, const uint8_t* w2_scale, uint16_t* y,
+                        uint16_t* activated, int64_t m, int64_t h, int64_t i, float situ_beta,
+                        float situ_linear_beta, void* stream) {
+  LK_REQUIRE(w1_packed && w1_scale && w3_packed && w3_scale && w2_packed && w2_scale && y &&
+                 activated,
+             "null pointer argument");
+  LK_REQUIRE(m >= 0 && h > 0 && i > 0, "invalid expert dimensions");
+  if (int rc = check_format(true, h, 32)) return rc;
+  if (int rc = check_format(true, i, 32)) return rc;
+  LK_REQUIRE(situ_beta != 0.f, "SiTU beta must be nonzero");
+  if (m == 0) return LK_OK;
+  LK_REQUIRE(x != nullptr, "null activation pointer");
+  LK_REQUIRE(m < (1LL << 30), "too many rows");
+  hipStream_t s = as_stream(stream);
+  const int64_t tiles = (m + kTileRows - 1) / kTileRows;
+  GemmArgs g{};
+  dense_args(g, x, m, i, h, 32);
+  g.act = kActSitu;
+  g.situ_beta = situ_beta;
+  g.situ_linear_beta = situ_linear_beta;
+  g.wp[0] = w1_packed;
+  g.ws[0] = w1_scale;
+  g.wp[1] = w3_packed;
+  g.ws[1] = w3_scale;
+  g.wp[2] = w1_packed;
+  g.ws[2] = w1_scale;
+  g.out[0] = g.out[1] = g.out[2] = activated;
+  if (int rc = gemm_launch<kFmtMxBf16, 2>(g, Mode::Dense, tiles, false, s, "mxfp4 expert gate/up"))
+    return rc;
+  GemmArgs d{};
+  dense_args(d, activated, m, h, i, 32);
+  d.wp[0] = d.wp[1] = d.wp[2] = w2_packed;
+  d.ws[0] = d.ws[1] = d.ws[2] = w2_scale;
+  d.out[0] = d.out[1] = d.out[2] = y;
+  return gemm_launch<kFmtMxBf16, 1>(d, Mode::Dense, tiles, wide_cols_for(tiles, h), s,
+                                    "mxfp4 expert down");
 }
 
 int lk_w4a16_fused_qkv(const uint16_t* x, const uint8_t* q_packed, const uint16_t* q_scales,
@@ -841,7 +1094,7 @@ int lk_w4a16_fused_qkv(const uint16_t* x, const uint8_t* q_packed, const uint16_
   }
   LK_REQUIRE(m < (1LL << 30), "too many rows");
   GemmArgs g{};
-  g.a = x;
+  dense_args(g, x, m, n, k, group_size);
   g.wp[0] = q_packed;
   g.wp[1] = k_packed;
   g.wp[2] = v_packed;
@@ -851,15 +1104,10 @@ int lk_w4a16_fused_qkv(const uint16_t* x, const uint8_t* q_packed, const uint16_
   g.out[0] = q;
   g.out[1] = k_out;
   g.out[2] = v;
-  g.n = n;
-  g.k = k;
-  g.group = group_size;
-  g.routes = 1;
-  g.dense_rows = static_cast<int>(m);
   g.outputs = 3;
   const int64_t tiles = (m + kTileRows - 1) / kTileRows;
-  return gemm_launch<1>(g, Mode::Dense, tiles, wide_cols_for(3 * tiles, n), as_stream(stream),
-                        "lk_w4a16_fused_qkv");
+  return gemm_launch<kFmtW4A16, 1>(g, Mode::Dense, tiles, wide_cols_for(3 * tiles, n),
+                                   as_stream(stream), "lk_w4a16_fused_qkv");
 }
 
 int64_t lk_w4a16_moe_forward_workspace(int64_t tokens, int64_t experts, int64_t h, int64_t i,
@@ -869,14 +1117,14 @@ int64_t lk_w4a16_moe_forward_workspace(int64_t tokens, int64_t experts, int64_t 
   return static_cast<int64_t>(moe_layout(tokens * (top_k + 1), experts, i, h).total);
 }
 
-int lk_w4a16_moe_forward(const uint16_t* x, const float* logits, const float* bias,
-                         const uint8_t* w1_packed, const uint16_t* w1_scales,
-                         const uint8_t* w3_packed, const uint16_t* w3_scales,
-                         const uint8_t* w2_packed, const uint16_t* w2_scales, uint16_t* y,
-                         int64_t* expert_indices, float* weights, void* workspace,
-                         int64_t workspace_bytes, int64_t tokens, int64_t experts, int64_t h,
-                         int64_t i, int64_t top_k, float routed_scaling_factor, int renormalize,
-                         int64_t group_size, void* stream) {
+static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, const float* bias,
+                              const uint8_t* w1_packed, const void* w1_scales,
+                              const uint8_t* w3_packed, const void* w3_scales,
+                              const uint8_t* w2_packed, const void* w2_scales, uint16_t* y,
+                              int64_t* expert_indices, float* weights, void* workspace,
+                              int64_t workspace_bytes, int64_t tokens, int64_t experts,
+                              int64_t h, int64_t i, int64_t top_k, float routed_scaling_factor,
+                              int renormalize, int64_t group_size, void* stream) {
   LK_REQUIRE(w1_packed && w1_scales && w3_packed && w3_scales && w2_packed && w2_scales && y &&
                  expert_indices && weights,
              "null pointer argument");
@@ -885,8 +1133,8 @@ int lk_w4a16_moe_forward(const uint16_t* x, const float* logits, const float* bi
              (long long)top_k);
   LK_REQUIRE(h > 0 && i > 0 && tokens >= 0, "invalid dimensions");
   LK_REQUIRE(h % 8 == 0, "hidden size must be a multiple of 8, got %lld", (long long)h);
-  if (int rc = check_pow2_group(h, group_size)) return rc;
-  if (int rc = check_pow2_group(i, group_size)) return rc;
+  if (int rc = check_format(mx, h, group_size)) return rc;
+  if (int rc = check_format(mx, i, group_size)) return rc;
   if (int rc = check_schedule_dims(tokens, top_k + 1, experts)) return rc;
   if (tokens == 0) return LK_OK;
   LK_REQUIRE(x && logits && workspace, "null pointer argument");
@@ -910,13 +1158,15 @@ int lk_w4a16_moe_forward(const uint16_t* x, const float* logits, const float* bi
   const RouteTable rt{expert_indices, top_k, routes, experts, experts - 1};
   if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, s)) return rc;
 
+  const int64_t group = mx ? 32 : group_size;
   GemmArgs g{};
   g.perm = perm;
   g.tiles = tiles;
   g.tile_count = count;
-  g.group = group_size;
+  g.group = group;
   g.routes = routes;
   g.outputs = 1;
+  g.act = kActSwiglu;
   // gate/up + SwiGLU: rows gathered from x, activations written in sorted order
   g.a = x;
   g.wp[0] = w1_packed;
@@ -929,9 +1179,9 @@ int lk_w4a16_moe_forward(const uint16_t* x, const float* logits, const float* bi
   g.n = i;
   g.k = h;
   g.wstride = i * h / 2;
-  g.sstride = i * (h / group_size);
+  g.sstride = i * (h / group);
   const int64_t mt = l.sched.max_tiles;
-  if (int rc = gemm_launch<2>(g, Mode::Gather, mt, wide_cols_for(mt, i), s, "moe gate/up gemm"))
+  if (int rc = launch_fmt<2>(mx, g, Mode::Gather, mt, wide_cols_for(mt, i), s, "moe gate/up gemm"))
     return rc;
   // down projection: sorted activation rows, outputs scattered to (token, route) rows
   g.a = act;
@@ -941,13 +1191,41 @@ int lk_w4a16_moe_forward(const uint16_t* x, const float* logits, const float* bi
   g.n = h;
   g.k = i;
   g.wstride = h * i / 2;
-  g.sstride = h * (i / group_size);
-  if (int rc = gemm_launch<1>(g, Mode::Scatter, mt, wide_cols_for(mt, h), s, "moe down gemm"))
+  g.sstride = h * (i / group);
+  if (int rc = launch_fmt<1>(mx, g, Mode::Scatter, mt, wide_cols_for(mt, h), s, "moe down gemm"))
     return rc;
   const int64_t work = tokens * (h / 8);
   moe_combine_kernel<<<static_cast<unsigned>((work + 255) / 256), 256, 0, s>>>(
       eo, weights, y, tokens, static_cast<int>(top_k), h);
   return check_launch("moe combine");
+}
+
+int lk_w4a16_moe_forward(const uint16_t* x, const float* logits, const float* bias,
+                         const uint8_t* w1_packed, const uint16_t* w1_scales,
+                         const uint8_t* w3_packed, const uint16_t* w3_scales,
+                         const uint8_t* w2_packed, const uint16_t* w2_scales, uint16_t* y,
+                         int64_t* expert_indices, float* weights, void* workspace,
+                         int64_t workspace_bytes, int64_t tokens, int64_t experts, int64_t h,
+                         int64_t i, int64_t top_k, float routed_scaling_factor, int renormalize,
+                         int64_t group_size, void* stream) {
+  return moe_forward_common(false, x, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
+                            w2_packed, w2_scales, y, expert_indices, weights, workspace,
+                            workspace_bytes, tokens, experts, h, i, top_k, routed_scaling_factor,
+                            renormalize, group_size, stream);
+}
+
+int lk_mxfp4_moe_forward(const uint16_t* x, const float* logits, const float* bias,
+                         const uint8_t* w1_packed, const uint8_t* w1_scale,
+                         const uint8_t* w3_packed, const uint8_t* w3_scale,
+                         const uint8_t* w2_packed, const uint8_t* w2_scale, uint16_t* y,
+                         int64_t* expert_indices, float* weights, void* workspace,
+                         int64_t workspace_bytes, int64_t tokens, int64_t experts, int64_t h,
+                         int64_t i, int64_t top_k, float routed_scaling_factor, int renormalize,
+                         void* stream) {
+  return moe_forward_common(true, x, logits, bias, w1_packed, w1_scale, w3_packed, w3_scale,
+                            w2_packed, w2_scale, y, expert_indices, weights, workspace,
+                            workspace_bytes, tokens, experts, h, i, top_k, routed_scaling_factor,
+                            renormalize, 32, stream);
 }
 
 }  // extern "C"

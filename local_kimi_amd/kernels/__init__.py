@@ -20,6 +20,9 @@ from . import registry
 from .moe import (moe_router, moe_schedule, shape_stable_expert_indices, w4a16_moe_block,
                   w4a16_moe_block_reference, w4a16_moe_decode, w4a16_moe_forward,
                   w4a16_moe_gateup)
+from .mxfp4 import (grouped_mxfp4_gemm, grouped_mxfp4_reference, grouped_mxfp4_swiglu_gemm,
+                    mxfp4_expert_mlp, mxfp4_gemm, mxfp4_gemm_reference, mxfp4_linear,
+                    mxfp4_moe_block, mxfp4_moe_block_reference)
 from .w4a16 import (fused_qkv_w4a16, fused_qkv_w4a16_reference, fused_w2_combine,
                     fused_w2_combine_reference, grouped_w4a16_gemm, grouped_w4a16_gemv,
                     grouped_w4a16_reference, grouped_w4a16_swiglu_gemm,
@@ -32,6 +35,9 @@ W4A16_SWIGLU = "w4a16_swiglu"
 W4A16_FUSED_QKV = "w4a16_fused_qkv"
 W4A16_W2_COMBINE = "w4a16_w2_combine"
 W4A16_MOE_BLOCK = "w4a16_moe_block"
+MXFP4_GEMM = "mxfp4_gemm"
+MXFP4_GROUPED = "mxfp4_grouped"
+MXFP4_MOE_BLOCK = "mxfp4_moe_block"
 
 HIP = "hip"
 REFERENCE = "reference"
@@ -103,10 +109,35 @@ def _register_others() -> None:
     registry.set_default(W4A16_MOE_BLOCK, HIP)
 
 
+def _register_mxfp4() -> None:
+    registry.register(MXFP4_GEMM, REFERENCE, reference=True, requires_cuda=True,
+                      description="Each weight decoded to the activation dtype, fp32 dot per "
+                      "output.")(mxfp4_gemm_reference)
+    registry.register(MXFP4_GEMM, HIP, requires_cuda=True,
+                      description="Scaled fp4 decode into bf16/fp16 MFMA tiles.")(mxfp4_gemm)
+    registry.set_default(MXFP4_GEMM, HIP)
+
+    registry.register(MXFP4_GROUPED, REFERENCE, reference=True, requires_cuda=True,
+                      description="Reference GEMM per expert over its gathered rows.")(
+        grouped_mxfp4_reference)
+    registry.register(MXFP4_GROUPED, HIP, requires_cuda=True,
+                      description="Expert-sorted schedule + MFMA GEMM.")(grouped_mxfp4_gemm)
+    registry.set_default(MXFP4_GROUPED, HIP)
+
+    registry.register(MXFP4_MOE_BLOCK, REFERENCE, reference=True, requires_cuda=True,
+                      description="Router, reference grouped GEMMs, silu*up, combine.")(
+        mxfp4_moe_block_reference)
+    registry.register(MXFP4_MOE_BLOCK, HIP, requires_cuda=True,
+                      description="Router, schedule, gate/up + SwiGLU GEMM, down GEMM, "
+                      "combine.")(mxfp4_moe_block)
+    registry.set_default(MXFP4_MOE_BLOCK, HIP)
+
+
 _register_grouped()
 _register_dense()
 _register_swiglu()
 _register_others()
+_register_mxfp4()
 
 __all__ = [
     "registry", "W4A16_GROUPED", "W4A16_DENSE", "W4A16_SWIGLU", "W4A16_FUSED_QKV",
@@ -115,4 +146,8 @@ __all__ = [
     "moe_schedule", "w4a16_dense", "w4a16_dense_gemm", "grouped_w4a16_gemv",
     "grouped_w4a16_gemm", "grouped_w4a16_swiglu_gemv", "grouped_w4a16_swiglu_gemm",
     "fused_w2_combine", "fused_qkv_w4a16", "route_combine", "silu_mul",
+    "MXFP4_GEMM", "MXFP4_GROUPED", "MXFP4_MOE_BLOCK", "mxfp4_gemm", "mxfp4_linear",
+    "mxfp4_gemm_reference", "grouped_mxfp4_gemm", "grouped_mxfp4_swiglu_gemm",
+    "grouped_mxfp4_reference", "mxfp4_moe_block", "mxfp4_moe_block_reference",
+    "mxfp4_expert_mlp",
 ]

@@ -94,3 +94,90 @@ def linear(x_bits: np.ndarray, packed: np.ndarray, scale: np.ndarray) -> np.ndar
     x = bf16_bits_to_f32(x_bits)
     acc = x.astype(np.float64) @ w.astype(np.float64).T
     return f32_to_bf16_bits(acc.astype(np.float32))
+
+
+def linear_f16(x_f16_bits: np.ndarray, packed: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """The same linear with fp16 activations: the decoded weight cast to fp16
+    (kernels/reference.py:75-80 with ``dtype=float16``), float64 accumulation,
+    fp16 output bits."""
+    w = dequantize(packed, scale).astype(np.float16).astype(np.float64)
+    x = np.asarray(x_f16_bits, dtype=np.uint16).view(np.float16).astype(np.float64)
+    return (x @ w.T).astype(np.float16).view(np.uint16)
+
+
+def grouped(x_bits, expert_indices, packed_bank, scale_bank) -> np.ndarray:
+    """``out[t, r] = linear(x[t], expert idx[t, r])`` -> bf16 bits ``[T, R, N]``.
+
+    The per-route evaluation of kernels/reference.py:119-165 with
+    ``mxfp4_linear_reference`` as the expert function.
+    """
+    x = np.asarray(x_bits)
+    idx = np.asarray(expert_indices, dtype=np.int64)
+    t_count, r_count = idx.shape
+    n = packed_bank.shape[1]
+    out = np.empty((t_count, r_count, n), dtype=np.uint16)
+    cache: dict[int, np.ndarray] = {}
+    for t in range(t_count):
+        for r in range(r_count):
+            e = int(idx[t, r])
+            if e not in cache:
+                cache[e] = bf16_bits_to_f32(f32_to_bf16_bits(dequantize(packed_bank[e], scale_bank[e])))
+            acc = bf16_bits_to_f32(x[t:t + 1]).astype(np.float64) @ cache[e].astype(np.float64).T
+            out[t, r] = f32_to_bf16_bits(acc.astype(np.float32))[0]
+    return out
+
+
+def swiglu(x_bits, expert_indices, w1_packed, w1_scale, w3_packed, w3_scale) -> np.ndarray:
+    """``bf16(bf16(silu(gate)) * up)`` with MXFP4 gate / up projections (the
+    SwiGLU contract of engine/kernels/__init__.py:182-197)."""
+    from .w4a16 import mul_bf16, silu_bf16
+
+    gate = grouped(x_bits, expert_indices, w1_packed, w1_scale)
+    up = grouped(x_bits, expert_indices, w3_packed, w3_scale)
+    return mul_bf16(silu_bf16(gate), up)
+
+
+def moe_block(x_bits, logits, bias, w1_packed, w1_scale, w3_packed, w3_scale, w2_packed,
+              w2_scale, *, top_k: int, routed_scaling_factor: float, renormalize: bool = True):
+    """The Kimi-Linear grouped MoE block (klinear/moe.py:278-334, 375-398) with
+    MXFP4 expert banks: route, shared expert appended as the last bank entry,
+    SwiGLU, W2 per route, fp32 weighted sum -> bf16, + shared expert (bf16).
+    Returns ``(y bf16 bits [T, H], idx [T, k], w [T, k])``."""
+    from . import moe as OM
+
+    num_routed = w1_packed.shape[0] - 1
+    idx, w = OM.route(logits, bias, top_k, routed_scaling_factor=routed_scaling_factor,
+                      renormalize=renormalize)
+    stable = OM.shape_stable_expert_indices(idx, num_routed)
+    act = swiglu(x_bits, stable, w1_packed, w1_scale, w3_packed, w3_scale)
+    t_count = act.shape[0]
+    eo = grouped(act.reshape(t_count * (top_k + 1), -1), stable.reshape(-1, 1), w2_packed,
+                 w2_scale).reshape(t_count, top_k + 1, -1)
+    full_w = np.concatenate((w, np.ones((t_count, 1), dtype=np.float32)), axis=1)
+    return OM.combine(eo, full_w), idx, w
+
+
+def situ(gate_bits, up_bits, beta: float = 4.0, linear_beta: float | None = 25.0) -> np.ndarray:
+    """K3's SiTU in float32, rounded once to bf16 (kernels/moe_grouped.py:163-178):
+    ``beta * tanh(g / beta) * sigmoid(g) * (linear_beta * tanh(u / linear_beta))``;
+    without ``linear_beta`` the up term is ``u``."""
+    g = bf16_bits_to_f32(gate_bits).astype(np.float32)
+    u = bf16_bits_to_f32(up_bits).astype(np.float32)
+    b = np.float32(beta)
+    with np.errstate(over="ignore"):
+        sig = (np.float32(1.0) / (np.float32(1.0) + np.exp(-g))).astype(np.float32)
+    ag = (b * np.tanh(g / b)).astype(np.float32) * sig
+    if linear_beta is not None:
+        lb = np.float32(linear_beta)
+        u = (lb * np.tanh(u / lb)).astype(np.float32)
+    return f32_to_bf16_bits((ag * u).astype(np.float32))
+
+
+def expert_mlp(x_bits, w1_packed, w1_scale, w3_packed, w3_scale, w2_packed, w2_scale,
+               beta: float = 4.0, linear_beta: float | None = 25.0) -> np.ndarray:
+    """One packed expert: gate / up projections, SiTU, down projection
+    (kernels/moe_grouped.py:181-194, kernels/reference.py:101-116)."""
+    gate = linear(x_bits, w1_packed, w1_scale)
+    up = linear(x_bits, w3_packed, w3_scale)
+    act = situ(gate, up, beta, linear_beta)
+    return linear(act, w2_packed, w2_scale)

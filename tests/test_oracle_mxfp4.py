@@ -94,3 +94,88 @@ def test_linear_matches_bf16_matmul(rng):
     ref = F.linear(xt.double(), wt.double()).float().to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     d = np.abs(y.astype(np.int32) - ref.astype(np.int32))
     assert d.max() <= 1
+
+
+# ---------------------------------------------------------------------------
+# SiTU (engine/kernels/moe_grouped.py:163-178) and the MXFP4 expert compositions
+
+
+def _bits(values):
+    return f32_to_bf16_bits(np.asarray(values, dtype=np.float32))
+
+
+def test_situ_closed_forms():
+    # g = 0 -> 0 for any u
+    assert np.all(bf16_bits_to_f32(X.situ(_bits([0.0, 0.0]), _bits([3.0, -7.0]))) == 0.0)
+    # saturation: tanh and sigmoid round to 1 in fp32 -> beta * linear_beta
+    assert bf16_bits_to_f32(X.situ(_bits([88.0]), _bits([1e4]))) == 4.0 * 25.0
+    # no linear_beta: the up term passes through -> beta * u
+    assert bf16_bits_to_f32(X.situ(_bits([88.0]), _bits([3.0]), linear_beta=None)) == 12.0
+    # odd in u, bit for bit
+    g = _bits(np.linspace(-6, 6, 25))
+    u = _bits(np.linspace(0.1, 40, 25))
+    pos, neg = X.situ(g, u), X.situ(g, _bits(-bf16_bits_to_f32(u)))
+    assert np.array_equal(pos ^ neg, np.where(pos & 0x7FFF, 0x8000, pos ^ neg).astype(np.uint16))
+    # small arguments: beta * tanh(g / beta) * sigmoid(g) -> g / 2, tanh(u / lb) * lb -> u
+    small = X.situ(_bits([2.0 ** -10]), _bits([2.0 ** -10]))
+    assert bf16_bits_to_f32(small)[0] == pytest.approx(2.0 ** -21, rel=2 ** -7)
+
+
+def test_situ_catches_swapped_betas():
+    rng = np.random.default_rng(5)
+    g, u = _bits(rng.normal(0, 3, 200)), _bits(rng.normal(0, 30, 200))
+    good = X.situ(g, u, 4.0, 25.0)
+    assert not np.array_equal(good, X.situ(g, u, 25.0, 4.0))
+
+
+def test_grouped_matches_per_route_linear():
+    rng = np.random.default_rng(6)
+    banks = [X.quantize(rng.normal(0, 0.02, (24, 64)).astype(np.float32)) for _ in range(3)]
+    p = np.stack([b[0] for b in banks])
+    s = np.stack([b[1] for b in banks])
+    x = _bits(rng.normal(0, 1, (4, 64)))
+    idx = np.array([[0, 2], [1, 1], [2, 0], [0, 0]])
+    out = X.grouped(x, idx, p, s)
+    for t in range(4):
+        for r in range(2):
+            assert np.array_equal(out[t, r], X.linear(x[t:t + 1], p[idx[t, r]], s[idx[t, r]])[0])
+
+
+def test_moe_block_matches_a_token_loop():
+    from oracle import moe as OM
+    from oracle.w4a16 import mul_bf16, silu_bf16
+
+    rng = np.random.default_rng(7)
+    e_routed, h, inter, k = 5, 64, 32, 2
+
+    def bank(n, kk):
+        enc = [X.quantize(rng.normal(0, 0.05, (n, kk)).astype(np.float32)) for _ in range(e_routed + 1)]
+        return np.stack([a for a, _ in enc]), np.stack([b for _, b in enc])
+
+    w1, w3, w2 = bank(inter, h), bank(inter, h), bank(h, inter)
+    x = _bits(rng.normal(0, 1, (3, h)))
+    logits = rng.normal(0, 1, (3, e_routed)).astype(np.float32)
+    y, idx, w = X.moe_block(x, logits, None, *w1, *w3, *w2, top_k=k, routed_scaling_factor=2.446)
+    for t in range(3):
+        eo = []
+        for e in list(idx[t]) + [e_routed]:
+            act = mul_bf16(silu_bf16(X.linear(x[t:t + 1], w1[0][e], w1[1][e])),
+                           X.linear(x[t:t + 1], w3[0][e], w3[1][e]))
+            eo.append(X.linear(act, w2[0][e], w2[1][e])[0])
+        want = OM.combine(np.stack(eo)[None], np.concatenate((w[t], [1.0]))[None].astype(np.float32))
+        assert np.array_equal(y[t], want[0])
+
+
+def test_expert_mlp_composition_and_f16_linear():
+    rng = np.random.default_rng(8)
+    w1, w3 = (X.quantize(rng.normal(0, 0.05, (32, 64)).astype(np.float32)) for _ in range(2))
+    w2 = X.quantize(rng.normal(0, 0.05, (64, 32)).astype(np.float32))
+    x = _bits(rng.normal(0, 1, (2, 64)))
+    y = X.expert_mlp(x, *w1, *w3, *w2)
+    act = X.situ(X.linear(x, *w1), X.linear(x, *w3))
+    assert np.array_equal(y, X.linear(act, *w2))
+    # fp16 linear agrees with the bf16 one where both types hold the inputs exactly
+    xf = np.asarray(bf16_bits_to_f32(x), np.float16).view(np.uint16)
+    a = np.asarray(X.linear_f16(xf, *w1), np.uint16).view(np.float16).astype(np.float64)
+    b = bf16_bits_to_f32(X.linear(x, *w1)).astype(np.float64)
+    assert np.allclose(a, b, rtol=1e-2, atol=1e-2)
