@@ -166,15 +166,16 @@ LK_API int lk_w4a16_moe_decode(const uint16_t* x, const float* logits, const flo
  *                        routes outside [0, E); offsets[E+1] = T*R
  *   perm int32 [T*R]:    sorted position -> entry, stable (row-major within
  *                        a bucket)
- *   tiles int32 [max_tiles,4]: (expert or -1, first position, rows <= 64, 0)
+ *   tiles int32 [max_tiles,4]: (expert or -1, first position, rows <= tile_rows, 0),
+ *                        tile_rows 16 or 64 (max_tiles covers both)
  *   tile_count int32 [1]
  * Requires experts <= 512. Sizes from lk_moe_schedule_sizes (R as above). */
 LK_API int lk_moe_schedule_sizes(int64_t tokens, int64_t routes, int64_t experts,
                                  int64_t* max_tiles, int64_t* workspace_bytes);
 LK_API int lk_moe_schedule(const int64_t* expert_indices, int64_t tokens, int64_t routes,
-                           int64_t experts, int64_t shared_expert, int32_t* offsets,
-                           int32_t* perm, int32_t* tiles, int32_t* tile_count, void* workspace,
-                           int64_t workspace_bytes, void* stream);
+                           int64_t experts, int64_t shared_expert, int64_t tile_rows,
+                           int32_t* offsets, int32_t* perm, int32_t* tiles, int32_t* tile_count,
+                           void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- op w4a16_grouped / w4a16_swiglu for many token-routes (the same
  *      contracts as lk_w4a16_grouped / lk_w4a16_swiglu above): expert-major

@@ -38,7 +38,7 @@ SIGNATURES: dict[str, list] = {
     "lk_w4a16_moe_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                             _I64, _I64, _I64, _I64, _I64, _F, _I, _I64, _P],
     "lk_moe_schedule_sizes": [_I64, _I64, _I64, _P, _P],
-    "lk_moe_schedule": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P],
+    "lk_moe_schedule": [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P],
     "lk_w4a16_grouped_gemm": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                               _P, _I64, _P],
     "lk_w4a16_swiglu_gemm": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,

@@ -25,6 +25,9 @@
 // with G = 32 or 64 each MFMA covers 32 consecutive codes and a lane loads
 // one dword per MFMA.
 
+#include <stdlib.h>
+#include <string.h>
+
 #include "lk_common.hpp"
 
 namespace lk {
@@ -39,7 +42,8 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kSchedThreads = 512;
 constexpr int kSchedWaves = kSchedThreads / kWave;
-constexpr int kTileRows = 64;
+constexpr int kTileRows = 64;       // rows per tile of the LDS-staged GEMM
+constexpr int kSmallTileRows = 16;  // rows per tile of the streaming GEMM
 constexpr int kMaxBuckets = 513;  // experts + 1 (the last bucket collects invalid routes)
 
 struct RouteTable {
@@ -64,6 +68,7 @@ struct Schedule {
   int32_t* perm;        // [n] sorted position -> entry
   int32_t* tiles;       // [max_tiles, 4] (expert or -1, first row, rows, 0)
   int32_t* tile_count;  // [1]
+  int tile_rows;        // rows per tile (16 or 64)
 };
 
 __device__ inline int wave_inclusive_scan(int v) {
@@ -109,8 +114,8 @@ __device__ void place_chunk(int64_t n, int nb, int* tot, int* before, int* start
   for (int i = threadIdx.x; i < nb; i += blockDim.x) sc.offsets[i] = start[i];
   if (threadIdx.x == 0) sc.offsets[nb] = static_cast<int32_t>(n);
   __syncthreads();
-  for (int i = threadIdx.x; i < nb; i += blockDim.x)
-    before[i] = (tot[i] + kTileRows - 1) / kTileRows;
+  const int tr = sc.tile_rows;
+  for (int i = threadIdx.x; i < nb; i += blockDim.x) before[i] = (tot[i] + tr - 1) / tr;
   __syncthreads();
   int total_tiles = 0;
   if (threadIdx.x < kWave) total_tiles = wave_exclusive_scan(before, nb);
@@ -119,8 +124,8 @@ __device__ void place_chunk(int64_t n, int nb, int* tot, int* before, int* start
     const int cnt = tot[bb];
     const int expert = bb < nb - 1 ? bb : -1;
     int4* out = reinterpret_cast<int4*>(sc.tiles) + before[bb];
-    for (int row = 0; row < cnt; row += kTileRows, ++out)
-      *out = make_int4(expert, start[bb] + row, min(kTileRows, cnt - row), 0);
+    for (int row = 0; row < cnt; row += tr, ++out)
+      *out = make_int4(expert, start[bb] + row, min(tr, cnt - row), 0);
   }
   if (threadIdx.x == 0) *sc.tile_count = total_tiles;
 }
@@ -640,6 +645,282 @@ w4a16_gemm_kernel(const GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// Streaming GEMM over tiles of at most 16 rows (decode batches)
+
+constexpr int kStWaves = 8;
+constexpr int kStDepth = 6;                      // k-steps of weights in flight per wave
+constexpr int kStMaxLds = 150 * 1024;            // two blocks per CU (160 KB of LDS)
+
+template <int FMT>
+__device__ inline uint16_t store_value(float v) {
+  if constexpr (FMT == kFmtMxF16) return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+  else return f32_to_bf16(v);
+}
+
+// LDS bytes of one streaming block: the tile's activation fragments for all
+// k-steps plus W4A16's -136 * sum(x) per (step, group-in-step, row).
+inline size_t stream_lds_bytes(int64_t k) {
+  const int64_t ksteps = (k + 127) / 128;
+  return static_cast<size_t>(ksteps) * (4 * kWave * sizeof(uint4) + 4 * 16 * sizeof(float));
+}
+
+// Block = 8 waves over one tile of <= 16 rows x (8 * 16 * NT) columns. The
+// block stages the tile's activation rows for the whole reduction in LDS once
+// (one barrier); then every wave streams its own columns over all of k with
+// kStDepth k-steps of weights in flight and no further barrier, and stores
+// its outputs itself.
+template <int FMT, int MATS, int NT, bool WIDE, bool GATHER, bool SCATTER, bool DENSE>
+__global__ void __launch_bounds__(kStWaves * kWave, 2)
+w4a16_stream_kernel(const GemmArgs g) {
+  constexpr bool kMx = FMT != kFmtW4A16;
+  static_assert(!(kMx && WIDE), "MXFP4 groups are 32 wide");
+  constexpr int kThreads = kStWaves * kWave;
+  constexpr int kBN = kStWaves * NT * 16;
+  extern __shared__ uint4 smem[];
+
+  const int per_tile = g.col_blocks * g.outputs;
+  const int id = blockIdx.x;
+  const int grp = id / (8 * per_tile);
+  const int rem = id - grp * 8 * per_tile;
+  const int tile = grp * 8 + (rem & 7);
+  const int cb_all = rem >> 3;
+  const int osel = cb_all / g.col_blocks;
+  const int cb = cb_all - osel * g.col_blocks;
+  int expert, row0, rows;
+  if constexpr (DENSE) {
+    row0 = tile * kSmallTileRows;
+    if (row0 >= g.dense_rows) return;
+    rows = min(kSmallTileRows, g.dense_rows - row0);
+    expert = 0;
+  } else {
+    // the descriptor load does not wait for the count (the list holds max_tiles entries)
+    const int4 d = reinterpret_cast<const int4*>(g.tiles)[tile];
+    if (tile >= *g.tile_count) return;
+    expert = d.x;
+    row0 = d.y;
+    rows = d.z;
+  }
+  const int64_t N = g.n, K = g.k;
+  uint16_t* const out = pick3(g.out, osel);
+  const int tid = threadIdx.x;
+  if (expert < 0) {  // routes outside the bank produce zero rows
+    for (int i = tid; i < rows * kBN; i += kThreads) {
+      const int m = i / kBN;
+      const int64_t col = static_cast<int64_t>(cb) * kBN + (i - m * kBN);
+      if (col < N) {
+        const int64_t orow = SCATTER ? g.perm[row0 + m] : row0 + m;
+        out[orow * N + col] = 0;
+      }
+    }
+    return;
+  }
+
+  const int lane = tid & (kWave - 1);
+  const int wv = tid / kWave;
+  const int jq = lane >> 4;
+  const int ln = lane & 15;
+  const int64_t rowb = K / 2;
+  const int64_t spr = K / g.group;
+  const int ksteps = static_cast<int>((K + 127) / 128);
+  const int cg = static_cast<int>(g.group / 32);
+  uint4* const afrag = smem;                                              // [ksteps][4][64]
+  float* const offs = reinterpret_cast<float*>(smem + ksteps * 4 * kWave);  // [ksteps][4][16]
+
+  // 1. this wave's first kStDepth k-steps of weights
+  const uint8_t* wrow[MATS][NT];
+  const void* srow[MATS][NT];
+  int64_t col[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    col[nt] = static_cast<int64_t>(cb) * kBN + (wv * NT + nt) * 16 + ln;
+    const int64_t cc = col[nt] < N ? col[nt] : N - 1;
+#pragma unroll
+    for (int mi = 0; mi < MATS; ++mi) {
+      wrow[mi][nt] = pick3(g.wp, osel + mi) + expert * g.wstride + cc * rowb;
+      if constexpr (kMx)
+        srow[mi][nt] = static_cast<const uint8_t*>(pick3(g.ws, osel + mi)) + expert * g.sstride +
+                       cc * spr;
+      else
+        srow[mi][nt] = static_cast<const uint16_t*>(pick3(g.ws, osel + mi)) +
+                       expert * g.sstride + cc * spr;
+    }
+  }
+  WeightStep<FMT, MATS, NT, WIDE> w[kStDepth];
+#pragma unroll
+  for (int j = 0; j < kStDepth; ++j)
+    if (j < ksteps) w[j].load(wrow, srow, j, jq, K, g.group);
+
+  // 2. the tile's activation rows (one lookup per row, shared through LDS)
+  __shared__ int64_t row_index[kSmallTileRows];
+  if (tid < rows) {
+    if constexpr (GATHER) row_index[tid] = g.perm[row0 + tid] / g.routes;
+    else row_index[tid] = row0 + tid;
+  }
+  __syncthreads();
+
+  // 3. stage them: unit u = ((m * ksteps) + step) * 16 + c, so the 16 units of
+  // one (row, step) sit in one 16-lane DPP row; loads go out in batches
+  constexpr int kBatch = 6;
+  const int units = rows * ksteps * 16;
+  for (int u0 = 0; u0 < units; u0 += kBatch * kThreads) {
+    uint4 v[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int u = u0 + b * kThreads + tid;
+      if (u < units) {
+        const int c = u & 15;
+        const int rest = u >> 4;
+        const int step = rest % ksteps;
+        const int m = rest / ksteps;
+        const int64_t k0 = static_cast<int64_t>(step) * 128 + c * 8;
+        v[b] = *reinterpret_cast<const uint4*>(g.a + row_index[m] * K + (k0 < K ? k0 : 0));
+        if (k0 >= K) v[b] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int u = u0 + b * kThreads + tid;
+      if (u < units) {  // uniform over each 16-lane row (units is a multiple of 16)
+        const int c = u & 15;
+        const int rest = u >> 4;
+        const int step = rest % ksteps;
+        const int m = rest / ksteps;
+        const int t = WIDE ? (c & 3) : (c >> 2);
+        const int j = WIDE ? (c >> 2) : (c & 3);
+        uint4* dst = &afrag[(step * 4 + t) * kWave + j * 16 + (m ^ (4 * t + j))];
+        if constexpr (kMx) {
+          *dst = v[b];
+        } else {
+          uint32_t p[4];
+          pair_x8(v[b], p);
+          *dst = make_uint4(p[0], p[1], p[2], p[3]);
+          float sx = sum_x8_dot(v[b]);
+          if constexpr (WIDE) {
+            sx = sum8(sx);
+            sx += dpp_f32<kRowMirror>(sx);
+            if (c == 0) offs[(step * 4) * 16 + m] = -kCodeOffset * sx;
+          } else {
+            sx = sum4(sx);
+            if (cg == 2) sx += dpp_f32<kRowHalfMirror>(sx);
+            if ((c & (4 * cg - 1)) == 0) offs[(step * 4 + t / cg) * 16 + m] = -kCodeOffset * sx;
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // 4. stream: slot j of the ring holds step base + j and is refilled with
+  // step base + j + kStDepth once consumed
+  const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t tot[MATS][NT], acc[MATS][NT];
+#pragma unroll
+  for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      tot[mi][nt] = zero4;
+      acc[mi][nt] = zero4;
+    }
+  for (int base = 0; base < ksteps; base += kStDepth) {
+#pragma unroll
+    for (int j = 0; j < kStDepth; ++j) {
+      const int step = base + j;
+      if (step >= ksteps) break;
+      if constexpr (kMx) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (static_cast<int64_t>(step) * 128 + 32 * t >= K) break;
+          const uint4 q = afrag[(step * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))];
+          const u32x4_t av = {q.x, q.y, q.z, q.w};
+#pragma unroll
+          for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+              const float sc = e8m0_to_f32(w[j].s[mi][nt][t]);
+              if constexpr (FMT == kFmtMxBf16)
+                tot[mi][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8_t, av),
+                    __builtin_bit_cast(bf16x8_t, unpack_fp4x8_bf16(w[j].w[mi][nt][t], sc)),
+                    tot[mi][nt], 0, 0, 0);
+              else
+                tot[mi][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(f16x8_t, av),
+                    __builtin_bit_cast(f16x8_t, unpack_fp4x8_f16(w[j].w[mi][nt][t], sc)),
+                    tot[mi][nt], 0, 0, 0);
+            }
+        }
+      } else if constexpr (WIDE) {
+        const bool first = (static_cast<int64_t>(step) * 128) % g.group == 0;
+        const bool last = (static_cast<int64_t>(step + 1) * 128) % g.group == 0;
+        const f32x4_t neg = *reinterpret_cast<const f32x4_t*>(&offs[(step * 4) * 16 + jq * 4]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const bf16x8_t af = __builtin_bit_cast(
+              bf16x8_t, afrag[(step * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
+#pragma unroll
+          for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+              const f32x4_t cin = t > 0 ? acc[mi][nt] : (first ? neg : acc[mi][nt] + neg);
+              acc[mi][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  af, unpack_q8(w[j].w[mi][nt][t]), cin, 0, 0, 0);
+            }
+        }
+        if (last) {
+#pragma unroll
+          for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+              tot[mi][nt] += bf16_to_f32(static_cast<uint16_t>(w[j].s[mi][nt][0])) * acc[mi][nt];
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (static_cast<int64_t>(step) * 128 + 32 * t >= K) break;
+          const bool first = (t % cg) == 0;
+          const bool last = ((t + 1) % cg) == 0;
+          const bf16x8_t af = __builtin_bit_cast(
+              bf16x8_t, afrag[(step * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
+          f32x4_t neg = zero4;
+          if (first)
+            neg = *reinterpret_cast<const f32x4_t*>(&offs[(step * 4 + t / cg) * 16 + jq * 4]);
+#pragma unroll
+          for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+              const f32x4_t cin = first ? neg : acc[mi][nt];
+              acc[mi][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  af, unpack_q8(w[j].w[mi][nt][t]), cin, 0, 0, 0);
+              if (last)
+                tot[mi][nt] += bf16_to_f32(static_cast<uint16_t>(w[j].s[mi][nt][t])) * acc[mi][nt];
+            }
+        }
+      }
+      if (step + kStDepth < ksteps) w[j].load(wrow, srow, step + kStDepth, jq, K, g.group);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = jq * 4 + i;
+    if (m >= rows) continue;
+    const int64_t orow = SCATTER ? static_cast<int64_t>(g.perm[row0 + m]) : row0 + m;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (col[nt] >= N) continue;
+      uint16_t v;
+      if constexpr (MATS == 2)
+        v = g.act == kActSitu ? situ_bf16(tot[0][nt][i], tot[1][nt][i], g.situ_beta,
+                                          g.situ_linear_beta)
+                              : swiglu_bf16(tot[0][nt][i], tot[1][nt][i]);
+      else
+        v = store_value<FMT>(tot[0][nt][i]);
+      out[orow * N + col[nt]] = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // route combine over entry-ordered expert outputs eo [T * (top_k + 1), H]:
 // y[t] = bf16(bf16(sum_{r < top_k} w[t, r] * eo[t, r]) + eo[t, top_k]),
 // 8 columns per thread.
@@ -694,14 +975,15 @@ struct SchedLayout {
   int64_t max_tiles;
 };
 
-int64_t max_tiles_for(int64_t entries, int64_t experts) {
-  return (experts + 1 < entries ? experts + 1 : entries) + entries / kTileRows + 1;
+int64_t max_tiles_for(int64_t entries, int64_t experts, int tile_rows) {
+  return (experts + 1 < entries ? experts + 1 : entries) + entries / tile_rows + 1;
 }
 
+// The layout holds the tile list of the smaller (16-row) tiles, which bounds both.
 SchedLayout sched_layout(int64_t entries, int64_t experts) {
   SchedLayout l;
   l.chunks = static_cast<int>((entries + kSchedThreads - 1) / kSchedThreads);
-  l.max_tiles = max_tiles_for(entries, experts);
+  l.max_tiles = max_tiles_for(entries, experts, kSmallTileRows);
   l.rank = 0;
   l.hist = align_up(static_cast<size_t>(entries) * 4);
   l.total = l.hist + align_up(static_cast<size_t>(l.chunks) * (experts + 1) * 4);
@@ -736,7 +1018,7 @@ MoeLayout moe_layout(int64_t entries, int64_t experts, int64_t act_cols, int64_t
 
 int schedule_launch(const RouteTable& rt, int64_t entries, char* ws, const SchedLayout& sl,
                     int32_t* offsets, int32_t* perm, int32_t* tiles, int32_t* tile_count,
-                    hipStream_t s) {
+                    int tile_rows, hipStream_t s) {
   Schedule sc;
   sc.rank = reinterpret_cast<int32_t*>(ws + sl.rank);
   sc.hist = reinterpret_cast<int32_t*>(ws + sl.hist);
@@ -744,6 +1026,7 @@ int schedule_launch(const RouteTable& rt, int64_t entries, char* ws, const Sched
   sc.perm = perm;
   sc.tiles = tiles;
   sc.tile_count = tile_count;
+  sc.tile_rows = tile_rows;
   schedule_count_kernel<<<sl.chunks, kSchedThreads, 0, s>>>(rt, entries, sc);
   if (sl.chunks > 1)
     schedule_place_kernel<<<sl.chunks, kSchedThreads, 0, s>>>(rt, entries, sl.chunks, sc);
@@ -813,6 +1096,73 @@ int gemm_launch(GemmArgs g, Mode mode, int64_t tiles, bool wide_cols, hipStream_
   return check_launch(what);
 }
 
+template <int FMT, int MATS, bool WIDE>
+void stream_dispatch(const GemmArgs& g, Mode mode, unsigned blocks, size_t lds, hipStream_t s) {
+  constexpr int NT = MATS == 2 ? 1 : 2;
+  constexpr int T = kStWaves * kWave;
+  if constexpr (FMT == kFmtMxF16) {
+    w4a16_stream_kernel<FMT, MATS, NT, false, false, false, true><<<blocks, T, lds, s>>>(g);
+  } else {
+    switch (mode) {
+      case Mode::Gather:
+        w4a16_stream_kernel<FMT, MATS, NT, WIDE, true, false, false><<<blocks, T, lds, s>>>(g);
+        break;
+      case Mode::Scatter:
+        w4a16_stream_kernel<FMT, MATS, NT, WIDE, false, true, false><<<blocks, T, lds, s>>>(g);
+        break;
+      case Mode::GatherScatter:
+        w4a16_stream_kernel<FMT, MATS, NT, WIDE, true, true, false><<<blocks, T, lds, s>>>(g);
+        break;
+      case Mode::Dense:
+        w4a16_stream_kernel<FMT, MATS, NT, WIDE, false, false, true><<<blocks, T, lds, s>>>(g);
+        break;
+    }
+  }
+}
+
+// The streaming kernel needs the whole reduction of a 16-row tile in LDS.
+bool stream_fits(int64_t k) { return stream_lds_bytes(k) <= static_cast<size_t>(kStMaxLds); }
+
+template <int FMT, int MATS, bool WIDE>
+void stream_set_lds_limit() {
+  constexpr int NT = MATS == 2 ? 1 : 2;
+  static bool done = false;  // once per process (the attribute is per function)
+  if (done) return;
+  done = true;
+  (void)hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&w4a16_stream_kernel<FMT, MATS, NT, WIDE, true, false, false>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, kStMaxLds);
+  (void)hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&w4a16_stream_kernel<FMT, MATS, NT, WIDE, false, true, false>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, kStMaxLds);
+  (void)hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&w4a16_stream_kernel<FMT, MATS, NT, WIDE, true, true, false>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, kStMaxLds);
+  (void)hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&w4a16_stream_kernel<FMT, MATS, NT, WIDE, false, false, true>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, kStMaxLds);
+}
+
+template <int FMT, int MATS>
+int stream_launch(GemmArgs g, Mode mode, int64_t tiles, hipStream_t s, const char* what) {
+  constexpr int NT = MATS == 2 ? 1 : 2;
+  const bool wide = FMT == kFmtW4A16 && g.group >= 128;
+  const size_t lds = stream_lds_bytes(g.k);
+  LK_REQUIRE(lds <= static_cast<size_t>(kStMaxLds), "%s: reduction width too large", what);
+  g.col_blocks = static_cast<int>((g.n + kStWaves * NT * 16 - 1) / (kStWaves * NT * 16));
+  const int64_t blocks = (tiles + 7) / 8 * 8 * g.col_blocks * g.outputs;
+  LK_REQUIRE(blocks > 0 && blocks < (1LL << 31), "%s: too many blocks", what);
+  const unsigned nb = static_cast<unsigned>(blocks);
+  if (wide) {
+    stream_set_lds_limit<FMT, MATS, FMT == kFmtW4A16>();
+    stream_dispatch<FMT, MATS, FMT == kFmtW4A16>(g, mode, nb, lds, s);
+  } else {
+    stream_set_lds_limit<FMT, MATS, false>();
+    stream_dispatch<FMT, MATS, false>(g, mode, nb, lds, s);
+  }
+  return check_launch(what);
+}
+
 // Wider column blocks once there are enough tiles to fill the machine.
 bool wide_cols_for(int64_t tiles, int64_t n) { return tiles * ((n + 63) / 64) >= 2048; }
 
@@ -829,6 +1179,25 @@ int launch_fmt(bool mx, const GemmArgs& g, Mode mode, int64_t tiles, bool wide_c
                       hipStream_t s, const char* what) {
   if (mx) return gemm_launch<kFmtMxBf16, MATS>(g, mode, tiles, wide_cols, s, what);
   return gemm_launch<kFmtW4A16, MATS>(g, mode, tiles, wide_cols, s, what);
+}
+
+template <int MATS>
+int stream_fmt(bool mx, const GemmArgs& g, Mode mode, int64_t tiles, hipStream_t s,
+               const char* what) {
+  if (mx) return stream_launch<kFmtMxBf16, MATS>(g, mode, tiles, s, what);
+  return stream_launch<kFmtW4A16, MATS>(g, mode, tiles, s, what);
+}
+
+// Token-routes up to which expert-major calls use the streaming kernel on
+// 16-row tiles (decode batches); larger calls use the LDS-staged kernel on
+// 64-row tiles. LK_MOE_GEMM=stream|lds forces one path.
+constexpr int64_t kStreamMaxEntries = 2048;
+
+bool use_stream(int64_t entries) {
+  const char* env = getenv("LK_MOE_GEMM");
+  if (env && strcmp(env, "lds") == 0) return false;
+  if (env && strcmp(env, "stream") == 0) return true;
+  return entries <= kStreamMaxEntries;
 }
 
 // W4A16: a power-of-two group (multiple of 32) dividing k; MXFP4: 32.
@@ -870,10 +1239,12 @@ int lk_moe_schedule_sizes(int64_t tokens, int64_t routes, int64_t experts, int64
 }
 
 int lk_moe_schedule(const int64_t* expert_indices, int64_t tokens, int64_t routes,
-                    int64_t experts, int64_t shared_expert, int32_t* offsets, int32_t* perm,
-                    int32_t* tiles, int32_t* tile_count, void* workspace,
+                    int64_t experts, int64_t shared_expert, int64_t tile_rows, int32_t* offsets,
+                    int32_t* perm, int32_t* tiles, int32_t* tile_count, void* workspace,
                     int64_t workspace_bytes, void* stream) {
   const int64_t r_total = routes + (shared_expert >= 0 ? 1 : 0);
+  LK_REQUIRE(tile_rows == kSmallTileRows || tile_rows == kTileRows,
+             "tile rows must be %d or %d", kSmallTileRows, kTileRows);
   if (int rc = check_schedule_dims(tokens, r_total, experts)) return rc;
   LK_REQUIRE(shared_expert < experts, "shared expert id %lld outside the bank",
              (long long)shared_expert);
@@ -893,7 +1264,7 @@ int lk_moe_schedule(const int64_t* expert_indices, int64_t tokens, int64_t route
   LK_REQUIRE(expert_indices != nullptr || routes == 0, "null pointer argument");
   const RouteTable rt{expert_indices, routes, r_total, experts, shared_expert};
   return schedule_launch(rt, entries, static_cast<char*>(workspace), l, offsets, perm, tiles,
-                         tile_count, as_stream(stream));
+                         tile_count, static_cast<int>(tile_rows), as_stream(stream));
 }
 
 int64_t lk_w4a16_grouped_gemm_workspace(int64_t tokens, int64_t routes, int64_t experts) {
@@ -925,8 +1296,11 @@ static int grouped_gemm_common(bool mx, const uint16_t* x, const int64_t* idx, c
   auto* perm = reinterpret_cast<int32_t*>(ws + l.perm);
   auto* tiles = reinterpret_cast<int32_t*>(ws + l.tiles);
   auto* count = reinterpret_cast<int32_t*>(ws + l.count);
+  const bool small = use_stream(entries) && stream_fits(k);
+  const int tr = small ? kSmallTileRows : kTileRows;
   const RouteTable rt{idx, routes, routes, experts, -1};
-  if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, s)) return rc;
+  if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, tr, s))
+    return rc;
   GemmArgs g{};
   g.a = x;
   g.perm = perm;
@@ -947,9 +1321,14 @@ static int grouped_gemm_common(bool mx, const uint16_t* x, const int64_t* idx, c
   g.routes = routes;
   g.outputs = 1;
   g.act = kActSwiglu;
-  const bool wc = wide_cols_for(l.sched.max_tiles, n);
-  if (swiglu) return launch_fmt<2>(mx, g, Mode::GatherScatter, l.sched.max_tiles, wc, s, name);
-  return launch_fmt<1>(mx, g, Mode::GatherScatter, l.sched.max_tiles, wc, s, name);
+  const int64_t mt = max_tiles_for(entries, experts, tr);
+  if (small) {
+    if (swiglu) return stream_fmt<2>(mx, g, Mode::GatherScatter, mt, s, name);
+    return stream_fmt<1>(mx, g, Mode::GatherScatter, mt, s, name);
+  }
+  const bool wc = wide_cols_for(mt, n);
+  if (swiglu) return launch_fmt<2>(mx, g, Mode::GatherScatter, mt, wc, s, name);
+  return launch_fmt<1>(mx, g, Mode::GatherScatter, mt, wc, s, name);
 }
 
 int lk_w4a16_grouped_gemm(const uint16_t* x, const int64_t* expert_indices,
@@ -1155,10 +1534,13 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   auto* count = reinterpret_cast<int32_t*>(ws + l.count);
   auto* act = reinterpret_cast<uint16_t*>(ws + l.act);
   auto* eo = reinterpret_cast<uint16_t*>(ws + l.eo);
-  const RouteTable rt{expert_indices, top_k, routes, experts, experts - 1};
-  if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, s)) return rc;
-
   const int64_t group = mx ? 32 : group_size;
+  const bool small = use_stream(entries) && stream_fits(h) && stream_fits(i);
+  const int tr = small ? kSmallTileRows : kTileRows;
+  const RouteTable rt{expert_indices, top_k, routes, experts, experts - 1};
+  if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, tr, s))
+    return rc;
+
   GemmArgs g{};
   g.perm = perm;
   g.tiles = tiles;
@@ -1180,8 +1562,10 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.k = h;
   g.wstride = i * h / 2;
   g.sstride = i * (h / group);
-  const int64_t mt = l.sched.max_tiles;
-  if (int rc = launch_fmt<2>(mx, g, Mode::Gather, mt, wide_cols_for(mt, i), s, "moe gate/up gemm"))
+  const int64_t mt = max_tiles_for(entries, experts, tr);
+  if (int rc = small ? stream_fmt<2>(mx, g, Mode::Gather, mt, s, "moe gate/up gemm")
+                     : launch_fmt<2>(mx, g, Mode::Gather, mt, wide_cols_for(mt, i), s,
+                                     "moe gate/up gemm"))
     return rc;
   // down projection: sorted activation rows, outputs scattered to (token, route) rows
   g.a = act;
@@ -1192,7 +1576,9 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.k = i;
   g.wstride = h * i / 2;
   g.sstride = h * (i / group);
-  if (int rc = launch_fmt<1>(mx, g, Mode::Scatter, mt, wide_cols_for(mt, h), s, "moe down gemm"))
+  if (int rc = small ? stream_fmt<1>(mx, g, Mode::Scatter, mt, s, "moe down gemm")
+                     : launch_fmt<1>(mx, g, Mode::Scatter, mt, wide_cols_for(mt, h), s,
+                                     "moe down gemm"))
     return rc;
   const int64_t work = tokens * (h / 8);
   moe_combine_kernel<<<static_cast<unsigned>((work + 255) / 256), 256, 0, s>>>(

@@ -30,7 +30,8 @@ MOE_EXPERT_MAJOR_MIN_TOKENS = 2
 MOE_EXPERT_MAJOR_MAX_EXPERTS = 512
 
 
-def moe_schedule(expert_indices: torch.Tensor, experts: int, shared_expert: int = -1):
+def moe_schedule(expert_indices: torch.Tensor, experts: int, shared_expert: int = -1,
+                 tile_rows: int = 64):
     """Expert-major schedule of a route table on the GPU.
 
     Returns ``(offsets int32 [E+2], perm int32 [T*R], tiles int32 [n, 4],
@@ -53,7 +54,7 @@ def moe_schedule(expert_indices: torch.Tensor, experts: int, shared_expert: int 
     idx = _w._c(expert_indices)
     with torch.cuda.device(dev):
         _lib.call("lk_moe_schedule", idx.data_ptr(), tokens, routes, experts, shared_expert,
-                  offsets.data_ptr(), perm.data_ptr(), tiles.data_ptr(), count.data_ptr(),
+                  tile_rows, offsets.data_ptr(), perm.data_ptr(), tiles.data_ptr(), count.data_ptr(),
                   ws.data_ptr(), ws.numel(), _w._stream(dev))
     return offsets, perm, tiles, count
 

@@ -58,8 +58,8 @@ def test_argument_errors_are_reported_without_touching_the_gpu(lib):
 
 def test_expert_major_sizes_and_argument_errors(lib):
     max_tiles, ws = _lib.schedule_sizes(2048, 9, 257)
-    # prefill bound: min(E + 1, n) + n / 64 + 1 tiles of 64 rows
-    assert max_tiles == 258 + 18432 // 64 + 1
+    # prefill bound for the smaller (16-row) tiles: min(E + 1, n) + n / 16 + 1
+    assert max_tiles == 258 + 18432 // 16 + 1
     assert ws >= 18432 * 4
     assert _lib.query("lk_w4a16_moe_forward_workspace", 64, 257, 2304, 1024, 8) > 0
     assert lib.lk_w4a16_moe_forward_workspace(64, 1000, 2304, 1024, 8) == -1
@@ -67,6 +67,8 @@ def test_expert_major_sizes_and_argument_errors(lib):
     with pytest.raises(RuntimeError, match="experts"):
         _lib.schedule_sizes(4, 8, 600)
     with pytest.raises(RuntimeError, match="workspace too small"):
-        _lib.call("lk_moe_schedule", 1, 4, 8, 16, -1, 1, 1, 1, 1, 1, 8, None)
+        _lib.call("lk_moe_schedule", 1, 4, 8, 16, -1, 64, 1, 1, 1, 1, 1, 8, None)
+    with pytest.raises(RuntimeError, match="tile rows"):
+        _lib.call("lk_moe_schedule", 1, 4, 8, 16, -1, 32, 1, 1, 1, 1, 1, 1 << 20, None)
     with pytest.raises(RuntimeError, match="divisible"):
         _lib.call("lk_w4a16_dense_gemm", 1, 1, 1, 1, 16, 8, 100, 32, None)

@@ -52,12 +52,13 @@ def _bank(rng, e, n, k, g):
 # schedule
 
 
-def _expected_tiles(offsets, experts):
+def _expected_tiles(offsets, experts, tile_rows):
     tiles = []
     for b in range(experts + 1):
         cnt = int(offsets[b + 1] - offsets[b])
-        for row in range(0, cnt, 64):
-            tiles.append((b if b < experts else -1, int(offsets[b]) + row, min(64, cnt - row), 0))
+        for row in range(0, cnt, tile_rows):
+            tiles.append((b if b < experts else -1, int(offsets[b]) + row,
+                          min(tile_rows, cnt - row), 0))
     return np.array(tiles, dtype=np.int32).reshape(-1, 4)
 
 
@@ -70,7 +71,8 @@ def _expected_tiles(offsets, experts):
     (5, 3, 512, -1, False),       # largest bank
     (700, 1, 3, -1, False),       # one hot expert split over many tiles
 ])
-def test_schedule_matches_oracle(rng, tokens, routes, experts, shared, invalid):
+@pytest.mark.parametrize("tile_rows", [16, 64])
+def test_schedule_matches_oracle(rng, tokens, routes, experts, shared, invalid, tile_rows):
     from local_kimi_amd.kernels import moe_schedule
 
     high = experts - 1 if shared >= 0 else experts
@@ -79,7 +81,7 @@ def test_schedule_matches_oracle(rng, tokens, routes, experts, shared, invalid):
         flat = idx.reshape(-1)
         pick = rng.choice(flat.size, size=max(1, flat.size // 7), replace=False)
         flat[pick] = rng.choice(np.array([-1, experts, experts + 5, -7]), size=pick.size)
-    offsets, perm, tiles, count = moe_schedule(_dev(idx), experts, shared)
+    offsets, perm, tiles, count = moe_schedule(_dev(idx), experts, shared, tile_rows)
     full = idx if shared < 0 else np.concatenate(
         (idx, np.full((tokens, 1), shared, dtype=np.int64)), axis=1)
     flat = full.reshape(-1)
@@ -91,12 +93,12 @@ def test_schedule_matches_oracle(rng, tokens, routes, experts, shared, invalid):
     p = perm.cpu().numpy()
     assert np.array_equal(p[: eoff[-1]], eperm)
     assert np.array_equal(p[eoff[-1]:], np.nonzero(~valid)[0])
-    want = _expected_tiles(off, experts)
+    want = _expected_tiles(off, experts, tile_rows)
     n_tiles = int(count.item())
     assert n_tiles == len(want)
     assert np.array_equal(tiles.cpu().numpy()[:n_tiles], want)
     # rerun: identical tables
-    again = moe_schedule(_dev(idx), experts, shared)
+    again = moe_schedule(_dev(idx), experts, shared, tile_rows)
     assert torch.equal(again[1], perm) and torch.equal(again[0], offsets)
 
 
