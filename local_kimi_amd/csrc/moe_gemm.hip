@@ -649,7 +649,8 @@ w4a16_gemm_kernel(const GemmArgs g) {
 
 constexpr int kStWaves = 8;
 constexpr int kStDepth = 6;                      // k-steps of weights in flight per wave
-constexpr int kStMaxLds = 150 * 1024;            // two blocks per CU (160 KB of LDS)
+constexpr int kStMaxLds = 150 * 1024;            // LDS a streaming block may take
+constexpr int kStPassSteps = 4;                  // k-steps per activation pass (64-row tiles)
 
 template <int FMT>
 __device__ inline uint16_t store_value(float v) {
@@ -657,26 +658,35 @@ __device__ inline uint16_t store_value(float v) {
   else return f32_to_bf16(v);
 }
 
-// LDS bytes of one streaming block: the tile's activation fragments for all
-// k-steps plus W4A16's -136 * sum(x) per (step, group-in-step, row).
-inline size_t stream_lds_bytes(int64_t k) {
+// LDS bytes of one streaming block with 16 * mt-row tiles: mt == 1 keeps all
+// k-steps of the tile's activations (one buffer); mt > 1 double-buffers
+// passes of kStPassSteps k-steps. Per (k-step, 16-row subtile): 4 MFMA
+// fragments of 64 x 16 bytes and W4A16's -136 * sum(x) per (group, row).
+inline size_t stream_lds_bytes(int64_t k, int mt) {
   const int64_t ksteps = (k + 127) / 128;
-  return static_cast<size_t>(ksteps) * (4 * kWave * sizeof(uint4) + 4 * 16 * sizeof(float));
+  const int64_t ps = mt == 1 ? ksteps : kStPassSteps;
+  const int64_t nbuf = mt == 1 ? 1 : 2;
+  return static_cast<size_t>(nbuf * ps * mt) * (4 * kWave * sizeof(uint4) + 4 * 16 * sizeof(float));
 }
 
-// Block = 8 waves over one tile of <= 16 rows x (8 * 16 * NT) columns. The
-// block stages the tile's activation rows for the whole reduction in LDS once
-// (one barrier); then every wave streams its own columns over all of k with
-// kStDepth k-steps of weights in flight and no further barrier, and stores
-// its outputs itself.
-template <int FMT, int MATS, int NT, bool WIDE, bool GATHER, bool SCATTER, bool DENSE>
+// Block = 8 waves over one tile of <= 16 * MT rows x (8 * 16 * NT) columns.
+// The block stages the tile's activation rows in LDS (MT == 1: the whole
+// reduction once, one barrier; MT > 1: passes of kStPassSteps k-steps,
+// double buffered, the next pass loaded while the current one computes, one
+// barrier per pass); every wave streams its own columns over all of k with
+// kStDepth k-steps of weights in flight and stores its outputs itself.
+template <int FMT, int MATS, int NT, int MT, bool WIDE, bool GATHER, bool SCATTER, bool DENSE>
 __global__ void __launch_bounds__(kStWaves * kWave, 2)
 w4a16_stream_kernel(const GemmArgs g) {
   constexpr bool kMx = FMT != kFmtW4A16;
   static_assert(!(kMx && WIDE), "MXFP4 groups are 32 wide");
   constexpr int kThreads = kStWaves * kWave;
   constexpr int kBN = kStWaves * NT * 16;
+  constexpr int kRows = 16 * MT;
+  constexpr int kNBuf = MT == 1 ? 1 : 2;
+  constexpr int kPassUnits = MT == 1 ? 1 : (kRows * kStPassSteps * 16 + kThreads - 1) / kThreads;
   extern __shared__ uint4 smem[];
+  __shared__ int64_t row_index[kRows];
 
   const int per_tile = g.col_blocks * g.outputs;
   const int id = blockIdx.x;
@@ -688,9 +698,9 @@ w4a16_stream_kernel(const GemmArgs g) {
   const int cb = cb_all - osel * g.col_blocks;
   int expert, row0, rows;
   if constexpr (DENSE) {
-    row0 = tile * kSmallTileRows;
+    row0 = tile * kRows;
     if (row0 >= g.dense_rows) return;
-    rows = min(kSmallTileRows, g.dense_rows - row0);
+    rows = min(kRows, g.dense_rows - row0);
     expert = 0;
   } else {
     // the descriptor load does not wait for the count (the list holds max_tiles entries)
@@ -722,9 +732,11 @@ w4a16_stream_kernel(const GemmArgs g) {
   const int64_t rowb = K / 2;
   const int64_t spr = K / g.group;
   const int ksteps = static_cast<int>((K + 127) / 128);
+  const int ps = MT == 1 ? ksteps : kStPassSteps;  // k-steps per pass
   const int cg = static_cast<int>(g.group / 32);
-  uint4* const afrag = smem;                                              // [ksteps][4][64]
-  float* const offs = reinterpret_cast<float*>(smem + ksteps * 4 * kWave);  // [ksteps][4][16]
+  const int mt_act = (rows + 15) >> 4;
+  uint4* const afrag = smem;  // [kNBuf][ps][MT][4][64]
+  float* const offs = reinterpret_cast<float*>(smem + kNBuf * ps * MT * 4 * kWave);  // [kNBuf][ps][MT][4][16]
 
   // 1. this wave's first kStDepth k-steps of weights
   const uint8_t* wrow[MATS][NT];
@@ -745,66 +757,78 @@ w4a16_stream_kernel(const GemmArgs g) {
                        expert * g.sstride + cc * spr;
     }
   }
-  WeightStep<FMT, MATS, NT, WIDE> w[kStDepth];
+  constexpr int kRing = MT == 1 ? kStDepth : kStPassSteps;
+  WeightStep<FMT, MATS, NT, WIDE> w[kRing];
 #pragma unroll
-  for (int j = 0; j < kStDepth; ++j)
+  for (int j = 0; j < kRing; ++j)
     if (j < ksteps) w[j].load(wrow, srow, j, jq, K, g.group);
 
   // 2. the tile's activation rows (one lookup per row, shared through LDS)
-  __shared__ int64_t row_index[kSmallTileRows];
   if (tid < rows) {
     if constexpr (GATHER) row_index[tid] = g.perm[row0 + tid] / g.routes;
     else row_index[tid] = row0 + tid;
   }
   __syncthreads();
 
-  // 3. stage them: unit u = ((m * ksteps) + step) * 16 + c, so the 16 units of
-  // one (row, step) sit in one 16-lane DPP row; loads go out in batches
-  constexpr int kBatch = 6;
-  const int units = rows * ksteps * 16;
-  for (int u0 = 0; u0 < units; u0 += kBatch * kThreads) {
-    uint4 v[kBatch];
-#pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      const int u = u0 + b * kThreads + tid;
-      if (u < units) {
-        const int c = u & 15;
-        const int rest = u >> 4;
-        const int step = rest % ksteps;
-        const int m = rest / ksteps;
-        const int64_t k0 = static_cast<int64_t>(step) * 128 + c * 8;
-        v[b] = *reinterpret_cast<const uint4*>(g.a + row_index[m] * K + (k0 < K ? k0 : 0));
-        if (k0 >= K) v[b] = make_uint4(0u, 0u, 0u, 0u);
+  // unit u of a pass: ((local step * kRows) + row slot m) * 16 + c, so the 16
+  // units of one (row, step) sit in one 16-lane DPP row; slots m >= rows are
+  // skipped (their MFMA rows are never stored)
+  constexpr int kRowShift = MT == 1 ? 4 : 6;
+  static_assert(kRows == (1 << kRowShift), "tile rows must be 16 or 64");
+  auto unit_live = [&](int u) { return ((u >> 4) & (kRows - 1)) < rows; };
+  auto unit_load = [&](int p, int u) -> uint4 {
+    const int c = u & 15;
+    const int m = (u >> 4) & (kRows - 1);
+    const int ls = u >> (4 + kRowShift);
+    const int64_t k0 = static_cast<int64_t>(p * ps + ls) * 128 + c * 8;
+    uint4 v = *reinterpret_cast<const uint4*>(g.a + row_index[m] * K + (k0 < K ? k0 : 0));
+    if (k0 >= K) v = make_uint4(0u, 0u, 0u, 0u);
+    return v;
+  };
+  auto unit_store = [&](int b, int u, const uint4 v) {  // uniform per 16-lane row
+    const int c = u & 15;
+    const int m = (u >> 4) & (kRows - 1);
+    const int ls = u >> (4 + kRowShift);
+    const int ms = m >> 4, mr = m & 15;
+    const int t = WIDE ? (c & 3) : (c >> 2);
+    const int j = WIDE ? (c >> 2) : (c & 3);
+    const int frag = ((b * ps + ls) * MT + ms) * 4;
+    uint4* dst = &afrag[(frag + t) * kWave + j * 16 + (mr ^ (4 * t + j))];
+    if constexpr (kMx) {
+      *dst = v;
+    } else {
+      uint32_t q[4];
+      pair_x8(v, q);
+      *dst = make_uint4(q[0], q[1], q[2], q[3]);
+      float sx = sum_x8_dot(v);
+      if constexpr (WIDE) {
+        sx = sum8(sx);
+        sx += dpp_f32<kRowMirror>(sx);
+        if (c == 0) offs[frag * 16 + mr] = -kCodeOffset * sx;
+      } else {
+        sx = sum4(sx);
+        if (cg == 2) sx += dpp_f32<kRowHalfMirror>(sx);
+        if ((c & (4 * cg - 1)) == 0) offs[(frag + t / cg) * 16 + mr] = -kCodeOffset * sx;
       }
     }
+  };
+  auto pass_steps = [&](int p) { return min(ps, ksteps - p * ps); };
+
+  // 3. stage the first pass
+  {
+    constexpr int kBatch = 6;
+    const int units = pass_steps(0) * kRows * 16;
+    for (int u0 = 0; u0 < units; u0 += kBatch * kThreads) {
+      uint4 v[kBatch];
 #pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      const int u = u0 + b * kThreads + tid;
-      if (u < units) {  // uniform over each 16-lane row (units is a multiple of 16)
-        const int c = u & 15;
-        const int rest = u >> 4;
-        const int step = rest % ksteps;
-        const int m = rest / ksteps;
-        const int t = WIDE ? (c & 3) : (c >> 2);
-        const int j = WIDE ? (c >> 2) : (c & 3);
-        uint4* dst = &afrag[(step * 4 + t) * kWave + j * 16 + (m ^ (4 * t + j))];
-        if constexpr (kMx) {
-          *dst = v[b];
-        } else {
-          uint32_t p[4];
-          pair_x8(v[b], p);
-          *dst = make_uint4(p[0], p[1], p[2], p[3]);
-          float sx = sum_x8_dot(v[b]);
-          if constexpr (WIDE) {
-            sx = sum8(sx);
-            sx += dpp_f32<kRowMirror>(sx);
-            if (c == 0) offs[(step * 4) * 16 + m] = -kCodeOffset * sx;
-          } else {
-            sx = sum4(sx);
-            if (cg == 2) sx += dpp_f32<kRowHalfMirror>(sx);
-            if ((c & (4 * cg - 1)) == 0) offs[(step * 4 + t / cg) * 16 + m] = -kCodeOffset * sx;
-          }
-        }
+      for (int b = 0; b < kBatch; ++b) {
+        const int u = u0 + b * kThreads + tid;
+        if (u < units && unit_live(u)) v[b] = unit_load(0, u);
+      }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const int u = u0 + b * kThreads + tid;
+        if (u < units && unit_live(u)) unit_store(0, u, v[b]);
       }
     }
   }
@@ -813,109 +837,179 @@ w4a16_stream_kernel(const GemmArgs g) {
   // 4. stream: slot j of the ring holds step base + j and is refilled with
   // step base + j + kStDepth once consumed
   const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
-  f32x4_t tot[MATS][NT], acc[MATS][NT];
+  f32x4_t tot[MATS][NT][MT], acc[MATS][NT][MT];
 #pragma unroll
   for (int mi = 0; mi < MATS; ++mi)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      tot[mi][nt] = zero4;
-      acc[mi][nt] = zero4;
-    }
-  for (int base = 0; base < ksteps; base += kStDepth) {
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-    for (int j = 0; j < kStDepth; ++j) {
-      const int step = base + j;
-      if (step >= ksteps) break;
-      if constexpr (kMx) {
+      for (int ms = 0; ms < MT; ++ms) {
+        tot[mi][nt][ms] = zero4;
+        acc[mi][nt][ms] = zero4;
+      }
+  // one k-step: weights wj (a ring slot), activation buffer b, local step ls.
+  // Every subtile is computed (no per-MFMA branch): rows past the tile read
+  // stale LDS and produce rows that are never stored (MFMA rows are independent).
+  auto compute_step = [&](const WeightStep<FMT, MATS, NT, WIDE>& wj, int step, int b, int ls) {
+    const int frag0 = (b * ps + ls) * MT * 4;
+    if constexpr (kMx) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          if (static_cast<int64_t>(step) * 128 + 32 * t >= K) break;
-          const uint4 q = afrag[(step * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))];
+      for (int t = 0; t < 4; ++t) {
+        if (static_cast<int64_t>(step) * 128 + 32 * t >= K) break;
+#pragma unroll
+        for (int ms = 0; ms < MT; ++ms) {
+          const uint4 q = afrag[(frag0 + ms * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))];
           const u32x4_t av = {q.x, q.y, q.z, q.w};
 #pragma unroll
           for (int mi = 0; mi < MATS; ++mi)
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
-              const float sc = e8m0_to_f32(w[j].s[mi][nt][t]);
+              const float sc = e8m0_to_f32(wj.s[mi][nt][t]);
               if constexpr (FMT == kFmtMxBf16)
-                tot[mi][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                tot[mi][nt][ms] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                     __builtin_bit_cast(bf16x8_t, av),
-                    __builtin_bit_cast(bf16x8_t, unpack_fp4x8_bf16(w[j].w[mi][nt][t], sc)),
-                    tot[mi][nt], 0, 0, 0);
+                    __builtin_bit_cast(bf16x8_t, unpack_fp4x8_bf16(wj.w[mi][nt][t], sc)),
+                    tot[mi][nt][ms], 0, 0, 0);
               else
-                tot[mi][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                tot[mi][nt][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     __builtin_bit_cast(f16x8_t, av),
-                    __builtin_bit_cast(f16x8_t, unpack_fp4x8_f16(w[j].w[mi][nt][t], sc)),
-                    tot[mi][nt], 0, 0, 0);
-            }
-        }
-      } else if constexpr (WIDE) {
-        const bool first = (static_cast<int64_t>(step) * 128) % g.group == 0;
-        const bool last = (static_cast<int64_t>(step + 1) * 128) % g.group == 0;
-        const f32x4_t neg = *reinterpret_cast<const f32x4_t*>(&offs[(step * 4) * 16 + jq * 4]);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const bf16x8_t af = __builtin_bit_cast(
-              bf16x8_t, afrag[(step * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
-#pragma unroll
-          for (int mi = 0; mi < MATS; ++mi)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-              const f32x4_t cin = t > 0 ? acc[mi][nt] : (first ? neg : acc[mi][nt] + neg);
-              acc[mi][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                  af, unpack_q8(w[j].w[mi][nt][t]), cin, 0, 0, 0);
-            }
-        }
-        if (last) {
-#pragma unroll
-          for (int mi = 0; mi < MATS; ++mi)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-              tot[mi][nt] += bf16_to_f32(static_cast<uint16_t>(w[j].s[mi][nt][0])) * acc[mi][nt];
-        }
-      } else {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          if (static_cast<int64_t>(step) * 128 + 32 * t >= K) break;
-          const bool first = (t % cg) == 0;
-          const bool last = ((t + 1) % cg) == 0;
-          const bf16x8_t af = __builtin_bit_cast(
-              bf16x8_t, afrag[(step * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
-          f32x4_t neg = zero4;
-          if (first)
-            neg = *reinterpret_cast<const f32x4_t*>(&offs[(step * 4 + t / cg) * 16 + jq * 4]);
-#pragma unroll
-          for (int mi = 0; mi < MATS; ++mi)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-              const f32x4_t cin = first ? neg : acc[mi][nt];
-              acc[mi][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                  af, unpack_q8(w[j].w[mi][nt][t]), cin, 0, 0, 0);
-              if (last)
-                tot[mi][nt] += bf16_to_f32(static_cast<uint16_t>(w[j].s[mi][nt][t])) * acc[mi][nt];
+                    __builtin_bit_cast(f16x8_t, unpack_fp4x8_f16(wj.w[mi][nt][t], sc)),
+                    tot[mi][nt][ms], 0, 0, 0);
             }
         }
       }
-      if (step + kStDepth < ksteps) w[j].load(wrow, srow, step + kStDepth, jq, K, g.group);
+    } else if constexpr (WIDE) {
+      // G == 128: the step is one whole group; its chain starts from the offset
+      f32x4_t neg[MT];
+#pragma unroll
+      for (int ms = 0; ms < MT; ++ms)
+        neg[ms] = *reinterpret_cast<const f32x4_t*>(&offs[(frag0 + ms * 4) * 16 + jq * 4]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        bf16x8_t af[MT];
+#pragma unroll
+        for (int ms = 0; ms < MT; ++ms)
+          af[ms] = __builtin_bit_cast(
+              bf16x8_t, afrag[(frag0 + ms * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
+#pragma unroll
+        for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            const bf16x8_t bv = unpack_q8(wj.w[mi][nt][t]);
+#pragma unroll
+            for (int ms = 0; ms < MT; ++ms)
+              acc[mi][nt][ms] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  af[ms], bv, t > 0 ? acc[mi][nt][ms] : neg[ms], 0, 0, 0);
+          }
+      }
+#pragma unroll
+      for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const float sc = bf16_to_f32(static_cast<uint16_t>(wj.s[mi][nt][0]));
+#pragma unroll
+          for (int ms = 0; ms < MT; ++ms) tot[mi][nt][ms] += sc * acc[mi][nt][ms];
+        }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (static_cast<int64_t>(step) * 128 + 32 * t >= K) break;
+        const bool first = (t % cg) == 0;
+        const bool last = ((t + 1) % cg) == 0;
+        bf16x8_t af[MT];
+        f32x4_t neg[MT];
+#pragma unroll
+        for (int ms = 0; ms < MT; ++ms) {
+          af[ms] = __builtin_bit_cast(
+              bf16x8_t, afrag[(frag0 + ms * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
+          neg[ms] = first ? *reinterpret_cast<const f32x4_t*>(
+                                &offs[(frag0 + ms * 4 + t / cg) * 16 + jq * 4])
+                          : zero4;
+        }
+#pragma unroll
+        for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            const bf16x8_t bv = unpack_q8(wj.w[mi][nt][t]);
+            const float sc = bf16_to_f32(static_cast<uint16_t>(wj.s[mi][nt][t]));
+#pragma unroll
+            for (int ms = 0; ms < MT; ++ms) {
+              acc[mi][nt][ms] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  af[ms], bv, first ? neg[ms] : acc[mi][nt][ms], 0, 0, 0);
+              if (last) tot[mi][nt][ms] += sc * acc[mi][nt][ms];
+            }
+          }
+      }
+    }
+  };
+
+  if constexpr (MT == 1) {
+    // 16-row tiles: all activations are resident; a ring kStDepth deep
+    for (int base = 0; base < ksteps; base += kStDepth) {
+#pragma unroll
+      for (int j = 0; j < kStDepth; ++j) {
+        const int step = base + j;
+        if (step >= ksteps) break;
+        compute_step(w[j], step, 0, step);
+        if (step + kStDepth < ksteps) w[j].load(wrow, srow, step + kStDepth, jq, K, g.group);
+      }
+    }
+  } else {
+    // 64-row tiles: passes of kStPassSteps k-steps; the ring is one pass deep
+    // (its first kStPassSteps slots), so slot j serves local step j
+    const int passes = (ksteps + ps - 1) / ps;
+    uint4 vnext[kPassUnits];  // the next pass, in flight during this one
+    for (int p = 0; p < passes; ++p) {
+      const int b = p % kNBuf;
+      const bool more = p + 1 < passes;
+      const int units1 = more ? pass_steps(p + 1) * kRows * 16 : 0;
+      if (more) {
+#pragma unroll
+        for (int q = 0; q < kPassUnits; ++q) {
+          const int u = q * kThreads + tid;
+          if (u < units1 && unit_live(u)) vnext[q] = unit_load(p + 1, u);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kStPassSteps; ++j) {
+        const int step = p * ps + j;
+        if (step >= ksteps) break;
+        compute_step(w[j], step, b, j);
+        if (step + kStPassSteps < ksteps) w[j].load(wrow, srow, step + kStPassSteps, jq, K, g.group);
+      }
+      if (more) {
+        // publish the next pass; the barrier also retires this pass's buffer,
+        // which the pass after next overwrites
+#pragma unroll
+        for (int q = 0; q < kPassUnits; ++q) {
+          const int u = q * kThreads + tid;
+          if (u < units1 && unit_live(u)) unit_store((p + 1) % kNBuf, u, vnext[q]);
+        }
+        __syncthreads();
+      }
     }
   }
 
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = jq * 4 + i;
-    if (m >= rows) continue;
-    const int64_t orow = SCATTER ? static_cast<int64_t>(g.perm[row0 + m]) : row0 + m;
+  for (int ms = 0; ms < MT; ++ms) {
+    if (ms >= mt_act) break;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      if (col[nt] >= N) continue;
-      uint16_t v;
-      if constexpr (MATS == 2)
-        v = g.act == kActSitu ? situ_bf16(tot[0][nt][i], tot[1][nt][i], g.situ_beta,
-                                          g.situ_linear_beta)
-                              : swiglu_bf16(tot[0][nt][i], tot[1][nt][i]);
-      else
-        v = store_value<FMT>(tot[0][nt][i]);
-      out[orow * N + col[nt]] = v;
+    for (int i = 0; i < 4; ++i) {
+      const int m = ms * 16 + jq * 4 + i;
+      if (m >= rows) continue;
+      const int64_t orow = SCATTER ? static_cast<int64_t>(g.perm[row0 + m]) : row0 + m;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        if (col[nt] >= N) continue;
+        uint16_t v;
+        if constexpr (MATS == 2)
+          v = g.act == kActSitu ? situ_bf16(tot[0][nt][ms][i], tot[1][nt][ms][i], g.situ_beta,
+                                            g.situ_linear_beta)
+                                : swiglu_bf16(tot[0][nt][ms][i], tot[1][nt][ms][i]);
+        else
+          v = store_value<FMT>(tot[0][nt][ms][i]);
+        out[orow * N + col[nt]] = v;
+      }
     }
   }
 }
@@ -1096,69 +1190,58 @@ int gemm_launch(GemmArgs g, Mode mode, int64_t tiles, bool wide_cols, hipStream_
   return check_launch(what);
 }
 
-template <int FMT, int MATS, bool WIDE>
-void stream_dispatch(const GemmArgs& g, Mode mode, unsigned blocks, size_t lds, hipStream_t s) {
+template <int FMT, int MATS, int MT, bool WIDE, bool GATHER, bool SCATTER, bool DENSE>
+void stream_one(const GemmArgs& g, unsigned blocks, size_t lds, hipStream_t s) {
   constexpr int NT = MATS == 2 ? 1 : 2;
-  constexpr int T = kStWaves * kWave;
+  auto* fn = &w4a16_stream_kernel<FMT, MATS, NT, MT, WIDE, GATHER, SCATTER, DENSE>;
+  static bool limit_set = false;  // the attribute is per function; set once per process
+  if (!limit_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kStMaxLds);
+    limit_set = true;
+  }
+  fn<<<blocks, kStWaves * kWave, lds, s>>>(g);
+}
+
+template <int FMT, int MATS, int MT, bool WIDE>
+void stream_dispatch(const GemmArgs& g, Mode mode, unsigned blocks, size_t lds, hipStream_t s) {
   if constexpr (FMT == kFmtMxF16) {
-    w4a16_stream_kernel<FMT, MATS, NT, false, false, false, true><<<blocks, T, lds, s>>>(g);
+    stream_one<FMT, MATS, MT, false, false, false, true>(g, blocks, lds, s);
   } else {
     switch (mode) {
-      case Mode::Gather:
-        w4a16_stream_kernel<FMT, MATS, NT, WIDE, true, false, false><<<blocks, T, lds, s>>>(g);
-        break;
-      case Mode::Scatter:
-        w4a16_stream_kernel<FMT, MATS, NT, WIDE, false, true, false><<<blocks, T, lds, s>>>(g);
-        break;
+      case Mode::Gather: stream_one<FMT, MATS, MT, WIDE, true, false, false>(g, blocks, lds, s); break;
+      case Mode::Scatter: stream_one<FMT, MATS, MT, WIDE, false, true, false>(g, blocks, lds, s); break;
       case Mode::GatherScatter:
-        w4a16_stream_kernel<FMT, MATS, NT, WIDE, true, true, false><<<blocks, T, lds, s>>>(g);
+        stream_one<FMT, MATS, MT, WIDE, true, true, false>(g, blocks, lds, s);
         break;
-      case Mode::Dense:
-        w4a16_stream_kernel<FMT, MATS, NT, WIDE, false, false, true><<<blocks, T, lds, s>>>(g);
-        break;
+      case Mode::Dense: stream_one<FMT, MATS, MT, WIDE, false, false, true>(g, blocks, lds, s); break;
     }
   }
 }
 
-// The streaming kernel needs the whole reduction of a 16-row tile in LDS.
-bool stream_fits(int64_t k) { return stream_lds_bytes(k) <= static_cast<size_t>(kStMaxLds); }
-
-template <int FMT, int MATS, bool WIDE>
-void stream_set_lds_limit() {
-  constexpr int NT = MATS == 2 ? 1 : 2;
-  static bool done = false;  // once per process (the attribute is per function)
-  if (done) return;
-  done = true;
-  (void)hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&w4a16_stream_kernel<FMT, MATS, NT, WIDE, true, false, false>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, kStMaxLds);
-  (void)hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&w4a16_stream_kernel<FMT, MATS, NT, WIDE, false, true, false>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, kStMaxLds);
-  (void)hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&w4a16_stream_kernel<FMT, MATS, NT, WIDE, true, true, false>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, kStMaxLds);
-  (void)hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&w4a16_stream_kernel<FMT, MATS, NT, WIDE, false, false, true>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, kStMaxLds);
+// Whether the streaming kernel with 16 * mt-row tiles covers this reduction
+// (W4A16 groups of 32, 64 or 128, or MXFP4; wider groups use the LDS-staged kernel).
+bool stream_fits(int64_t k, int mt, int64_t group, bool mx) {
+  if (!mx && group > 128) return false;
+  return stream_lds_bytes(k, mt) <= static_cast<size_t>(kStMaxLds);
 }
 
 template <int FMT, int MATS>
-int stream_launch(GemmArgs g, Mode mode, int64_t tiles, hipStream_t s, const char* what) {
+int stream_launch(GemmArgs g, Mode mode, int64_t tiles, int mt, hipStream_t s, const char* what) {
   constexpr int NT = MATS == 2 ? 1 : 2;
   const bool wide = FMT == kFmtW4A16 && g.group >= 128;
-  const size_t lds = stream_lds_bytes(g.k);
+  const size_t lds = stream_lds_bytes(g.k, mt);
   LK_REQUIRE(lds <= static_cast<size_t>(kStMaxLds), "%s: reduction width too large", what);
   g.col_blocks = static_cast<int>((g.n + kStWaves * NT * 16 - 1) / (kStWaves * NT * 16));
   const int64_t blocks = (tiles + 7) / 8 * 8 * g.col_blocks * g.outputs;
   LK_REQUIRE(blocks > 0 && blocks < (1LL << 31), "%s: too many blocks", what);
   const unsigned nb = static_cast<unsigned>(blocks);
-  if (wide) {
-    stream_set_lds_limit<FMT, MATS, FMT == kFmtW4A16>();
-    stream_dispatch<FMT, MATS, FMT == kFmtW4A16>(g, mode, nb, lds, s);
+  if (mt == 1) {
+    if (wide) stream_dispatch<FMT, MATS, 1, FMT == kFmtW4A16>(g, mode, nb, lds, s);
+    else stream_dispatch<FMT, MATS, 1, false>(g, mode, nb, lds, s);
   } else {
-    stream_set_lds_limit<FMT, MATS, false>();
-    stream_dispatch<FMT, MATS, false>(g, mode, nb, lds, s);
+    if (wide) stream_dispatch<FMT, MATS, 4, FMT == kFmtW4A16>(g, mode, nb, lds, s);
+    else stream_dispatch<FMT, MATS, 4, false>(g, mode, nb, lds, s);
   }
   return check_launch(what);
 }
@@ -1182,22 +1265,25 @@ int launch_fmt(bool mx, const GemmArgs& g, Mode mode, int64_t tiles, bool wide_c
 }
 
 template <int MATS>
-int stream_fmt(bool mx, const GemmArgs& g, Mode mode, int64_t tiles, hipStream_t s,
+int stream_fmt(bool mx, const GemmArgs& g, Mode mode, int64_t tiles, int mt, hipStream_t s,
                const char* what) {
-  if (mx) return stream_launch<kFmtMxBf16, MATS>(g, mode, tiles, s, what);
-  return stream_launch<kFmtW4A16, MATS>(g, mode, tiles, s, what);
+  if (mx) return stream_launch<kFmtMxBf16, MATS>(g, mode, tiles, mt, s, what);
+  return stream_launch<kFmtW4A16, MATS>(g, mode, tiles, mt, s, what);
 }
 
-// Token-routes up to which expert-major calls use the streaming kernel on
-// 16-row tiles (decode batches); larger calls use the LDS-staged kernel on
-// 64-row tiles. LK_MOE_GEMM=stream|lds forces one path.
-constexpr int64_t kStreamMaxEntries = 2048;
+// Expert-major calls use the streaming kernel: 16-row tiles up to
+// kStreamSmallEntries token-routes (decode batches, few rows per expert),
+// 64-row tiles above (prefill). LK_MOE_GEMM=lds selects the LDS-staged
+// kernel instead, LK_MOE_GEMM=stream16|stream64 forces a tile height.
+constexpr int64_t kStreamSmallEntries = 2048;
 
-bool use_stream(int64_t entries) {
+// 16-row tiles -> 1, 64-row tiles -> 4, the LDS-staged kernel -> 0.
+int stream_tile_mt(int64_t entries) {
   const char* env = getenv("LK_MOE_GEMM");
-  if (env && strcmp(env, "lds") == 0) return false;
-  if (env && strcmp(env, "stream") == 0) return true;
-  return entries <= kStreamMaxEntries;
+  if (env && strcmp(env, "lds") == 0) return 0;
+  if (env && strcmp(env, "stream16") == 0) return 1;
+  if (env && strcmp(env, "stream64") == 0) return 4;
+  return entries <= kStreamSmallEntries ? 1 : 4;
 }
 
 // W4A16: a power-of-two group (multiple of 32) dividing k; MXFP4: 32.
@@ -1296,8 +1382,9 @@ static int grouped_gemm_common(bool mx, const uint16_t* x, const int64_t* idx, c
   auto* perm = reinterpret_cast<int32_t*>(ws + l.perm);
   auto* tiles = reinterpret_cast<int32_t*>(ws + l.tiles);
   auto* count = reinterpret_cast<int32_t*>(ws + l.count);
-  const bool small = use_stream(entries) && stream_fits(k);
-  const int tr = small ? kSmallTileRows : kTileRows;
+  int mt = stream_tile_mt(entries);
+  if (mt && !stream_fits(k, mt, group, mx)) mt = 0;
+  const int tr = mt == 1 ? kSmallTileRows : kTileRows;
   const RouteTable rt{idx, routes, routes, experts, -1};
   if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, tr, s))
     return rc;
@@ -1321,14 +1408,14 @@ static int grouped_gemm_common(bool mx, const uint16_t* x, const int64_t* idx, c
   g.routes = routes;
   g.outputs = 1;
   g.act = kActSwiglu;
-  const int64_t mt = max_tiles_for(entries, experts, tr);
-  if (small) {
-    if (swiglu) return stream_fmt<2>(mx, g, Mode::GatherScatter, mt, s, name);
-    return stream_fmt<1>(mx, g, Mode::GatherScatter, mt, s, name);
+  const int64_t tiles_bound = max_tiles_for(entries, experts, tr);
+  if (mt) {
+    if (swiglu) return stream_fmt<2>(mx, g, Mode::GatherScatter, tiles_bound, mt, s, name);
+    return stream_fmt<1>(mx, g, Mode::GatherScatter, tiles_bound, mt, s, name);
   }
-  const bool wc = wide_cols_for(mt, n);
-  if (swiglu) return launch_fmt<2>(mx, g, Mode::GatherScatter, mt, wc, s, name);
-  return launch_fmt<1>(mx, g, Mode::GatherScatter, mt, wc, s, name);
+  const bool wc = wide_cols_for(tiles_bound, n);
+  if (swiglu) return launch_fmt<2>(mx, g, Mode::GatherScatter, tiles_bound, wc, s, name);
+  return launch_fmt<1>(mx, g, Mode::GatherScatter, tiles_bound, wc, s, name);
 }
 
 int lk_w4a16_grouped_gemm(const uint16_t* x, const int64_t* expert_indices,
@@ -1535,8 +1622,9 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   auto* act = reinterpret_cast<uint16_t*>(ws + l.act);
   auto* eo = reinterpret_cast<uint16_t*>(ws + l.eo);
   const int64_t group = mx ? 32 : group_size;
-  const bool small = use_stream(entries) && stream_fits(h) && stream_fits(i);
-  const int tr = small ? kSmallTileRows : kTileRows;
+  int mt = stream_tile_mt(entries);
+  if (mt && !(stream_fits(h, mt, group, mx) && stream_fits(i, mt, group, mx))) mt = 0;
+  const int tr = mt == 1 ? kSmallTileRows : kTileRows;
   const RouteTable rt{expert_indices, top_k, routes, experts, experts - 1};
   if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, tr, s))
     return rc;
@@ -1562,10 +1650,10 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.k = h;
   g.wstride = i * h / 2;
   g.sstride = i * (h / group);
-  const int64_t mt = max_tiles_for(entries, experts, tr);
-  if (int rc = small ? stream_fmt<2>(mx, g, Mode::Gather, mt, s, "moe gate/up gemm")
-                     : launch_fmt<2>(mx, g, Mode::Gather, mt, wide_cols_for(mt, i), s,
-                                     "moe gate/up gemm"))
+  const int64_t tb = max_tiles_for(entries, experts, tr);
+  if (int rc = mt ? stream_fmt<2>(mx, g, Mode::Gather, tb, mt, s, "moe gate/up gemm")
+                  : launch_fmt<2>(mx, g, Mode::Gather, tb, wide_cols_for(tb, i), s,
+                                  "moe gate/up gemm"))
     return rc;
   // down projection: sorted activation rows, outputs scattered to (token, route) rows
   g.a = act;
@@ -1576,9 +1664,9 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.k = i;
   g.wstride = h * i / 2;
   g.sstride = h * (i / group);
-  if (int rc = small ? stream_fmt<1>(mx, g, Mode::Scatter, mt, s, "moe down gemm")
-                     : launch_fmt<1>(mx, g, Mode::Scatter, mt, wide_cols_for(mt, h), s,
-                                     "moe down gemm"))
+  if (int rc = mt ? stream_fmt<1>(mx, g, Mode::Scatter, tb, mt, s, "moe down gemm")
+                  : launch_fmt<1>(mx, g, Mode::Scatter, tb, wide_cols_for(tb, h), s,
+                                  "moe down gemm"))
     return rc;
   const int64_t work = tokens * (h / 8);
   moe_combine_kernel<<<static_cast<unsigned>((work + 255) / 256), 256, 0, s>>>(
