@@ -267,10 +267,59 @@ def run_dense(args, dev) -> dict:
     return result
 
 
-def _layer_banks(layers: int, gen: torch.Generator, dev):
-    master = (*make_bank(INTER, H, E_ROUTED + 1, gen, dev), *make_bank(INTER, H, E_ROUTED + 1, gen, dev),
-              *make_bank(H, INTER, E_ROUTED + 1, gen, dev))
+def make_mx_bank(rows: int, cols: int, experts: int, gen: torch.Generator, dev):
+    from local_kimi_amd.quant import quantize_mxfp4
+
+    packed = torch.empty((experts, rows, cols // 2), dtype=torch.uint8, device=dev)
+    scale = torch.empty((experts, rows, cols // 32), dtype=torch.uint8, device=dev)
+    for e in range(experts):
+        w = (torch.randn((rows, cols), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        p, sc = quantize_mxfp4(w)
+        packed[e].copy_(p)
+        scale[e].copy_(sc)
+    return packed, scale
+
+
+MX_EXPERT_BYTES = 3 * (INTER * H // 2 + INTER * (H // 32))   # 3,760,128
+
+
+def _layer_banks(layers: int, gen: torch.Generator, dev, weights: str = "w4a16"):
+    mk = make_mx_bank if weights == "mxfp4" else make_bank
+    master = (*mk(INTER, H, E_ROUTED + 1, gen, dev), *mk(INTER, H, E_ROUTED + 1, gen, dev),
+              *mk(H, INTER, E_ROUTED + 1, gen, dev))
     return [master] + [tuple(t.clone() for t in master) for _ in range(layers - 1)]
+
+
+def _block_fn(weights: str, path: str = "expert"):
+    from local_kimi_amd.kernels import mxfp4_moe_block, w4a16_moe_decode, w4a16_moe_forward
+
+    if weights == "mxfp4":
+        return mxfp4_moe_block
+    return w4a16_moe_forward if path == "expert" else w4a16_moe_decode
+
+
+def cpu_baseline_block(banks_l0, xs, logits, tokens: int, weights: str) -> dict:
+    """Oracle block for `tokens` tokens of the step on one host thread."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import moe as OM
+    from oracle import mxfp4 as OX
+
+    host = [t.cpu().numpy() if t.dtype == torch.uint8 else
+            t.cpu().view(torch.int16).numpy().view(np.uint16) for t in banks_l0]
+    x = xs[:tokens].cpu().view(torch.int16).numpy().view(np.uint16)
+    lg = logits[:tokens].cpu().numpy()
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        if weights == "mxfp4":
+            OX.moe_block(x, lg, None, *host, top_k=TOP_K, routed_scaling_factor=SCALING)
+        else:
+            OM.moe_block(x, lg, None, *host, top_k=TOP_K, routed_scaling_factor=SCALING, group_size=G)
+        dt = time.perf_counter() - t0
+    return {"value": round(dt * 1e6 / tokens, 1), "unit": "us/token", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle of the MoE block ({weights}: router, dequantise the routed "
+                      f"experts, gate/up, SwiGLU, W2, combine) for {tokens} tokens of the step "
+                      "on one host thread"}
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
@@ -279,17 +328,15 @@ EXPERT_FLOPS = 2 * 3 * INTER * H  # gate, up and down projections per routed row
 
 def run_moe_batched(args, dev) -> dict:
     """Batched decode: M tokens per step, Zipf(1.1)-skewed routing, expert-major path."""
-    from local_kimi_amd.kernels import w4a16_moe_decode, w4a16_moe_forward
     from local_kimi_amd.workloads import zipf_router_logits
     from oracle import moe as OM
-
-    block = w4a16_moe_forward if args.moe_path == "expert" else w4a16_moe_decode
 
     m, layers = args.tokens, args.layers
     gen = torch.Generator(device=dev).manual_seed(20260729)
     rng = np.random.default_rng(20260729)
     t0 = time.time()
-    banks = _layer_banks(layers, gen, dev)
+    banks = _layer_banks(layers, gen, dev, args.weights)
+    block = _block_fn(args.weights, args.moe_path)
     xs = [(torch.randn((m, H), device=dev, generator=gen)).to(torch.bfloat16) for _ in range(layers)]
     host_logits = [zipf_router_logits(rng, m, E_ROUTED) for _ in range(layers)]
     logits = [torch.from_numpy(lg).to(dev) for lg in host_logits]
@@ -311,20 +358,21 @@ def run_moe_batched(args, dev) -> dict:
     ms = time_graph(graph, reps, stream)
     steps = reps * layers
     us_step = ms * 1000.0 / steps
-    step_bytes = float(np.mean([(u + 1) * EXPERT_BYTES for u in unions])) + m * TOKEN_IO_BYTES
+    ebytes = MX_EXPERT_BYTES if args.weights == "mxfp4" else EXPERT_BYTES
+    step_bytes = float(np.mean([(u + 1) * ebytes for u in unions])) + m * TOKEN_IO_BYTES
     step_flops = m * (TOP_K + 1) * EXPERT_FLOPS
     gbps = step_bytes / (us_step * 1e3)
-    return {
-        "metric": "Batched MoE decode us/step + achieved HBM GB/s (% of peak) at W4A16",
+    result = {
+        "metric": f"Batched MoE decode us/step + achieved HBM GB/s (% of peak) at {args.weights.upper()}",
         "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": steps,
         "warmup": warm * layers, "ms_per_step": round(ms / steps, 6), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x, "
-                "Zipf(1.1) router logits (log p + Gumbel)",
-        "config": {"workload": f"moe_batched_decode_m{m}", "path": f"{args.moe_path}-major",
-                   "tokens_per_step": m, "hidden": H,
+        "data": f"synthetic: N(0,0.02) weights quantised {_weights_desc(args.weights)} on the GPU, "
+                "N(0,1) x, Zipf(1.1) router logits (log p + Gumbel)",
+        "config": {"workload": f"moe_batched_decode_m{m}", "weights": args.weights,
+                   "path": f"{args.moe_path}-major", "tokens_per_step": m, "hidden": H,
                    "routed_experts": E_ROUTED, "shared_experts": 1, "moe_intermediate": INTER,
-                   "top_k": TOP_K, "group_size": G, "layer_banks_rotated": layers,
+                   "top_k": TOP_K, "layer_banks_rotated": layers,
                    "mean_distinct_routed_experts": round(float(np.mean(unions)), 2)},
         "us_per_token": round(us_step / m, 3),
         "achieved_gbps": round(gbps, 1),
@@ -335,22 +383,30 @@ def run_moe_batched(args, dev) -> dict:
                      "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "mfma_tflops": round(step_flops / (us_step * 1e6), 2)},
     }
+    if args.cpu_sample > 0:
+        log(f"[bench] timing the CPU oracle on {min(args.cpu_sample, m)} tokens")
+        result["cpu_baseline"] = cpu_baseline_block(banks[0], xs[0], logits[0], min(args.cpu_sample, m),
+                                                    args.weights)
+    return result
+
+
+def _weights_desc(weights: str) -> str:
+    return "OCP MXFP4 (E2M1, E8M0 per 32)" if weights == "mxfp4" else "W4A16 g128"
 
 
 def run_moe_prefill(args, dev) -> dict:
     """Prefill: 2048 tokens x top-8 (+ shared) through one layer, N(0,1) logits."""
-    from local_kimi_amd.kernels import w4a16_moe_forward
-
     m = args.prefill_tokens
     gen = torch.Generator(device=dev).manual_seed(20260729)
-    banks = _layer_banks(2, gen, dev)
+    banks = _layer_banks(2, gen, dev, args.weights)
+    block = _block_fn(args.weights)
     xs = [(torch.randn((m, H), device=dev, generator=gen)).to(torch.bfloat16) for _ in range(2)]
     logits = [torch.randn((m, E_ROUTED), device=dev, generator=gen) for _ in range(2)]
     stream = torch.cuda.Stream(device=dev)
 
     def both():
         for l in range(2):
-            w4a16_moe_forward(xs[l], logits[l], None, *banks[l], TOP_K, SCALING)
+            block(xs[l], logits[l], None, *banks[l], TOP_K, SCALING)
 
     graph = capture(both, stream)
     reps = max(1, args.prefill_steps // 2)
@@ -359,18 +415,21 @@ def run_moe_prefill(args, dev) -> dict:
     ms = time_graph(graph, reps, stream)
     steps = 2 * reps
     us = ms * 1000.0 / steps
-    nbytes = (E_ROUTED + 1) * EXPERT_BYTES + m * TOKEN_IO_BYTES
+    ebytes = MX_EXPERT_BYTES if args.weights == "mxfp4" else EXPERT_BYTES
+    nbytes = (E_ROUTED + 1) * ebytes + m * TOKEN_IO_BYTES
     flops = m * (TOP_K + 1) * EXPERT_FLOPS
     tflops = flops / (us * 1e6)
     gbps = nbytes / (us * 1e3)
-    return {
-        "metric": "MoE prefill us/layer + MFMA TFLOP/s and HBM GB/s at W4A16",
+    result = {
+        "metric": f"MoE prefill us/layer + MFMA TFLOP/s and HBM GB/s at {args.weights.upper()}",
         "value": round(us, 2), "unit": "us/layer", "n_gpus": 1, "steps": steps, "warmup": 6,
         "ms_per_step": round(ms / steps, 6), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x and logits",
-        "config": {"workload": f"moe_prefill_{m}", "tokens": m, "hidden": H, "routed_experts": E_ROUTED,
-                   "shared_experts": 1, "moe_intermediate": INTER, "top_k": TOP_K, "group_size": G},
+        "data": f"synthetic: N(0,0.02) weights quantised {_weights_desc(args.weights)} on the GPU, "
+                "N(0,1) x and logits",
+        "config": {"workload": f"moe_prefill_{m}", "weights": args.weights, "tokens": m, "hidden": H,
+                   "routed_experts": E_ROUTED, "shared_experts": 1, "moe_intermediate": INTER,
+                   "top_k": TOP_K},
         "tokens_per_s": round(m / (us * 1e-6), 1),
         "achieved_gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
         "achieved_tflops": round(tflops, 1),
@@ -381,6 +440,11 @@ def run_moe_prefill(args, dev) -> dict:
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                      "traffic": None, "hbm_gbps": round(gbps, 1)},
     }
+    if args.cpu_sample > 0:
+        n = min(args.cpu_sample, m)
+        log(f"[bench] timing the CPU oracle on {n} tokens")
+        result["cpu_baseline"] = cpu_baseline_block(banks[0], xs[0], logits[0], n, args.weights)
+    return result
 
 
 def run_qkv_prefill(args, dev) -> dict:
@@ -406,7 +470,7 @@ def run_qkv_prefill(args, dev) -> dict:
     nbytes = 3 * w4a16_bytes(n, H) + m * H * 2 + 3 * m * n * 2
     flops = 2 * m * H * 3 * n
     tflops = flops / (us * 1e6)
-    return {
+    result = {
         "metric": "Fused QKV prefill GEMM us + MFMA TFLOP/s at W4A16",
         "value": round(us, 2), "unit": "us/call", "n_gpus": 1, "steps": reps, "warmup": 3,
         "ms_per_step": round(ms / reps, 6), "higher_is_better": False, "scaling": "weak",
@@ -418,10 +482,28 @@ def run_qkv_prefill(args, dev) -> dict:
         "pct_mfma_peak": round(100 * tflops / MFMA_BF16_PEAK_TFLOPS, 2),
         "achieved_gbps": round(nbytes / (us * 1e3), 1),
         "algorithmic_bytes_per_step": nbytes, "flops_per_step": flops,
-        "roofline": {"kernel": "w4a16_gemm_kernel (dense, 3 outputs)", "bound": "mfma",
+        "roofline": {"kernel": "dense W4A16 GEMM (3 outputs, one launch)", "bound": "mfma",
                      "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None},
     }
+    if args.cpu_sample > 0:
+        from threadpoolctl import threadpool_limits
+
+        from oracle import w4a16 as OW
+
+        rows = min(args.cpu_sample, m)
+        host = [t.cpu().numpy() if t.dtype == torch.uint8 else
+                t.cpu().view(torch.int16).numpy().view(np.uint16) for t in mats]
+        xb = x[:rows].cpu().view(torch.int16).numpy().view(np.uint16)
+        with threadpool_limits(1):
+            t0 = time.perf_counter()
+            OW.fused_qkv(xb, *host, G)
+            dt = time.perf_counter() - t0
+        result["cpu_baseline"] = {
+            "value": round(dt * 1e6 / rows, 1), "unit": "us/token", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle fused QKV (dequantise 3 x [4096, 2304] + matmul) for {rows} "
+                      "rows on one host thread"}
+    return result
 
 
 def run_copy(args, dev) -> dict:
@@ -455,6 +537,8 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=64, help="moe_batched tokens per step")
     ap.add_argument("--moe-path", choices=["expert", "token"], default="expert",
                     help="moe_batched: expert-major GEMMs or the token-major GEMV kernels")
+    ap.add_argument("--weights", choices=["w4a16", "mxfp4"], default="w4a16",
+                    help="moe_batched / moe_prefill expert weight format")
     ap.add_argument("--prefill-tokens", type=int, default=2048)
     ap.add_argument("--prefill-steps", type=int, default=40)
     ap.add_argument("--copy-mb", type=int, default=256, help="copy workload size (MiB)")
