@@ -285,7 +285,9 @@ __device__ inline float sum_x8_dot(const uint4 v) {
 
 // One 128-wide k-step of a lane's weights: 4 packed dwords (one per MFMA) and
 // the scale of the group each MFMA belongs to, per matrix and column tile.
-// W4A16 with G >= 128 (WIDE): one 16-byte load, one group per step.
+// WIDE: one 16-byte load of 32 consecutive codes; dword t feeds MFMA t. For
+// W4A16 (G >= 128) the step lies in one group; for MXFP4 the 32 codes are
+// exactly one E8M0 block, so one scale byte serves all four dwords.
 // Otherwise each MFMA covers 32 consecutive codes (one dword per lane).
 template <int FMT, int MATS, int NT, bool WIDE>
 struct WeightStep {
@@ -306,8 +308,11 @@ struct WeightStep {
           w[mi][nt][1] = v.y;
           w[mi][nt][2] = v.z;
           w[mi][nt][3] = v.w;
-          s[mi][nt][0] = static_cast<const uint16_t*>(
-              srow[mi][nt])[static_cast<int64_t>(step) * 128 / group];
+          if constexpr (FMT == kFmtW4A16)
+            s[mi][nt][0] = static_cast<const uint16_t*>(
+                srow[mi][nt])[static_cast<int64_t>(step) * 128 / group];
+          else
+            s[mi][nt][0] = static_cast<const uint8_t*>(srow[mi][nt])[static_cast<int64_t>(step) * 4 + jq];
         } else {
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
@@ -679,7 +684,7 @@ template <int FMT, int MATS, int NT, int MT, bool WIDE, bool GATHER, bool SCATTE
 __global__ void __launch_bounds__(kStWaves * kWave, 2)
 w4a16_stream_kernel(const GemmArgs g) {
   constexpr bool kMx = FMT != kFmtW4A16;
-  static_assert(!(kMx && WIDE), "MXFP4 groups are 32 wide");
+  static_assert(!(FMT == kFmtMxF16 && WIDE), "fp16 activations use the narrow layout");
   constexpr int kThreads = kStWaves * kWave;
   constexpr int kBN = kStWaves * NT * 16;
   constexpr int kRows = 16 * MT;
@@ -852,7 +857,33 @@ w4a16_stream_kernel(const GemmArgs g) {
   // stale LDS and produce rows that are never stored (MFMA rows are independent).
   auto compute_step = [&](const WeightStep<FMT, MATS, NT, WIDE>& wj, int step, int b, int ls) {
     const int frag0 = (b * ps + ls) * MT * 4;
-    if constexpr (kMx) {
+    if constexpr (kMx && WIDE) {
+      // k % 128 == 0: every sub-step is real; the lane's block scale is decoded once
+      float sc[MATS][NT];
+#pragma unroll
+      for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) sc[mi][nt] = e8m0_to_f32(wj.s[mi][nt][0]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        bf16x8_t af[MT];
+#pragma unroll
+        for (int ms = 0; ms < MT; ++ms)
+          af[ms] = __builtin_bit_cast(
+              bf16x8_t, afrag[(frag0 + ms * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
+#pragma unroll
+        for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            const bf16x8_t bv =
+                __builtin_bit_cast(bf16x8_t, unpack_fp4x8_bf16(wj.w[mi][nt][t], sc[mi][nt]));
+#pragma unroll
+            for (int ms = 0; ms < MT; ++ms)
+              tot[mi][nt][ms] =
+                  __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ms], bv, tot[mi][nt][ms], 0, 0, 0);
+          }
+      }
+    } else if constexpr (kMx) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         if (static_cast<int64_t>(step) * 128 + 32 * t >= K) break;
@@ -1229,7 +1260,9 @@ bool stream_fits(int64_t k, int mt, int64_t group, bool mx) {
 template <int FMT, int MATS>
 int stream_launch(GemmArgs g, Mode mode, int64_t tiles, int mt, hipStream_t s, const char* what) {
   constexpr int NT = MATS == 2 ? 1 : 2;
-  const bool wide = FMT == kFmtW4A16 && g.group >= 128;
+  // W4A16 G == 128 (wider groups use the LDS-staged kernel) or MXFP4 with k % 128 == 0
+  const bool wide = FMT == kFmtW4A16 ? g.group >= 128 : (FMT == kFmtMxBf16 && g.k % 128 == 0);
+  constexpr bool kWideOk = FMT != kFmtMxF16;
   const size_t lds = stream_lds_bytes(g.k, mt);
   LK_REQUIRE(lds <= static_cast<size_t>(kStMaxLds), "%s: reduction width too large", what);
   g.col_blocks = static_cast<int>((g.n + kStWaves * NT * 16 - 1) / (kStWaves * NT * 16));
@@ -1237,10 +1270,10 @@ int stream_launch(GemmArgs g, Mode mode, int64_t tiles, int mt, hipStream_t s, c
   LK_REQUIRE(blocks > 0 && blocks < (1LL << 31), "%s: too many blocks", what);
   const unsigned nb = static_cast<unsigned>(blocks);
   if (mt == 1) {
-    if (wide) stream_dispatch<FMT, MATS, 1, FMT == kFmtW4A16>(g, mode, nb, lds, s);
+    if (wide) stream_dispatch<FMT, MATS, 1, kWideOk>(g, mode, nb, lds, s);
     else stream_dispatch<FMT, MATS, 1, false>(g, mode, nb, lds, s);
   } else {
-    if (wide) stream_dispatch<FMT, MATS, 4, FMT == kFmtW4A16>(g, mode, nb, lds, s);
+    if (wide) stream_dispatch<FMT, MATS, 4, kWideOk>(g, mode, nb, lds, s);
     else stream_dispatch<FMT, MATS, 4, false>(g, mode, nb, lds, s);
   }
   return check_launch(what);

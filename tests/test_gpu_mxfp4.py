@@ -153,10 +153,11 @@ def test_gemm_validation_messages():
 # grouped, MoE block, expert MLP
 
 
-def test_grouped_and_swiglu_gemm_match_oracle(rng):
+@pytest.mark.parametrize("k", [256, 160])  # 16-byte (k % 128 == 0) and 4-byte weight loads
+def test_grouped_and_swiglu_gemm_match_oracle(rng, k):
     from local_kimi_amd.kernels import grouped_mxfp4_gemm, grouped_mxfp4_swiglu_gemm
 
-    t, r, e, n, k = 40, 3, 6, 96, 256
+    t, r, e, n = 40, 3, 6, 96
     x = random_bf16_bits(rng, (t, k))
     idx = rng.integers(0, e, (t, r)).astype(np.int64)
     idx[5, 2] = -1
