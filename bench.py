@@ -327,16 +327,21 @@ EXPERT_FLOPS = 2 * 3 * INTER * H  # gate, up and down projections per routed row
 
 
 def run_moe_batched(args, dev) -> dict:
-    """Batched decode: M tokens per step, Zipf(1.1)-skewed routing, expert-major path."""
+    """Batched decode: M tokens per step, Zipf(1.1)-skewed routing (the block's path by default)."""
     from local_kimi_amd.workloads import zipf_router_logits
     from oracle import moe as OM
 
+    from local_kimi_amd.kernels.moe import MOE_EXPERT_MAJOR_MIN_TOKENS
+
     m, layers = args.tokens, args.layers
+    path = args.moe_path
+    if path == "auto":  # the block's own choice
+        path = "expert" if m >= MOE_EXPERT_MAJOR_MIN_TOKENS or args.weights == "mxfp4" else "token"
     gen = torch.Generator(device=dev).manual_seed(20260729)
     rng = np.random.default_rng(20260729)
     t0 = time.time()
     banks = _layer_banks(layers, gen, dev, args.weights)
-    block = _block_fn(args.weights, args.moe_path)
+    block = _block_fn(args.weights, path)
     xs = [(torch.randn((m, H), device=dev, generator=gen)).to(torch.bfloat16) for _ in range(layers)]
     host_logits = [zipf_router_logits(rng, m, E_ROUTED) for _ in range(layers)]
     logits = [torch.from_numpy(lg).to(dev) for lg in host_logits]
@@ -370,7 +375,7 @@ def run_moe_batched(args, dev) -> dict:
         "data": f"synthetic: N(0,0.02) weights quantised {_weights_desc(args.weights)} on the GPU, "
                 "N(0,1) x, Zipf(1.1) router logits (log p + Gumbel)",
         "config": {"workload": f"moe_batched_decode_m{m}", "weights": args.weights,
-                   "path": f"{args.moe_path}-major", "tokens_per_step": m, "hidden": H,
+                   "path": f"{path}-major", "tokens_per_step": m, "hidden": H,
                    "routed_experts": E_ROUTED, "shared_experts": 1, "moe_intermediate": INTER,
                    "top_k": TOP_K, "layer_banks_rotated": layers,
                    "mean_distinct_routed_experts": round(float(np.mean(unions)), 2)},
@@ -535,8 +540,8 @@ def main() -> int:
                     choices=["moe_decode", "dense_decode", "moe_batched", "moe_prefill",
                              "qkv_prefill", "copy"])
     ap.add_argument("--tokens", type=int, default=64, help="moe_batched tokens per step")
-    ap.add_argument("--moe-path", choices=["expert", "token"], default="expert",
-                    help="moe_batched: expert-major GEMMs or the token-major GEMV kernels")
+    ap.add_argument("--moe-path", choices=["auto", "expert", "token"], default="auto",
+                    help="moe_batched: the block's choice, expert-major GEMMs or token-major GEMVs")
     ap.add_argument("--weights", choices=["w4a16", "mxfp4"], default="w4a16",
                     help="moe_batched / moe_prefill expert weight format")
     ap.add_argument("--prefill-tokens", type=int, default=2048)

@@ -24,8 +24,12 @@ from .. import _lib
 from . import w4a16 as _w
 
 
-# tokens from which the MoE block runs expert-major (each expert read once)
-MOE_EXPERT_MAJOR_MIN_TOKENS = 2
+# tokens from which the MoE block runs expert-major (each expert read once).
+# Below it the token-major kernels win: at the Kimi-Linear shape with
+# Zipf(1.1) routing, 6 tokens take 67 us token-major vs 72 us expert-major,
+# 8 tokens 83 us vs 77 us (the expert-major chain has a ~50 us floor of six
+# launches: router, two schedule passes, two GEMMs, combine).
+MOE_EXPERT_MAJOR_MIN_TOKENS = 8
 # bank entries (routed + shared) the expert-major schedule supports
 MOE_EXPERT_MAJOR_MAX_EXPERTS = 512
 
@@ -151,8 +155,9 @@ def w4a16_moe_block(hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Tens
                     routed_scaling_factor: float = 1.0, renormalize: bool = True):
     """Router + SwiGLU experts + W2 + combine + shared expert on HIP.
 
-    One token: two launches (token-major decode). More tokens: the
-    expert-major path (:func:`w4a16_moe_forward`).
+    Fewer than ``MOE_EXPERT_MAJOR_MIN_TOKENS`` tokens: two launches per call
+    (token-major decode). More tokens: the expert-major path
+    (:func:`w4a16_moe_forward`).
     Returns ``(y bf16 [T, H], expert_indices int64 [T, k], weights float32 [T, k])``.
     """
     if hidden.ndim == 2 and hidden.shape[0] >= MOE_EXPERT_MAJOR_MIN_TOKENS and \
