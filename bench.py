@@ -383,7 +383,9 @@ def run_moe_batched(args, dev) -> dict:
         "achieved_gbps": round(gbps, 1),
         "pct_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
         "algorithmic_bytes_per_step": int(step_bytes),
-        "roofline": {"kernel": "whole block (router, schedule, gate/up GEMM, down GEMM, combine)",
+        "roofline": {"kernel": ("whole block (router, schedule, gate/up GEMM, down GEMM, combine)"
+                                if path == "expert" else
+                                "whole block (router + gate/up GEMV, W2 + combine GEMV)"),
                      "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "mfma_tflops": round(step_flops / (us_step * 1e6), 2)},
