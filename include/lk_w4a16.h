@@ -278,7 +278,15 @@ LK_API int lk_mxfp4_swiglu_gemm(const uint16_t* x, const int64_t* expert_indices
                                 void* stream);
 
 /* The MoE block of lk_w4a16_moe_forward with MXFP4 expert banks (the
- * Kimi-Linear SwiGLU block; workspace from lk_w4a16_moe_forward_workspace). */
+ * Kimi-Linear SwiGLU block; workspace from lk_mxfp4_moe_forward_workspace).
+ * With h and i multiples of 128, prefill-sized calls (64-row expert tiles,
+ * more than 2048 token-routes) run the expert GEMMs on the scaled fp4 MFMA
+ * (v_mfma_scale_f32_16x16x128_f8f6f4): raw E2M1 weights and E8M0 exponents,
+ * activations split into fp8 hi + lo (lk_mxfp4_split_activations); decode
+ * sizes use bf16 MFMA on weights decoded by the scaled fp4 convert. The
+ * environment variable LK_MXFP4_MFMA=fp4 or =bf16 forces one form. */
+LK_API int64_t lk_mxfp4_moe_forward_workspace(int64_t tokens, int64_t experts, int64_t h,
+                                              int64_t i, int64_t top_k);
 LK_API int lk_mxfp4_moe_forward(const uint16_t* x, const float* logits, const float* bias,
                                 const uint8_t* w1_packed, const uint8_t* w1_scale,
                                 const uint8_t* w3_packed, const uint8_t* w3_scale,
@@ -287,6 +295,16 @@ LK_API int lk_mxfp4_moe_forward(const uint16_t* x, const float* logits, const fl
                                 int64_t workspace_bytes, int64_t tokens, int64_t experts,
                                 int64_t h, int64_t i, int64_t top_k,
                                 float routed_scaling_factor, int renormalize, void* stream);
+
+/* fp8 split of bf16 activations x [rows, k] (k % 32 == 0) for the scaled fp4
+ * MFMA; no reference counterpart (the reference multiplies bf16 activations by
+ * decoded weights). Per 32 values along k: x ~= hi * 2^e_hi + lo * 2^e_lo,
+ * hi/lo uint8 [rows, k] OCP E4M3 codes (nearest, ties to even, magnitudes
+ * below 2^-6 flushed), scales uint16 [rows, k/32] = (e_hi + 127) | (e_lo + 127) << 8,
+ * e = clamp(floor(log2(block max)) - 7, -127, 127); lo encodes the exact
+ * residual. */
+LK_API int lk_mxfp4_split_activations(const uint16_t* x, uint8_t* hi, uint8_t* lo,
+                                      uint16_t* scales, int64_t rows, int64_t k, void* stream);
 
 /* One packed expert MLP with K3's SiTU activation:
  * engine/kernels/moe_grouped.py:163-194 (mxfp4_expert_mlp, situ_and_mul).

@@ -57,12 +57,14 @@ SIGNATURES: dict[str, list] = {
     "lk_mxfp4_moe_forward": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                              _I64, _I64, _I64, _I64, _I64, _F, _I, _P],
     "lk_mxfp4_expert_mlp": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _P],
+    "lk_mxfp4_split_activations": [_P, _P, _P, _P, _I64, _I64, _P],
 }
 
 # name -> argument types of the size queries (they return int64, -1 on bad input)
 QUERIES: dict[str, list] = {
     "lk_w4a16_grouped_gemm_workspace": [_I64, _I64, _I64],
     "lk_w4a16_moe_forward_workspace": [_I64, _I64, _I64, _I64, _I64],
+    "lk_mxfp4_moe_forward_workspace": [_I64, _I64, _I64, _I64, _I64],
 }
 
 _lock = threading.Lock()

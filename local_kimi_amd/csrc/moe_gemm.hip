@@ -201,11 +201,16 @@ schedule_place_kernel(const RouteTable rt, int64_t n, int chunks, Schedule sc) {
 // ---------------------------------------------------------------------------
 // W4A16 GEMM on the matrix cores
 
-enum : int { kFmtW4A16 = 0, kFmtMxBf16 = 1, kFmtMxF16 = 2 };  // weight format x activation type
+// weight format x activation type; kFmtMxF8: MXFP4 weights x activations
+// split into fp8 hi + lo with per-32 E8M0 exponents (scaled fp4 MFMA)
+enum : int { kFmtW4A16 = 0, kFmtMxBf16 = 1, kFmtMxF16 = 2, kFmtMxF8 = 3 };
 enum : int { kActSwiglu = 0, kActSitu = 1 };                   // two-matrix epilogues
 
 struct GemmArgs {
   const uint16_t* a;         // activations (bf16, or fp16 for kFmtMxF16), rows of k
+  const uint8_t* a_hi;       // kFmtMxF8: fp8 hi codes, rows of k bytes
+  const uint8_t* a_lo;       // kFmtMxF8: fp8 lo codes
+  const uint16_t* a_sc;      // kFmtMxF8: per-32 exponents, byte 0 hi, byte 1 lo
   const int32_t* perm;       // sorted position -> entry (gather / scatter modes)
   const int32_t* tiles;      // [*, 4] tile list (schedule modes)
   const int32_t* tile_count;
@@ -233,6 +238,7 @@ constexpr int kGemmWaves = 4;
 constexpr uint32_t kOnesBf16x2 = 0x3F803F80u;  // (1.0, 1.0) in bf16
 
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef int v8i32_t __attribute__((ext_vector_type(8)));
 
 __device__ inline bf16x8_t unpack_q8(uint32_t w) {
   const uint32_t u = w ^ kNibbleFlip;
@@ -684,7 +690,9 @@ template <int FMT, int MATS, int NT, int MT, bool WIDE, bool GATHER, bool SCATTE
 __global__ void __launch_bounds__(kStWaves * kWave, 2)
 w4a16_stream_kernel(const GemmArgs g) {
   constexpr bool kMx = FMT != kFmtW4A16;
+  constexpr bool kF8 = FMT == kFmtMxF8;
   static_assert(!(FMT == kFmtMxF16 && WIDE), "fp16 activations use the narrow layout");
+  static_assert(!kF8 || WIDE, "the scaled fp4 MFMA takes 16-byte weight loads (k % 128 == 0)");
   constexpr int kThreads = kStWaves * kWave;
   constexpr int kBN = kStWaves * NT * 16;
   constexpr int kRows = 16 * MT;
@@ -781,23 +789,47 @@ w4a16_stream_kernel(const GemmArgs g) {
   constexpr int kRowShift = MT == 1 ? 4 : 6;
   static_assert(kRows == (1 << kRowShift), "tile rows must be 16 or 64");
   auto unit_live = [&](int u) { return ((u >> 4) & (kRows - 1)) < rows; };
+  // kFmtMxF8: unit c < 8 is 16 fp8 hi codes (k = 16c..16c+15 of the step),
+  // c >= 8 the lo codes of chunk c - 8; units c < 4 also carry the row's
+  // exponent word of 32-block c. MFMA lane (row, kb) takes k = 16kb.. and
+  // 64 + 16kb.. of hi (slots t = 0, 1) and of lo (t = 2, 3), and the exponent
+  // word of block kb (byte 0 hi, byte 1 lo).
   auto unit_load = [&](int p, int u) -> uint4 {
     const int c = u & 15;
     const int m = (u >> 4) & (kRows - 1);
     const int ls = u >> (4 + kRowShift);
+    if constexpr (kF8) {
+      const int64_t k0 = static_cast<int64_t>(p * ps + ls) * 128 + (c & 7) * 16;  // k % 128 == 0
+      return *reinterpret_cast<const uint4*>((c < 8 ? g.a_hi : g.a_lo) + row_index[m] * K + k0);
+    }
     const int64_t k0 = static_cast<int64_t>(p * ps + ls) * 128 + c * 8;
     uint4 v = *reinterpret_cast<const uint4*>(g.a + row_index[m] * K + (k0 < K ? k0 : 0));
     if (k0 >= K) v = make_uint4(0u, 0u, 0u, 0u);
     return v;
   };
-  auto unit_store = [&](int b, int u, const uint4 v) {  // uniform per 16-lane row
+  auto unit_scale = [&](int p, int u) -> uint32_t {  // kFmtMxF8 units c < 4 only
+    const int c = u & 15;
+    const int m = (u >> 4) & (kRows - 1);
+    const int ls = u >> (4 + kRowShift);
+    if (!kF8 || c >= 4) return 0u;
+    return g.a_sc[row_index[m] * (K / 32) + static_cast<int64_t>(p * ps + ls) * 4 + c];
+  };
+  auto unit_store = [&](int b, int u, const uint4 v, uint32_t sv) {  // uniform per 16-lane row
     const int c = u & 15;
     const int m = (u >> 4) & (kRows - 1);
     const int ls = u >> (4 + kRowShift);
     const int ms = m >> 4, mr = m & 15;
+    const int frag = ((b * ps + ls) * MT + ms) * 4;
+    if constexpr (kF8) {
+      const int kb = c & 3;
+      const int t = (c >> 2);  // 0, 1: hi halves; 2, 3: lo halves
+      afrag[(frag + t) * kWave + kb * 16 + (mr ^ (4 * t + kb))] = v;
+      if (c < 4) reinterpret_cast<uint32_t*>(offs)[(frag + c) * 16 + mr] = sv;
+      return;
+    }
+    (void)sv;
     const int t = WIDE ? (c & 3) : (c >> 2);
     const int j = WIDE ? (c >> 2) : (c & 3);
-    const int frag = ((b * ps + ls) * MT + ms) * 4;
     uint4* dst = &afrag[(frag + t) * kWave + j * 16 + (mr ^ (4 * t + j))];
     if constexpr (kMx) {
       *dst = v;
@@ -825,15 +857,19 @@ w4a16_stream_kernel(const GemmArgs g) {
     const int units = pass_steps(0) * kRows * 16;
     for (int u0 = 0; u0 < units; u0 += kBatch * kThreads) {
       uint4 v[kBatch];
+      uint32_t sv[kBatch];
 #pragma unroll
       for (int b = 0; b < kBatch; ++b) {
         const int u = u0 + b * kThreads + tid;
-        if (u < units && unit_live(u)) v[b] = unit_load(0, u);
+        if (u < units && unit_live(u)) {
+          v[b] = unit_load(0, u);
+          sv[b] = unit_scale(0, u);
+        }
       }
 #pragma unroll
       for (int b = 0; b < kBatch; ++b) {
         const int u = u0 + b * kThreads + tid;
-        if (u < units && unit_live(u)) unit_store(0, u, v[b]);
+        if (u < units && unit_live(u)) unit_store(0, u, v[b], sv[b]);
       }
     }
   }
@@ -857,7 +893,43 @@ w4a16_stream_kernel(const GemmArgs g) {
   // stale LDS and produce rows that are never stored (MFMA rows are independent).
   auto compute_step = [&](const WeightStep<FMT, MATS, NT, WIDE>& wj, int step, int b, int ls) {
     const int frag0 = (b * ps + ls) * MT * 4;
-    if constexpr (kMx && WIDE) {
+    if constexpr (kF8) {
+      // two scaled MFMAs per 16x16 tile and k-step: fp8 hi, then fp8 lo, each
+      // times the raw fp4 weights with their E8M0 block exponents
+      v8i32_t ahi[MT], alo[MT];
+      int32_t sa[MT];
+#pragma unroll
+      for (int ms = 0; ms < MT; ++ms) {
+        const int f = frag0 + ms * 4;
+        const uint4 h0 = afrag[(f + 0) * kWave + jq * 16 + (ln ^ (0 + jq))];
+        const uint4 h1 = afrag[(f + 1) * kWave + jq * 16 + (ln ^ (4 + jq))];
+        const uint4 l0 = afrag[(f + 2) * kWave + jq * 16 + (ln ^ (8 + jq))];
+        const uint4 l1 = afrag[(f + 3) * kWave + jq * 16 + (ln ^ (12 + jq))];
+        ahi[ms] = v8i32_t{static_cast<int>(h0.x), static_cast<int>(h0.y), static_cast<int>(h0.z),
+                          static_cast<int>(h0.w), static_cast<int>(h1.x), static_cast<int>(h1.y),
+                          static_cast<int>(h1.z), static_cast<int>(h1.w)};
+        alo[ms] = v8i32_t{static_cast<int>(l0.x), static_cast<int>(l0.y), static_cast<int>(l0.z),
+                          static_cast<int>(l0.w), static_cast<int>(l1.x), static_cast<int>(l1.y),
+                          static_cast<int>(l1.z), static_cast<int>(l1.w)};
+        sa[ms] = reinterpret_cast<const int32_t*>(offs)[(f + jq) * 16 + ln];
+      }
+#pragma unroll
+      for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const v8i32_t bw = {static_cast<int>(wj.w[mi][nt][0]), static_cast<int>(wj.w[mi][nt][1]),
+                              static_cast<int>(wj.w[mi][nt][2]), static_cast<int>(wj.w[mi][nt][3]),
+                              0, 0, 0, 0};
+          const int sb = static_cast<int>(wj.s[mi][nt][0]);
+#pragma unroll
+          for (int ms = 0; ms < MT; ++ms) {
+            tot[mi][nt][ms] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                ahi[ms], bw, tot[mi][nt][ms], 0, 4, 0, sa[ms], 0, sb);
+            tot[mi][nt][ms] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                alo[ms], bw, tot[mi][nt][ms], 0, 4, 1, sa[ms], 0, sb);
+          }
+        }
+    } else if constexpr (kMx && WIDE) {
       // k % 128 == 0: every sub-step is real; the lane's block scale is decoded once
       float sc[MATS][NT];
 #pragma unroll
@@ -990,6 +1062,7 @@ w4a16_stream_kernel(const GemmArgs g) {
     // (its first kStPassSteps slots), so slot j serves local step j
     const int passes = (ksteps + ps - 1) / ps;
     uint4 vnext[kPassUnits];  // the next pass, in flight during this one
+    uint32_t snext[kPassUnits];
     for (int p = 0; p < passes; ++p) {
       const int b = p % kNBuf;
       const bool more = p + 1 < passes;
@@ -998,7 +1071,10 @@ w4a16_stream_kernel(const GemmArgs g) {
 #pragma unroll
         for (int q = 0; q < kPassUnits; ++q) {
           const int u = q * kThreads + tid;
-          if (u < units1 && unit_live(u)) vnext[q] = unit_load(p + 1, u);
+          if (u < units1 && unit_live(u)) {
+            vnext[q] = unit_load(p + 1, u);
+            snext[q] = unit_scale(p + 1, u);
+          }
         }
       }
 #pragma unroll
@@ -1014,7 +1090,7 @@ w4a16_stream_kernel(const GemmArgs g) {
 #pragma unroll
         for (int q = 0; q < kPassUnits; ++q) {
           const int u = q * kThreads + tid;
-          if (u < units1 && unit_live(u)) unit_store((p + 1) % kNBuf, u, vnext[q]);
+          if (u < units1 && unit_live(u)) unit_store((p + 1) % kNBuf, u, vnext[q], snext[q]);
         }
         __syncthreads();
       }
@@ -1043,6 +1119,91 @@ w4a16_stream_kernel(const GemmArgs g) {
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// fp8 hi/lo split of bf16 activations for the scaled fp4 MFMA. Per block of
+// 32 values along k: x ~= hi * 2^e_hi + lo * 2^e_lo with OCP E4M3 codes
+// (nearest, ties to even; magnitudes under 2^-6 flush to signed zero) and
+// e = clamp(E(block max) - 7, -127, 127), E = the float exponent field - 127,
+// so the scaled block max lies in [128, 256) and never saturates. lo encodes
+// the exact residual x - hi * 2^e_hi the same way. hi and lo together keep
+// the 8 significant bits of a bf16 value. One thread per (row, block).
+
+__device__ inline uint32_t e4m3_code(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  if (a < 0x3C800000u) return sign;  // below 2^-6
+  const uint32_t r = a + 0x7FFFFu + ((a >> 20) & 1u);
+  return sign | ((((r >> 23) - 120u) & 15u) << 3) | ((r >> 20) & 7u);
+}
+
+// value of a code produced by e4m3_code (normal or signed zero)
+__device__ inline float e4m3_value(uint32_t c) {
+  const uint32_t e = (c >> 3) & 15u;
+  const uint32_t sign = (c & 0x80u) << 24;
+  return __uint_as_float(e == 0u ? sign : sign | ((e + 120u) << 23) | ((c & 7u) << 20));
+}
+
+__device__ inline int split_exponent(float amax) {
+  const int field = static_cast<int>((__float_as_uint(amax) >> 23) & 0xFFu);
+  return min(max(field - 134, -127), 127);
+}
+
+__global__ void __launch_bounds__(256)
+mx_split_kernel(const uint16_t* __restrict__ x, uint8_t* __restrict__ hi, uint8_t* __restrict__ lo,
+                uint16_t* __restrict__ sc, int64_t blocks) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (b >= blocks) return;
+  const uint4* src = reinterpret_cast<const uint4*>(x + b * 32);
+  float v[32];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint4 w = src[q];
+    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[q * 8 + 2 * j] = __uint_as_float(d[j] << 16);
+      v[q * 8 + 2 * j + 1] = __uint_as_float(d[j] & 0xFFFF0000u);
+    }
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  const int e1 = split_exponent(amax);
+  const float inv1 = __uint_as_float(static_cast<uint32_t>(127 - e1) << 23);
+  const float s1 = e8m0_to_f32(static_cast<uint32_t>(e1 + 127));
+  uint32_t h[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+  float ramax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const uint32_t c = e4m3_code(v[i] * inv1);
+    h[i >> 2] |= c << (8 * (i & 3));
+    v[i] -= e4m3_value(c) * s1;  // exact residual
+    ramax = fmaxf(ramax, fabsf(v[i]));
+  }
+  const int e2 = split_exponent(ramax);
+  const float inv2 = __uint_as_float(static_cast<uint32_t>(127 - e2) << 23);
+  uint32_t l[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 32; ++i) l[i >> 2] |= e4m3_code(v[i] * inv2) << (8 * (i & 3));
+  uint4* dh = reinterpret_cast<uint4*>(hi + b * 32);
+  uint4* dl = reinterpret_cast<uint4*>(lo + b * 32);
+  dh[0] = make_uint4(h[0], h[1], h[2], h[3]);
+  dh[1] = make_uint4(h[4], h[5], h[6], h[7]);
+  dl[0] = make_uint4(l[0], l[1], l[2], l[3]);
+  dl[1] = make_uint4(l[4], l[5], l[6], l[7]);
+  sc[b] = static_cast<uint16_t>((e1 + 127) | ((e2 + 127) << 8));
+}
+
+int split_launch(const uint16_t* x, uint8_t* hi, uint8_t* lo, uint16_t* sc, int64_t rows, int64_t k,
+                 hipStream_t s) {
+  const int64_t blocks = rows * (k / 32);
+  if (blocks == 0) return LK_OK;
+  LK_REQUIRE((blocks + 255) / 256 < (1LL << 31), "too many rows for the fp8 split");
+  mx_split_kernel<<<static_cast<unsigned>((blocks + 255) / 256), 256, 0, s>>>(x, hi, lo, sc, blocks);
+  return check_launch("mxfp4 activation split");
 }
 
 // ---------------------------------------------------------------------------
@@ -1116,12 +1277,34 @@ SchedLayout sched_layout(int64_t entries, int64_t experts) {
 }
 
 // Private buffers of one expert-major call, carved from the caller's workspace.
+// bytes of one fp8 split region (hi, lo, exponent words) of `elems` values
+size_t split_bytes(int64_t elems) {
+  const size_t e = static_cast<size_t>(elems);
+  return align_up(e) * 2 + align_up(e / 16);
+}
+
 struct MoeLayout {
   SchedLayout sched;
-  size_t offsets, perm, tiles, count, act, eo, total;
+  size_t offsets, perm, tiles, count, act, eo, x_split, act_split, total;
 };
 
-MoeLayout moe_layout(int64_t entries, int64_t experts, int64_t act_cols, int64_t out_cols) {
+// Pointers into one fp8 split region of `elems` values: hi, lo, exponent words.
+struct SplitBufs {
+  uint8_t* hi;
+  uint8_t* lo;
+  uint16_t* sc;
+};
+
+SplitBufs split_bufs(char* base, int64_t elems) {
+  SplitBufs b;
+  b.hi = reinterpret_cast<uint8_t*>(base);
+  b.lo = b.hi + align_up(static_cast<size_t>(elems));
+  b.sc = reinterpret_cast<uint16_t*>(b.lo + align_up(static_cast<size_t>(elems)));
+  return b;
+}
+
+MoeLayout moe_layout(int64_t entries, int64_t experts, int64_t act_cols, int64_t out_cols,
+                     int64_t split_x_elems = 0) {
   MoeLayout l;
   l.sched = sched_layout(entries, experts);
   size_t at = l.sched.total;
@@ -1137,6 +1320,12 @@ MoeLayout moe_layout(int64_t entries, int64_t experts, int64_t act_cols, int64_t
   at += align_up(static_cast<size_t>(entries) * act_cols * 2);
   l.eo = at;
   at += align_up(static_cast<size_t>(entries) * out_cols * 2);
+  // fp8 hi/lo splits of the gathered input and of the activations (MXFP4 on
+  // the scaled fp4 MFMA only): hi and lo bytes plus one exponent word per 32
+  l.x_split = at;
+  at += split_bytes(split_x_elems);
+  l.act_split = at;
+  if (split_x_elems > 0) at += split_bytes(entries * act_cols);
   l.total = at;
   return l;
 }
@@ -1269,7 +1458,11 @@ int stream_launch(GemmArgs g, Mode mode, int64_t tiles, int mt, hipStream_t s, c
   const int64_t blocks = (tiles + 7) / 8 * 8 * g.col_blocks * g.outputs;
   LK_REQUIRE(blocks > 0 && blocks < (1LL << 31), "%s: too many blocks", what);
   const unsigned nb = static_cast<unsigned>(blocks);
-  if (mt == 1) {
+  if constexpr (FMT == kFmtMxF8) {  // 16-byte weight loads only
+    LK_REQUIRE(g.k % 128 == 0, "%s: the scaled fp4 MFMA needs k %% 128 == 0", what);
+    if (mt == 1) stream_dispatch<FMT, MATS, 1, true>(g, mode, nb, lds, s);
+    else stream_dispatch<FMT, MATS, 4, true>(g, mode, nb, lds, s);
+  } else if (mt == 1) {
     if (wide) stream_dispatch<FMT, MATS, 1, kWideOk>(g, mode, nb, lds, s);
     else stream_dispatch<FMT, MATS, 1, false>(g, mode, nb, lds, s);
   } else {
@@ -1309,6 +1502,19 @@ int stream_fmt(bool mx, const GemmArgs& g, Mode mode, int64_t tiles, int mt, hip
 // 64-row tiles above (prefill). LK_MOE_GEMM=lds selects the LDS-staged
 // kernel instead, LK_MOE_GEMM=stream16|stream64 forces a tile height.
 constexpr int64_t kStreamSmallEntries = 2048;
+
+// Which MFMA form the MXFP4 expert GEMMs take. The scaled fp4 MFMA (raw fp4
+// weights, activations split into fp8 hi + lo) wins on 64-row prefill tiles
+// (782 vs 831 us for a 2048-token Kimi-Linear layer); on 16-row decode tiles
+// the GEMMs are weight-bandwidth bound and bf16 MFMA on decoded weights is
+// faster (175 vs 198 us at 64 tokens: no split launches, fewer registers).
+// LK_MXFP4_MFMA=fp4 or =bf16 forces one form for every tile height.
+bool mxfp4_scaled_mfma(int mt) {
+  const char* env = getenv("LK_MXFP4_MFMA");
+  if (env && strcmp(env, "bf16") == 0) return false;
+  if (env && strcmp(env, "fp4") == 0) return true;
+  return mt == 4;
+}
 
 // 16-row tiles -> 1, 64-row tiles -> 4, the LDS-staged kernel -> 0.
 int stream_tile_mt(int64_t entries) {
@@ -1616,6 +1822,21 @@ int64_t lk_w4a16_moe_forward_workspace(int64_t tokens, int64_t experts, int64_t 
   return static_cast<int64_t>(moe_layout(tokens * (top_k + 1), experts, i, h).total);
 }
 
+int64_t lk_mxfp4_moe_forward_workspace(int64_t tokens, int64_t experts, int64_t h, int64_t i,
+                                       int64_t top_k) {
+  if (tokens < 0 || experts < 2 || h <= 0 || i <= 0 || top_k <= 0) return -1;
+  if (check_schedule_dims(tokens, top_k + 1, experts)) return -1;
+  return static_cast<int64_t>(moe_layout(tokens * (top_k + 1), experts, i, h, tokens * h).total);
+}
+
+int lk_mxfp4_split_activations(const uint16_t* x, uint8_t* hi, uint8_t* lo, uint16_t* scales,
+                               int64_t rows, int64_t k, void* stream) {
+  LK_REQUIRE(rows >= 0 && k > 0 && k % 32 == 0, "fp8 split needs rows >= 0 and k %% 32 == 0");
+  if (rows == 0) return LK_OK;
+  LK_REQUIRE(x && hi && lo && scales, "null pointer argument");
+  return split_launch(x, hi, lo, scales, rows, k, as_stream(stream));
+}
+
 static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, const float* bias,
                               const uint8_t* w1_packed, const void* w1_scales,
                               const uint8_t* w3_packed, const void* w3_scales,
@@ -1639,7 +1860,7 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   LK_REQUIRE(x && logits && workspace, "null pointer argument");
   const int64_t routes = top_k + 1;
   const int64_t entries = tokens * routes;
-  const MoeLayout l = moe_layout(entries, experts, i, h);
+  const MoeLayout l = moe_layout(entries, experts, i, h, mx ? tokens * h : 0);
   LK_REQUIRE(workspace_bytes >= static_cast<int64_t>(l.total),
              "MoE workspace too small: %lld < %lld bytes", (long long)workspace_bytes,
              (long long)l.total);
@@ -1662,6 +1883,15 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, tr, s))
     return rc;
 
+  // MXFP4 on the scaled fp4 MFMA: x and the activations go in as fp8 hi + lo
+  const bool f8 = mx && mt != 0 && h % 128 == 0 && i % 128 == 0 && mxfp4_scaled_mfma(mt);
+  SplitBufs xs{}, as{};
+  if (f8) {
+    xs = split_bufs(ws + l.x_split, tokens * h);
+    as = split_bufs(ws + l.act_split, entries * i);
+    if (int rc = split_launch(x, xs.hi, xs.lo, xs.sc, tokens, h, s)) return rc;
+  }
+
   GemmArgs g{};
   g.perm = perm;
   g.tiles = tiles;
@@ -1672,6 +1902,9 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.act = kActSwiglu;
   // gate/up + SwiGLU: rows gathered from x, activations written in sorted order
   g.a = x;
+  g.a_hi = xs.hi;
+  g.a_lo = xs.lo;
+  g.a_sc = xs.sc;
   g.wp[0] = w1_packed;
   g.ws[0] = w1_scales;
   g.wp[1] = w3_packed;
@@ -1684,12 +1917,19 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.wstride = i * h / 2;
   g.sstride = i * (h / group);
   const int64_t tb = max_tiles_for(entries, experts, tr);
-  if (int rc = mt ? stream_fmt<2>(mx, g, Mode::Gather, tb, mt, s, "moe gate/up gemm")
-                  : launch_fmt<2>(mx, g, Mode::Gather, tb, wide_cols_for(tb, i), s,
-                                  "moe gate/up gemm"))
+  if (int rc = f8 ? stream_launch<kFmtMxF8, 2>(g, Mode::Gather, tb, mt, s, "moe gate/up gemm")
+               : mt ? stream_fmt<2>(mx, g, Mode::Gather, tb, mt, s, "moe gate/up gemm")
+                    : launch_fmt<2>(mx, g, Mode::Gather, tb, wide_cols_for(tb, i), s,
+                                    "moe gate/up gemm"))
     return rc;
   // down projection: sorted activation rows, outputs scattered to (token, route) rows
+  if (f8) {
+    if (int rc = split_launch(act, as.hi, as.lo, as.sc, entries, i, s)) return rc;
+  }
   g.a = act;
+  g.a_hi = as.hi;
+  g.a_lo = as.lo;
+  g.a_sc = as.sc;
   g.wp[0] = g.wp[1] = g.wp[2] = w2_packed;
   g.ws[0] = g.ws[1] = g.ws[2] = w2_scales;
   g.out[0] = g.out[1] = g.out[2] = eo;
@@ -1697,9 +1937,10 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.k = i;
   g.wstride = h * i / 2;
   g.sstride = h * (i / group);
-  if (int rc = mt ? stream_fmt<1>(mx, g, Mode::Scatter, tb, mt, s, "moe down gemm")
-                  : launch_fmt<1>(mx, g, Mode::Scatter, tb, wide_cols_for(tb, h), s,
-                                  "moe down gemm"))
+  if (int rc = f8 ? stream_launch<kFmtMxF8, 1>(g, Mode::Scatter, tb, mt, s, "moe down gemm")
+               : mt ? stream_fmt<1>(mx, g, Mode::Scatter, tb, mt, s, "moe down gemm")
+                    : launch_fmt<1>(mx, g, Mode::Scatter, tb, wide_cols_for(tb, h), s,
+                                    "moe down gemm"))
     return rc;
   const int64_t work = tokens * (h / 8);
   moe_combine_kernel<<<static_cast<unsigned>((work + 255) / 256), 256, 0, s>>>(

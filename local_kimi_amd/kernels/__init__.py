@@ -22,7 +22,7 @@ from .moe import (moe_router, moe_schedule, shape_stable_expert_indices, w4a16_m
                   w4a16_moe_gateup)
 from .mxfp4 import (grouped_mxfp4_gemm, grouped_mxfp4_reference, grouped_mxfp4_swiglu_gemm,
                     mxfp4_expert_mlp, mxfp4_gemm, mxfp4_gemm_reference, mxfp4_linear,
-                    mxfp4_moe_block, mxfp4_moe_block_reference)
+                    mxfp4_moe_block, mxfp4_moe_block_reference, split_activations_fp8)
 from .w4a16 import (fused_qkv_w4a16, fused_qkv_w4a16_reference, fused_w2_combine,
                     fused_w2_combine_reference, grouped_w4a16_gemm, grouped_w4a16_gemv,
                     grouped_w4a16_reference, grouped_w4a16_swiglu_gemm,
@@ -149,5 +149,6 @@ __all__ = [
     "MXFP4_GEMM", "MXFP4_GROUPED", "MXFP4_MOE_BLOCK", "mxfp4_gemm", "mxfp4_linear",
     "mxfp4_gemm_reference", "grouped_mxfp4_gemm", "grouped_mxfp4_swiglu_gemm",
     "grouped_mxfp4_reference", "mxfp4_moe_block", "mxfp4_moe_block_reference",
+    "split_activations_fp8",
     "mxfp4_expert_mlp",
 ]

@@ -9,7 +9,12 @@ matrix cores with fp32 accumulation.
 
 Grouped banks stack experts on a leading axis; the MoE block is the
 Kimi-Linear SwiGLU block of :mod:`.moe` with MXFP4 banks (shared expert
-last). ``mxfp4_expert_mlp`` is the K3 packed expert with SiTU
+last). At prefill sizes its expert GEMMs run on the gfx950 scaled fp4 MFMA:
+raw E2M1 weights with their E8M0 exponents, activations split into fp8 hi +
+lo (:func:`split_activations_fp8`) so the product keeps bf16 activation
+precision; decode sizes (bandwidth bound) use bf16 MFMA on decoded weights
+(``LK_MXFP4_MFMA=fp4|bf16`` forces one form).
+``mxfp4_expert_mlp`` is the K3 packed expert with SiTU
 (engine/kernels/moe_grouped.py:163-194).
 """
 
@@ -156,6 +161,28 @@ def grouped_mxfp4_swiglu_gemm(activations, expert_indices, w1_packed, w1_scale, 
     return out
 
 
+def split_activations_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """bf16 ``[M, K]`` -> ``(hi uint8 [M, K], lo uint8 [M, K], scales int16 [M, K/32])``:
+    per 32 values x ~= hi * 2**e_hi + lo * 2**e_lo (OCP E4M3 codes; scale word
+    byte 0 = e_hi + 127, byte 1 = e_lo + 127)."""
+    if x.ndim != 2 or x.dtype != torch.bfloat16:
+        raise TypeError("the fp8 split takes a BF16 [rows, reduction] matrix")
+    if x.device.type != "cuda":
+        raise ValueError("the fp8 split requires CUDA tensors")
+    m, k = x.shape
+    if k == 0 or k % MXFP4_GROUP_SIZE:
+        raise ValueError("the fp8 split needs a reduction width that is a nonzero multiple of 32")
+    xc = _w._c(x)
+    hi = torch.empty((m, k), dtype=torch.uint8, device=x.device)
+    lo = torch.empty((m, k), dtype=torch.uint8, device=x.device)
+    sc = torch.empty((m, k // MXFP4_GROUP_SIZE), dtype=torch.int16, device=x.device)
+    if m:
+        with torch.cuda.device(x.device):
+            _lib.call("lk_mxfp4_split_activations", xc.data_ptr(), hi.data_ptr(), lo.data_ptr(),
+                      sc.data_ptr(), m, k, _w._stream(x.device))
+    return hi, lo, sc
+
+
 def mxfp4_moe_block(hidden, logits, bias, w1_packed, w1_scale, w3_packed, w3_scale, w2_packed,
                     w2_scale, top_k: int, routed_scaling_factor: float = 1.0,
                     renormalize: bool = True):
@@ -188,7 +215,7 @@ def mxfp4_moe_block(hidden, logits, bias, w1_packed, w1_scale, w3_packed, w3_sca
     b = _w._c(bias) if bias is not None else None
     banks = [_w._c(a) for a in (w1_packed, w1_scale, w3_packed, w3_scale, w2_packed, w2_scale)]
     with torch.cuda.device(dev):
-        ws = _w.workspace(_lib.query("lk_w4a16_moe_forward_workspace", tokens, e1, h, inter,
+        ws = _w.workspace(_lib.query("lk_mxfp4_moe_forward_workspace", tokens, e1, h, inter,
                                      top_k), dev)
         _lib.call("lk_mxfp4_moe_forward", x.data_ptr(), lg.data_ptr(),
                   b.data_ptr() if b is not None else None, *(a.data_ptr() for a in banks),

@@ -181,3 +181,77 @@ def expert_mlp(x_bits, w1_packed, w1_scale, w3_packed, w3_scale, w2_packed, w2_s
     up = linear(x_bits, w3_packed, w3_scale)
     act = situ(gate, up, beta, linear_beta)
     return linear(act, w2_packed, w2_scale)
+
+
+# ---------------------------------------------------------------------------
+# fp8 activation split for the scaled fp4 MFMA. This build's own encoding (the
+# reference multiplies bf16 activations by decoded weights and has no fp8
+# step): per block of 32 values along K, x ~= hi * 2**e_hi + lo * 2**e_lo with
+# hi and lo OCP FP8 E4M3 codes and E8M0 exponents e + 127.
+#   e     = clamp(E(amax) - 7, -127, 127), E(a) = the float32 exponent field
+#           minus 127 (floor(log2 a) for normal a, -127 for zero/subnormal),
+#           so the scaled block max lies in [128, 256) and never saturates;
+#   codes = round to nearest, ties to even, on the E4M3 grid; magnitudes below
+#           2**-6 (the smallest normal) flush to a signed zero;
+#   lo    = the same encoding of the exact residual x - hi * 2**e_hi.
+# Pinned in tests by brute force over the E4M3 grid and by reconstruction
+# bounds; the scaled MFMA consumes it (gfx950 v_mfma_scale_f32_16x16x128_f8f6f4).
+
+E4M3_MIN_NORMAL = 2.0 ** -6
+
+
+def e4m3_decode(codes: np.ndarray) -> np.ndarray:
+    """float64 values of OCP E4M3 codes (bias 7, subnormals m/8 * 2**-6)."""
+    c = np.asarray(codes, dtype=np.int64)
+    e = (c >> 3) & 15
+    m = c & 7
+    mag = np.where(e > 0, np.ldexp(1.0 + m / 8.0, e - 7), np.ldexp(m / 8.0, -6))
+    return np.where(c & 0x80, -mag, mag)
+
+
+def e4m3_encode(v: np.ndarray) -> np.ndarray:
+    """E4M3 codes of float32 values with |v| < 448: nearest, ties to even,
+    |v| < 2**-6 flushed to signed zero (float32 bit arithmetic)."""
+    u = np.asarray(v, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    sign = (u >> 24) & 0x80
+    a = u & 0x7FFFFFFF
+    r = a + 0x7FFFF + ((a >> 20) & 1)
+    code = sign | ((((r >> 23) - 120) & 15) << 3) | ((r >> 20) & 7)
+    return np.where(a < 0x3C800000, sign, code).astype(np.uint8)
+
+
+def _block_exponent(amax: np.ndarray) -> np.ndarray:
+    field = (np.asarray(amax, dtype=np.float32).view(np.uint32) >> 23).astype(np.int64) & 0xFF
+    return np.clip(field - 127 - 7, -127, 127)
+
+
+def _split_once(x: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """(codes [M, K], exponents [M, K/32], exact residual float32 [M, K])."""
+    m, k = x.shape
+    xb = x.reshape(m, k // GROUP, GROUP)
+    e = _block_exponent(np.abs(xb).max(-1))
+    scaled = (xb * np.ldexp(np.float32(1.0), -e)[..., None].astype(np.float32)).astype(np.float32)
+    codes = e4m3_encode(scaled)
+    val = (e4m3_decode(codes) * np.ldexp(1.0, e)[..., None]).astype(np.float32)
+    resid = (xb - val).astype(np.float32)
+    return codes.reshape(m, k), e, resid.reshape(m, k)
+
+
+def split_fp8(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """bf16 bits [M, K] -> (hi u8 [M, K], lo u8 [M, K], scales u16 [M, K/32] with
+    byte 0 = hi exponent + 127 and byte 1 = lo exponent + 127)."""
+    x = bf16_bits_to_f32(np.asarray(x_bits, dtype=np.uint16))
+    if x.shape[-1] % GROUP:
+        raise ValueError("the fp8 split needs K % 32 == 0")
+    hi, e_hi, resid = _split_once(x)
+    lo, e_lo, _ = _split_once(resid)
+    sc = ((e_hi + EXP_BIAS) | ((e_lo + EXP_BIAS) << 8)).astype(np.uint16)
+    return hi, lo, sc
+
+
+def split_decode(hi: np.ndarray, lo: np.ndarray, sc: np.ndarray) -> np.ndarray:
+    """float64 hi * 2**e_hi + lo * 2**e_lo."""
+    s = np.asarray(sc, dtype=np.int64)
+    e_hi = np.repeat((s & 0xFF) - EXP_BIAS, GROUP, axis=-1)
+    e_lo = np.repeat((s >> 8) - EXP_BIAS, GROUP, axis=-1)
+    return e4m3_decode(hi) * np.ldexp(1.0, e_hi) + e4m3_decode(lo) * np.ldexp(1.0, e_lo)

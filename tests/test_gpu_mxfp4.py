@@ -280,3 +280,38 @@ def test_mxfp4_variants_match_the_reference_variant(op):
 
     reports = equivalence.assert_equivalent(op, make, rtol=1e-2, atol=2e-2, device=DEV)
     assert reports and all(r.passed for r in reports)
+
+
+# ---------------------------------------------------------------------------
+# scaled fp4 MFMA: fp8 hi/lo activation split and both MFMA forms of the block
+
+def test_split_activations_bit_exact(rng):
+    from local_kimi_amd.kernels import split_activations_fp8
+
+    x = (rng.normal(0, 1, (48, 512)) * np.exp(rng.normal(0, 3, (48, 1)))).astype(np.float32)
+    x[3] = 0.0
+    x[5, :40] = -0.0
+    x[7, 32:64] = 1.0 + 1.0 / 16.0  # midpoints between E4M3 neighbours: ties to even
+    bits = f32_to_bf16_bits(x)
+    hi, lo, sc = split_activations_fp8(_dev(bits))
+    ehi, elo, esc = X.split_fp8(bits)
+    assert np.array_equal(hi.cpu().numpy(), ehi)
+    assert np.array_equal(lo.cpu().numpy(), elo)
+    assert np.array_equal(sc.cpu().numpy().view(np.uint16), esc)
+
+
+@pytest.mark.parametrize("form", ["scaled-fp4", "bf16"])
+@pytest.mark.parametrize("tokens", [1, 40])
+def test_moe_block_both_mfma_forms_match_oracle(rng, monkeypatch, form, tokens):
+    from local_kimi_amd.kernels import mxfp4_moe_block
+
+    monkeypatch.setenv("LK_MXFP4_MFMA", "bf16" if form == "bf16" else "fp4")
+    e_routed, h, inter, k = 12, 384, 256, 4
+    banks = (*_bank(rng, e_routed + 1, inter, h), *_bank(rng, e_routed + 1, inter, h),
+             *_bank(rng, e_routed + 1, h, inter))
+    x = random_bf16_bits(rng, (tokens, h))
+    logits = rng.normal(0, 1, (tokens, e_routed)).astype(np.float32)
+    ey, eidx, _ = X.moe_block(x, logits, None, *banks, top_k=k, routed_scaling_factor=2.446)
+    y, idx, _ = mxfp4_moe_block(_dev(x), _dev(logits), None, *(_dev(b) for b in banks), k, 2.446)
+    assert np.array_equal(idx.cpu().numpy(), eidx)
+    assert_close_bf16(to_bits(y), ey, what=f"mxfp4 moe block ({form}, T={tokens})")

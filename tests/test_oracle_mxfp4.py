@@ -179,3 +179,77 @@ def test_expert_mlp_composition_and_f16_linear():
     a = np.asarray(X.linear_f16(xf, *w1), np.uint16).view(np.float16).astype(np.float64)
     b = bf16_bits_to_f32(X.linear(x, *w1)).astype(np.float64)
     assert np.allclose(a, b, rtol=1e-2, atol=1e-2)
+
+
+# ---------------------------------------------------------------------------
+# fp8 hi/lo activation split (the scaled fp4 MFMA's A operand)
+
+def _e4m3_grid():
+    codes = np.arange(256)
+    codes = codes[(codes & 0x7F) != 0x7F]  # 0x7F / 0xFF are NaN in OCP E4M3
+    return codes, X.e4m3_decode(codes)
+
+
+def test_e4m3_decode_known_codes():
+    kat = {0x38: 1.0, 0xB8: -1.0, 0x7E: 448.0, 0x08: 2.0 ** -6, 0x01: 2.0 ** -9, 0x00: 0.0,
+           0x3C: 1.5, 0x40: 2.0, 0x78: 256.0}
+    for c, v in kat.items():
+        assert X.e4m3_decode(np.array([c]))[0] == v, hex(c)
+
+
+def test_e4m3_encode_is_nearest_with_ties_to_even(rng):
+    codes, vals = _e4m3_grid()
+    normal = vals[(np.abs(vals) >= 2.0 ** -6) & (np.abs(vals) <= 256.0)]
+    v = np.exp(rng.uniform(np.log(2.0 ** -6), np.log(255.0), 20000)) * rng.choice([-1.0, 1.0], 20000)
+    v = v.astype(np.float32)
+    got = X.e4m3_decode(X.e4m3_encode(v))
+    dist = np.abs(normal[None, :] - v.astype(np.float64)[:, None]).min(1)
+    assert np.array_equal(np.abs(got - v), dist)
+    # exact midpoints between neighbours go to the even mantissa
+    pos = np.sort(normal[normal > 0])
+    mids = ((pos[:-1] + pos[1:]) / 2).astype(np.float32)
+    enc = X.e4m3_encode(mids)
+    assert np.all((enc & 1) == 0)
+    assert np.all(np.isin(X.e4m3_decode(enc), pos))
+
+
+def test_e4m3_encode_flushes_below_smallest_normal():
+    v = np.array([2.0 ** -6, 0.99 * 2.0 ** -6, -(2.0 ** -7), 0.0, -0.0], np.float32)
+    assert list(X.e4m3_encode(v)) == [0x08, 0x00, 0x80, 0x00, 0x80]
+
+
+def test_split_reconstructs_bf16_blocks(rng):
+    x = f32_to_bf16_bits((rng.normal(0, 1, (32, 2304)) * np.exp(rng.normal(0, 2, (32, 1))))
+                         .astype(np.float32))
+    hi, lo, sc = X.split_fp8(x)
+    xf = bf16_bits_to_f32(x).astype(np.float64)
+    d = X.split_decode(hi, lo, sc)
+    amax = np.repeat(np.abs(xf).reshape(32, -1, 32).max(-1), 32, axis=-1)
+    # hi holds the top 4 significant bits, lo the next 4: error below 2**-9 of the block max
+    assert np.all(np.abs(d - xf) <= amax * 2.0 ** -9)
+    assert np.linalg.norm(d - xf) / np.linalg.norm(xf) < 1e-6
+    # the scaled block max lies in [128, 256): hi never saturates
+    assert np.all(np.abs(X.e4m3_decode(hi)) <= 256.0)
+
+
+def test_split_exact_for_four_bit_values_and_zero_blocks():
+    vals = np.array([1.0, -1.5, 0.75, 3.5, 0.0, 448.0 / 64, -0.125, 2.0], np.float32)
+    x = f32_to_bf16_bits(np.tile(vals, 8)[None, :].astype(np.float32))
+    x = np.concatenate((x, np.zeros((1, 64), np.uint16)), 0)
+    hi, lo, sc = X.split_fp8(x)
+    assert np.array_equal(X.split_decode(hi, lo, sc), bf16_bits_to_f32(x).astype(np.float64))
+    assert np.all(lo[0] & 0x7F == 0)  # no residual
+    assert np.all(hi[1] == 0) and np.all(lo[1] == 0) and np.all(sc[1] == 0)  # exponent -127 -> byte 0
+    # block exponents: block max 7.0 -> E = 2 -> e = -5 (byte 122)
+    assert np.all((sc[0] & 0xFF) == 122)
+
+
+def test_split_keeps_the_mxfp4_product_within_tolerance(rng):
+    """The whole point: x . W with x split is within the bf16 tolerance of x . W."""
+    w = rng.normal(0, 0.02, (256, 2304)).astype(np.float32)
+    p, s = X.quantize(w)
+    wd = X.dequantize(p, s).astype(np.float64)
+    x = f32_to_bf16_bits(rng.normal(0, 1, (16, 2304)).astype(np.float32))
+    ref = bf16_bits_to_f32(x).astype(np.float64) @ wd.T
+    got = X.split_decode(*X.split_fp8(x)) @ wd.T
+    assert np.max(np.abs(got - ref) / (2e-2 + 1e-2 * np.abs(ref))) < 0.01
