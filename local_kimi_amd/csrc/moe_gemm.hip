@@ -1159,6 +1159,336 @@ w4a16_stream_kernel(const GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// Persistent streaming GEMM over 16-row tiles (decode batches; 16-byte
+// weight loads). The grid is one resident block (8 waves) per CU slot. Block b
+// takes an equal contiguous range of units (tile, 16 * NT-column group) in
+// tile order, and wave w of the block takes units w, w + 8, ... of its range,
+// so the work is balanced to one unit per wave and there are no rounds of
+// blocks. Each wave keeps DEPTH k-steps of weights in flight across its units:
+// the loads of a unit's first k-steps are issued while the previous unit's
+// last k-steps are computed, so the weight stream never drains between tiles.
+// The block's tiles (segments) are staged in LDS once, nbuf at a time (a range
+// covering more tiles advances in phases with a block barrier between them);
+// their activation loads are issued before the weight ring, so staging does
+// not wait behind the ring. Tile descriptors and output rows sit in LDS: the
+// per-unit epilogue touches no global memory but its stores.
+constexpr int kPsMaxSegs = 8;     // tiles one block may cover (checked on the host)
+constexpr int kPsStageRegs = 24;  // 16-byte staging units per thread, all loaded before the ring
+
+template <int FMT>
+__device__ inline void ps_stage_store(uint4* afrag, float* offs, int frag, int c, int mr,
+                                      const uint4 v) {
+  const int t = c & 3, j = c >> 2;  // 16-byte unit c of the step feeds MFMA t, lane block j
+  uint4* dst = &afrag[(frag + t) * kWave + j * 16 + (mr ^ (4 * t + j))];
+  if constexpr (FMT != kFmtW4A16) {
+    *dst = v;
+  } else {
+    uint32_t q[4];
+    pair_x8(v, q);
+    *dst = make_uint4(q[0], q[1], q[2], q[3]);
+    float sx = sum8(sum_x8_dot(v));
+    sx += dpp_f32<kRowMirror>(sx);  // the 16 units of a (row, step) sit in one 16-lane row
+    if (c == 0) offs[frag * 16 + mr] = -kCodeOffset * sx;
+  }
+}
+
+// One 128-wide k-step of a lane's weights for the persistent kernel: the
+// 16-byte code load, and the scale as the aligned dword that holds it (W4A16
+// G = 128: the bf16 pair of steps 2q, 2q + 1; MXFP4: the step's four E8M0
+// bytes, one per 32-block). Dword scale loads keep the ring free of narrow
+// loads, whose zero-extension the compiler otherwise places at the loop latch,
+// where it waits for every load in flight.
+template <int FMT, int MATS, int NT>
+struct PsStep {
+  uint32_t w[MATS][NT][4];
+  uint32_t s[MATS][NT];
+
+  __device__ inline void load(const uint8_t* const (&wrow)[MATS][NT],
+                              const void* const (&srow)[MATS][NT], int step, int jq, int ksteps,
+                              const uint8_t* dummy) {
+    const bool live = step < ksteps;  // past the end: the shared zero line
+#pragma unroll
+    for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const uint8_t* wp = live ? wrow[mi][nt] + static_cast<int64_t>(step) * 64 + jq * 16 : dummy;
+        const uint4 v = *reinterpret_cast<const uint4*>(wp);
+        w[mi][nt][0] = v.x;
+        w[mi][nt][1] = v.y;
+        w[mi][nt][2] = v.z;
+        w[mi][nt][3] = v.w;
+        const void* sp;
+        if constexpr (FMT == kFmtW4A16)
+          sp = static_cast<const uint16_t*>(srow[mi][nt]) + (step & ~1);
+        else
+          sp = static_cast<const uint8_t*>(srow[mi][nt]) + static_cast<int64_t>(step) * 4;
+        s[mi][nt] = *static_cast<const uint32_t*>(live ? sp : static_cast<const void*>(dummy));
+      }
+  }
+};
+
+template <int FMT, int MATS, int DEPTH, bool GATHER, bool SCATTER>
+__global__ void __launch_bounds__(kStWaves * kWave)
+w4a16_persist_kernel(const GemmArgs g, int nbuf) {
+  static_assert(FMT == kFmtW4A16 || FMT == kFmtMxBf16, "bf16 activations, 16-byte weight loads");
+  static_assert(DEPTH % 2 == 0, "a slot's step parity is its index parity");
+  constexpr int NT = MATS == 2 ? 1 : 2;
+  constexpr bool kMx = FMT != kFmtW4A16;
+  constexpr int kThreads = kStWaves * kWave;
+  extern __shared__ uint4 smem[];
+  __shared__ int64_t seg_row[kPsMaxSegs][16];  // activation row of tile row m
+  __shared__ int32_t seg_out[kPsMaxSegs][16];  // output row of tile row m
+  __shared__ int32_t seg_exp[kPsMaxSegs], seg_rows[kPsMaxSegs];
+
+  const int64_t N = g.n, K = g.k;
+  const int ksteps = static_cast<int>(K >> 7);  // k % 128 == 0
+  const int rounds = ksteps / DEPTH;  // DEPTH divides ksteps (host-checked)
+  const int cgs = static_cast<int>((N + NT * 16 - 1) / (NT * 16));
+  const int total = *g.tile_count * cgs;
+  const int per = (total + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+  const int ub = static_cast<int>(blockIdx.x) * per;
+  const int ue = min(ub + per, total);
+  if (ub >= ue) return;  // block-uniform
+  const int t_first = ub / cgs;
+  const int nseg = min((ue - 1) / cgs - t_first + 1, kPsMaxSegs);
+  const int phases = (nseg + nbuf - 1) / nbuf;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform
+  const int jq = lane >> 4;
+  const int ln = lane & 15;
+  const int64_t rowb = K / 2;
+  const int64_t spr = K / g.group;
+  const uint8_t* const dummy = g_tail_pad;
+  uint4* const afrag = smem;  // [nbuf][ksteps][4][64]
+  float* const offs = reinterpret_cast<float*>(smem + nbuf * ksteps * 4 * kWave);  // [nbuf][ksteps][4][16]
+
+  // 1. descriptors and row tables of the block's tiles
+  if (tid < nseg * 16) {
+    const int s = tid >> 4, m = tid & 15;
+    const int4 d = reinterpret_cast<const int4*>(g.tiles)[t_first + s];
+    if (m == 0) {
+      seg_exp[s] = d.x;
+      seg_rows[s] = d.z;
+    }
+    if (m < d.z) {
+      const int32_t p = (GATHER || SCATTER) ? g.perm[d.y + m] : d.y + m;
+      seg_row[s][m] = GATHER ? p / g.routes : static_cast<int64_t>(d.y) + m;
+      seg_out[s][m] = SCATTER ? p : d.y + m;
+    }
+  }
+  __syncthreads();
+
+  // staging of phase p: the activation rows of segments [p * nbuf, p * nbuf + nbuf)
+  // into buffers 0..; unit u = (buffer-local step index) * 256 + m * 16 + c
+  const int seg_units = ksteps * 256;
+  auto stage_load = [&](int p, int u, uint4& v) -> bool {
+    const int sb = u / seg_units;
+    const int s = p * nbuf + sb;
+    const int r = u - sb * seg_units;
+    const int m = (r >> 4) & 15;
+    if (s >= nseg || m >= seg_rows[s]) return false;
+    const int64_t k0 = static_cast<int64_t>(r >> 8) * 128 + (r & 15) * 8;
+    v = *reinterpret_cast<const uint4*>(g.a + seg_row[s][m] * K + k0);
+    return true;
+  };
+  auto stage_store = [&](int u, const uint4 v) {
+    const int sb = u / seg_units;
+    const int r = u - sb * seg_units;
+    const int frag = (sb * ksteps + (r >> 8)) * 4;
+    ps_stage_store<FMT>(afrag, offs, frag, r & 15, (r >> 4) & 15, v);
+  };
+  constexpr int kStageRegs = kPsStageRegs;
+  const int stage_total = nbuf * seg_units;
+
+  // the wave's units: ub + wv + 8 i, i < n_w
+  const int n_w = ub + wv < ue ? (ue - 1 - (ub + wv)) / kStWaves + 1 : 0;
+  auto unit_tile = [&](int i, int& s, int& cgi) {
+    const int u = ub + wv + kStWaves * i;
+    const int t = u / cgs;
+    s = t - t_first;
+    cgi = u - t * cgs;
+  };
+  const uint8_t* lw[MATS][NT];
+  const void* lsr[MATS][NT];
+  auto set_ptrs = [&](int i) {
+    int s, cgi;
+    unit_tile(i, s, cgi);
+    const int64_t e = max(seg_exp[s], 0);  // invalid routes: read expert 0, store zeros
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int64_t col = static_cast<int64_t>(cgi) * (NT * 16) + nt * 16 + ln;
+      const int64_t cc = col < N ? col : N - 1;
+#pragma unroll
+      for (int mi = 0; mi < MATS; ++mi) {
+        lw[mi][nt] = g.wp[mi] + e * g.wstride + cc * rowb;
+        if constexpr (kMx)
+          lsr[mi][nt] = static_cast<const uint8_t*>(g.ws[mi]) + e * g.sstride + cc * spr;
+        else
+          lsr[mi][nt] = static_cast<const uint16_t*>(g.ws[mi]) + e * g.sstride + cc * spr;
+      }
+    }
+  };
+
+  // 2. the first phase's activation loads, then the first round of weights
+  uint4 sv[kStageRegs];
+  bool sl[kStageRegs];
+#pragma unroll
+  for (int q = 0; q < kStageRegs; ++q) {
+    const int u = q * kThreads + tid;
+    sl[q] = u < stage_total && stage_load(0, u, sv[q]);
+  }
+  PsStep<FMT, MATS, NT> w[DEPTH];
+  int li = 0, lr = 0;  // load cursor: unit, round
+  if (n_w > 0) set_ptrs(0);
+  // slot by slot, in the order the loop refills them, so the loop's per-slot
+  // waits hold on entry as well
+#pragma unroll
+  for (int j = 0; j < DEPTH; ++j) {
+    w[j].load(lw, lsr, n_w > 0 ? j : ksteps, jq, ksteps, dummy);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (++lr == rounds) {
+    lr = 0;
+    if (++li < n_w) set_ptrs(li);
+  }
+#pragma unroll
+  for (int q = 0; q < kStageRegs; ++q)  // stage_total <= kStageRegs * kThreads (host-checked)
+    if (sl[q]) stage_store(q * kThreads + tid, sv[q]);
+  __syncthreads();
+
+  // 3. stream
+  const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t tot[MATS][NT], acc[MATS][NT];
+#pragma unroll
+  for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      tot[mi][nt] = zero4;
+      acc[mi][nt] = zero4;
+    }
+  int ci = 0, cr = 0;  // compute cursor: unit, round
+  int cseg = 0, ccg = 0;
+  if (n_w > 0) unit_tile(0, cseg, ccg);
+
+  auto compute_step = [&](const PsStep<FMT, MATS, NT>& wj, int frag0, int odd) {
+    if constexpr (kMx) {
+      float sc[MATS][NT];
+#pragma unroll
+      for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) sc[mi][nt] = e8m0_to_f32((wj.s[mi][nt] >> (8 * jq)) & 0xFFu);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bf16x8_t af = __builtin_bit_cast(
+            bf16x8_t, afrag[(frag0 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
+#pragma unroll
+        for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            tot[mi][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                af, __builtin_bit_cast(bf16x8_t, unpack_fp4x8_bf16(wj.w[mi][nt][t], sc[mi][nt])),
+                tot[mi][nt], 0, 0, 0);
+      }
+    } else {
+      // the bf16 scale is decoded first, by an instruction the register
+      // allocator cannot recompute later: the ring register holding the
+      // loaded dword is then dead before the slot is refilled (otherwise the
+      // refill needs a copy at the loop head, which waits for every load)
+      float sc[MATS][NT];
+#pragma unroll
+      for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          if (odd)
+            asm("v_and_b32 %0, 0xffff0000, %1" : "=v"(sc[mi][nt]) : "v"(wj.s[mi][nt]));
+          else
+            asm("v_lshlrev_b32 %0, 16, %1" : "=v"(sc[mi][nt]) : "v"(wj.s[mi][nt]));
+        }
+      const f32x4_t neg = *reinterpret_cast<const f32x4_t*>(&offs[frag0 * 16 + jq * 4]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bf16x8_t af = __builtin_bit_cast(
+            bf16x8_t, afrag[(frag0 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
+#pragma unroll
+        for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            acc[mi][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                af, unpack_q8(wj.w[mi][nt][t]), t > 0 ? acc[mi][nt] : neg, 0, 0, 0);
+      }
+#pragma unroll
+      for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) tot[mi][nt] += sc[mi][nt] * acc[mi][nt];
+    }
+  };
+
+  uint16_t* const out = g.out[0];
+  for (int p = 0; p < phases; ++p) {
+    if (p > 0) {  // every wave is done with the previous phase's buffers
+      __syncthreads();
+      for (int u0 = 0; u0 < stage_total; u0 += kThreads) {
+        uint4 v;
+        if (stage_load(p, u0 + tid, v)) stage_store(u0 + tid, v);
+      }
+      __syncthreads();
+    }
+    const int seg_end = min(nseg, (p + 1) * nbuf);
+    while (ci < n_w && cseg < seg_end) {
+      const int fbase = (cseg - p * nbuf) * ksteps;
+      // one round: DEPTH k-steps of the current unit (DEPTH divides the
+      // k-steps); every slot is refilled, past the wave's last unit from the
+      // shared zero line
+#pragma unroll
+      for (int j = 0; j < DEPTH; ++j) {
+        const int step = cr * DEPTH + j;
+        compute_step(w[j], (fbase + step) * 4, j & 1);  // DEPTH even: the parity of step
+        // slot order is kept (each slot waits for its own loads only) and the
+        // refill follows the slot's compute, so the slot's registers are reused
+        __builtin_amdgcn_sched_barrier(0);
+        w[j].load(lw, lsr, li < n_w ? lr * DEPTH + j : ksteps, jq, ksteps, dummy);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (++lr == rounds) {
+        lr = 0;
+        if (++li < n_w) set_ptrs(li);
+      }
+      if (++cr == rounds) {  // the unit is complete: store it
+        const int rows = seg_rows[cseg];
+        const bool zero = seg_exp[cseg] < 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = jq * 4 + i;
+          if (m >= rows) continue;
+          const int64_t orow = seg_out[cseg][m];
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            const int64_t col = static_cast<int64_t>(ccg) * (NT * 16) + nt * 16 + ln;
+            if (col >= N) continue;
+            uint16_t v;
+            if constexpr (MATS == 2)
+              v = g.act == kActSitu ? situ_bf16(tot[0][nt][i], tot[1][nt][i], g.situ_beta,
+                                                g.situ_linear_beta)
+                                    : swiglu_bf16(tot[0][nt][i], tot[1][nt][i]);
+            else
+              v = store_value<FMT>(tot[0][nt][i]);
+            out[orow * N + col] = zero ? static_cast<uint16_t>(0) : v;
+          }
+        }
+#pragma unroll
+        for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) tot[mi][nt] = zero4;
+        cr = 0;
+        if (++ci < n_w) unit_tile(ci, cseg, ccg);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // fp8 hi/lo split of bf16 activations for the scaled fp4 MFMA. Per block of
 // 32 values along k: x ~= hi * 2^e_hi + lo * 2^e_lo with OCP E4M3 codes
 // (nearest, ties to even; magnitudes under 2^-6 flush to signed zero) and
@@ -1460,6 +1790,13 @@ void stream_one(const GemmArgs& g, unsigned blocks, size_t lds, hipStream_t s) {
   fn<<<blocks, kStWaves * kWave, lds, s>>>(g);
 }
 
+// LK_MOE_PERSIST=0 takes the per-tile streaming kernel for 16-row tiles (read
+// per call, like LK_MOE_GEMM).
+bool persist_disabled() {
+  const char* v = getenv("LK_MOE_PERSIST");
+  return v && strcmp(v, "0") == 0;
+}
+
 template <int FMT, int MATS, int MT, bool WIDE>
 void stream_dispatch(const GemmArgs& g, Mode mode, unsigned blocks, size_t lds, hipStream_t s) {
   if constexpr (FMT == kFmtMxF16) {
@@ -1483,6 +1820,88 @@ bool stream_fits(int64_t k, int mt, int64_t group, bool mx) {
   return stream_lds_bytes(k, mt) <= static_cast<size_t>(kStMaxLds);
 }
 
+// ---- persistent 16-row streaming GEMM: host side ----
+
+constexpr int kPsMaxLds = 160 * 1024 - 2048;  // dynamic LDS of one persistent block
+
+template <int FMT, int MATS, int DEPTH, bool GATHER, bool SCATTER>
+int persist_one(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hipStream_t s) {
+  auto* fn = &w4a16_persist_kernel<FMT, MATS, DEPTH, GATHER, SCATTER>;
+  struct Cfg {
+    int device = -1, blocks_per_cu = 0, cus = 0;
+    size_t lds = 0;
+  };
+  static Cfg cfg[16];  // per device; the attribute is per function
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return -1;
+  Cfg& c = cfg[dev];
+  if (c.device != dev || c.lds != lds) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kPsMaxLds) != hipSuccess)
+      return -1;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kStWaves * kWave, lds) !=
+            hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        per_cu < 1 || cus < 1)
+      return -1;
+    c = Cfg{dev, per_cu, cus, lds};
+  }
+  const int64_t grid = static_cast<int64_t>(c.cus) * c.blocks_per_cu;
+  constexpr int NT = MATS == 2 ? 1 : 2;
+  const int64_t cgs = (g.n + NT * 16 - 1) / (NT * 16);
+  // a block's range covers at most (per - 1) / cgs + 2 tiles; its tables hold kPsMaxSegs
+  const int64_t per = (tiles_bound * cgs + grid - 1) / grid;
+  if ((per - 1) / cgs + 2 > kPsMaxSegs) return -1;
+  if (tiles_bound * cgs >= (1LL << 31)) return -1;
+  fn<<<static_cast<unsigned>(grid), kStWaves * kWave, lds, s>>>(g, nbuf);
+  return 0;
+}
+
+template <int FMT, int MATS, bool GATHER, bool SCATTER>
+int persist_depth(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hipStream_t s) {
+  // the ring depth divides the k-steps (at least one whole round per unit)
+  const int64_t ksteps = g.k / 128;
+  if (ksteps >= 6 && ksteps % 6 == 0)
+    return persist_one<FMT, MATS, 6, GATHER, SCATTER>(g, nbuf, lds, tiles_bound, s);
+  if (ksteps >= 4 && ksteps % 4 == 0)
+    return persist_one<FMT, MATS, 4, GATHER, SCATTER>(g, nbuf, lds, tiles_bound, s);
+  return -1;
+}
+
+// Launches the persistent 16-row GEMM when it applies (schedule modes, 16-byte
+// weight loads, the block's tiles fit in LDS) and returns the launch status;
+// returns kPsNotApplicable when it does not, so the caller takes the per-tile
+// streaming kernel.
+constexpr int kPsNotApplicable = -1000;
+template <int FMT, int MATS>
+int persist_launch(const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_t s,
+                   const char* what) {
+  if constexpr (FMT != kFmtW4A16 && FMT != kFmtMxBf16) {
+    return kPsNotApplicable;
+  } else {
+    if (persist_disabled() || mode == Mode::Dense || g.outputs != 1) return kPsNotApplicable;
+    // W4A16: G = 128 and an even number of groups per row (dword scale pairs stay in the row)
+    if (g.k % 128 != 0 || (FMT == kFmtW4A16 && (g.group != 128 || g.k % 256 != 0)))
+      return kPsNotApplicable;
+    const size_t one = stream_lds_bytes(g.k, 1);
+    const int nbuf = 2 * one <= static_cast<size_t>(kPsMaxLds) ? 2 : (one <= static_cast<size_t>(kPsMaxLds) ? 1 : 0);
+    if (nbuf == 0) return kPsNotApplicable;
+    const size_t lds = nbuf * one;
+    // a phase's activations are staged from one batch of registers per thread
+    if (nbuf * (g.k / 128) * 256 > kPsStageRegs * kStWaves * kWave) return kPsNotApplicable;
+    int rc = -1;
+    switch (mode) {
+      case Mode::Gather: rc = persist_depth<FMT, MATS, true, false>(g, nbuf, lds, tiles_bound, s); break;
+      case Mode::Scatter: rc = persist_depth<FMT, MATS, false, true>(g, nbuf, lds, tiles_bound, s); break;
+      case Mode::GatherScatter: rc = persist_depth<FMT, MATS, true, true>(g, nbuf, lds, tiles_bound, s); break;
+      default: break;
+    }
+    if (rc < 0) return kPsNotApplicable;
+    return check_launch(what);
+  }
+}
+
 template <int FMT, int MATS>
 int stream_launch(GemmArgs g, Mode mode, int64_t tiles, int mt, hipStream_t s, const char* what) {
   constexpr int NT = MATS == 2 ? 1 : 2;
@@ -1500,6 +1919,10 @@ int stream_launch(GemmArgs g, Mode mode, int64_t tiles, int mt, hipStream_t s, c
     if (mt == 1) stream_dispatch<FMT, MATS, 1, true>(g, mode, nb, lds, s);
     else stream_dispatch<FMT, MATS, 4, true>(g, mode, nb, lds, s);
   } else if (mt == 1) {
+    if (wide) {
+      const int rc = persist_launch<FMT, MATS>(g, mode, tiles, s, what);
+      if (rc != kPsNotApplicable) return rc;
+    }
     if (wide) stream_dispatch<FMT, MATS, 1, kWideOk>(g, mode, nb, lds, s);
     else stream_dispatch<FMT, MATS, 1, false>(g, mode, nb, lds, s);
   } else {
