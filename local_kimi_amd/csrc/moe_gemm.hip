@@ -1162,9 +1162,8 @@ w4a16_stream_kernel(const GemmArgs g) {
 // Persistent streaming GEMM over 16-row tiles (decode batches; 16-byte
 // weight loads). The grid is one resident block (8 waves) per CU slot. Block b
 // takes an equal contiguous range of units (tile, 16 * NT-column group) in
-// tile order, and wave w of the block takes units w, w + 8, ... of its range,
-// so the work is balanced to one unit per wave and there are no rounds of
-// blocks. Each wave keeps DEPTH k-steps of weights in flight across its units:
+// tile order, and its waves claim the units of the range one at a time, in
+// order, so there are no rounds of blocks and a CU's waves finish together. Each wave keeps DEPTH k-steps of weights in flight across its units:
 // the loads of a unit's first k-steps are issued while the previous unit's
 // last k-steps are computed, so the weight stream never drains between tiles.
 // The block's tiles (segments) are staged in LDS once, nbuf at a time (a range
@@ -1174,6 +1173,7 @@ w4a16_stream_kernel(const GemmArgs g) {
 // per-unit epilogue touches no global memory but its stores.
 constexpr int kPsMaxSegs = 8;     // tiles one block may cover (checked on the host)
 constexpr int kPsStageRegs = 24;  // 16-byte staging units per thread, all loaded before the ring
+constexpr int kPsEarlyPairs = 1;  // ring pairs issued before the first staging completes
 
 template <int FMT>
 __device__ inline void ps_stage_store(uint4* afrag, float* offs, int frag, int c, int mr,
@@ -1192,38 +1192,57 @@ __device__ inline void ps_stage_store(uint4* afrag, float* offs, int frag, int c
   }
 }
 
-// One 128-wide k-step of a lane's weights for the persistent kernel: the
-// 16-byte code load, and the scale as the aligned dword that holds it (W4A16
-// G = 128: the bf16 pair of steps 2q, 2q + 1; MXFP4: the step's four E8M0
-// bytes, one per 32-block). Dword scale loads keep the ring free of narrow
-// loads, whose zero-extension the compiler otherwise places at the loop latch,
-// where it waits for every load in flight.
+// Two consecutive 128-wide k-steps (2q, 2q + 1) of a lane's weights for the
+// persistent kernel: per matrix and column tile, the two 16-byte code loads
+// are issued back to back (they are the two halves of one 128-byte line of
+// the weight row, so the line is fetched once: requested apart, each half
+// costs a fetch of its own), and one scale load serves both steps (W4A16
+// G = 128: the bf16 pair, low half = step 2q; MXFP4: eight E8M0 bytes, four
+// per step). Whole-dword scale loads keep the ring free of narrow loads, whose
+// zero-extension the compiler otherwise places at the loop latch, where it
+// waits for every load in flight.
 template <int FMT, int MATS, int NT>
-struct PsStep {
-  uint32_t w[MATS][NT][4];
-  uint32_t s[MATS][NT];
+struct PsPair {
+  static constexpr int kSw = FMT == kFmtW4A16 ? 1 : 2;  // scale dwords per pair
+  uint32_t w[2][MATS][NT][4];
+  uint32_t s[MATS][NT][kSw];
 
   __device__ inline void load(const uint8_t* const (&wrow)[MATS][NT],
-                              const void* const (&srow)[MATS][NT], int step, int jq, int ksteps,
+                              const void* const (&srow)[MATS][NT], int step0, int jq, int ksteps,
                               const uint8_t* dummy) {
-    const bool live = step < ksteps;  // past the end: the shared zero line
+    const bool live = step0 < ksteps;  // step0 even, ksteps even; past the end: the zero line
 #pragma unroll
     for (int mi = 0; mi < MATS; ++mi)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const uint8_t* wp = live ? wrow[mi][nt] + static_cast<int64_t>(step) * 64 + jq * 16 : dummy;
-        const uint4 v = *reinterpret_cast<const uint4*>(wp);
-        w[mi][nt][0] = v.x;
-        w[mi][nt][1] = v.y;
-        w[mi][nt][2] = v.z;
-        w[mi][nt][3] = v.w;
         const void* sp;
         if constexpr (FMT == kFmtW4A16)
-          sp = static_cast<const uint16_t*>(srow[mi][nt]) + (step & ~1);
+          sp = static_cast<const uint16_t*>(srow[mi][nt]) + step0;
         else
-          sp = static_cast<const uint8_t*>(srow[mi][nt]) + static_cast<int64_t>(step) * 4;
-        s[mi][nt] = *static_cast<const uint32_t*>(live ? sp : static_cast<const void*>(dummy));
+          sp = static_cast<const uint8_t*>(srow[mi][nt]) + static_cast<int64_t>(step0) * 4;
+        if (!live) sp = dummy;
+        if constexpr (kSw == 1) {
+          s[mi][nt][0] = *static_cast<const uint32_t*>(sp);
+        } else {
+          const uint2 v = *static_cast<const uint2*>(sp);
+          s[mi][nt][0] = v.x;
+          s[mi][nt][1] = v.y;
+        }
       }
+#pragma unroll
+    for (int mi = 0; mi < MATS; ++mi)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint8_t* wp =
+              live ? wrow[mi][nt] + static_cast<int64_t>(step0 + h) * 64 + jq * 16 : dummy;
+          const uint4 v = *reinterpret_cast<const uint4*>(wp);
+          w[h][mi][nt][0] = v.x;
+          w[h][mi][nt][1] = v.y;
+          w[h][mi][nt][2] = v.z;
+          w[h][mi][nt][3] = v.w;
+        }
   }
 };
 
@@ -1231,7 +1250,9 @@ template <int FMT, int MATS, int DEPTH, bool GATHER, bool SCATTER>
 __global__ void __launch_bounds__(kStWaves * kWave)
 w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   static_assert(FMT == kFmtW4A16 || FMT == kFmtMxBf16, "bf16 activations, 16-byte weight loads");
-  static_assert(DEPTH % 2 == 0, "a slot's step parity is its index parity");
+  static_assert(DEPTH % 2 == 0, "the ring holds pairs of k-steps");
+  constexpr int kPairs = DEPTH / 2;
+  static_assert(kPsEarlyPairs < kPairs, "the staging barrier sits inside the first round");
   constexpr int NT = MATS == 2 ? 1 : 2;
   constexpr bool kMx = FMT != kFmtW4A16;
   constexpr int kThreads = kStWaves * kWave;
@@ -1239,6 +1260,7 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   __shared__ int64_t seg_row[kPsMaxSegs][16];  // activation row of tile row m
   __shared__ int32_t seg_out[kPsMaxSegs][16];  // output row of tile row m
   __shared__ int32_t seg_exp[kPsMaxSegs], seg_rows[kPsMaxSegs];
+  __shared__ int32_t next_unit;  // the block's next unclaimed unit
 
   const int64_t N = g.n, K = g.k;
   const int ksteps = static_cast<int>(K >> 7);  // k % 128 == 0
@@ -1265,6 +1287,7 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   float* const offs = reinterpret_cast<float*>(smem + nbuf * ksteps * 4 * kWave);  // [nbuf][ksteps][4][16]
 
   // 1. descriptors and row tables of the block's tiles
+  if (tid == 0) next_unit = ub;
   if (tid < nseg * 16) {
     const int s = tid >> 4, m = tid & 15;
     const int4 d = reinterpret_cast<const int4*>(g.tiles)[t_first + s];
@@ -1302,19 +1325,25 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   constexpr int kStageRegs = kPsStageRegs;
   const int stage_total = nbuf * seg_units;
 
-  // the wave's units: ub + wv + 8 i, i < n_w
-  const int n_w = ub + wv < ue ? (ue - 1 - (ub + wv)) / kStWaves + 1 : 0;
-  auto unit_tile = [&](int i, int& s, int& cgi) {
-    const int u = ub + wv + kStWaves * i;
+  // Waves claim the block's units in order, one at a time, when their ring
+  // reaches a new unit: a wave that streams faster takes more units (the waves
+  // of a CU do not get equal shares of its memory bandwidth). A claim at or
+  // past ue means no unit.
+  auto claim = [&]() -> int {
+    int u = 0;
+    if (lane == 0) u = atomicAdd(&next_unit, 1);
+    return __builtin_amdgcn_readfirstlane(u);
+  };
+  auto unit_tile = [&](int u, int& s, int& cgi) {
     const int t = u / cgs;
     s = t - t_first;
     cgi = u - t * cgs;
   };
   const uint8_t* lw[MATS][NT];
   const void* lsr[MATS][NT];
-  auto set_ptrs = [&](int i) {
+  auto set_ptrs = [&](int u) {
     int s, cgi;
-    unit_tile(i, s, cgi);
+    unit_tile(u, s, cgi);
     const int64_t e = max(seg_exp[s], 0);  // invalid routes: read expert 0, store zeros
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -1331,7 +1360,10 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
     }
   };
 
-  // 2. the first phase's activation loads, then the first round of weights
+  // 2. the first phase's activation loads, then the first kPsEarlyPairs
+  // pairs of k-steps of weights; the rest of the first round goes out once the
+  // activations are staged, so the activation rows that miss L2 do not queue
+  // behind every CU's whole first round
   uint4 sv[kStageRegs];
   bool sl[kStageRegs];
 #pragma unroll
@@ -1339,24 +1371,28 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
     const int u = q * kThreads + tid;
     sl[q] = u < stage_total && stage_load(0, u, sv[q]);
   }
-  PsStep<FMT, MATS, NT> w[DEPTH];
-  int li = 0, lr = 0;  // load cursor: unit, round
-  if (n_w > 0) set_ptrs(0);
+  PsPair<FMT, MATS, NT> w[kPairs];
+  int lu = claim(), lr = 0;  // load cursor: unit, round
+  if (lu < ue) set_ptrs(lu);
   // slot by slot, in the order the loop refills them, so the loop's per-slot
   // waits hold on entry as well
 #pragma unroll
-  for (int j = 0; j < DEPTH; ++j) {
-    w[j].load(lw, lsr, n_w > 0 ? j : ksteps, jq, ksteps, dummy);
+  for (int j = 0; j < kPairs; ++j) {
+    if (j == kPsEarlyPairs) {
+#pragma unroll
+      for (int q = 0; q < kStageRegs; ++q)  // stage_total <= kStageRegs * kThreads (host-checked)
+        if (sl[q]) stage_store(q * kThreads + tid, sv[q]);
+      __syncthreads();
+    }
+    w[j].load(lw, lsr, lu < ue ? 2 * j : ksteps, jq, ksteps, dummy);
     __builtin_amdgcn_sched_barrier(0);
   }
+  int issued = lu;  // the unit of the round whose loads were issued last
   if (++lr == rounds) {
     lr = 0;
-    if (++li < n_w) set_ptrs(li);
+    lu = claim();
+    if (lu < ue) set_ptrs(lu);
   }
-#pragma unroll
-  for (int q = 0; q < kStageRegs; ++q)  // stage_total <= kStageRegs * kThreads (host-checked)
-    if (sl[q]) stage_store(q * kThreads + tid, sv[q]);
-  __syncthreads();
 
   // 3. stream
   const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
@@ -1368,17 +1404,18 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
       tot[mi][nt] = zero4;
       acc[mi][nt] = zero4;
     }
-  int ci = 0, cr = 0;  // compute cursor: unit, round
+  int cu = issued, cr = 0;  // compute cursor: unit, round
   int cseg = 0, ccg = 0;
-  if (n_w > 0) unit_tile(0, cseg, ccg);
+  if (cu < ue) unit_tile(cu, cseg, ccg);
 
-  auto compute_step = [&](const PsStep<FMT, MATS, NT>& wj, int frag0, int odd) {
+  // step 2q + h of pair wj (h = 0, 1), activation fragments from frag0
+  auto compute_step = [&](const PsPair<FMT, MATS, NT>& wj, int h, int frag0) {
     if constexpr (kMx) {
       float sc[MATS][NT];
 #pragma unroll
       for (int mi = 0; mi < MATS; ++mi)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) sc[mi][nt] = e8m0_to_f32((wj.s[mi][nt] >> (8 * jq)) & 0xFFu);
+        for (int nt = 0; nt < NT; ++nt) sc[mi][nt] = e8m0_to_f32((wj.s[mi][nt][h] >> (8 * jq)) & 0xFFu);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const bf16x8_t af = __builtin_bit_cast(
@@ -1388,7 +1425,7 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt)
             tot[mi][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                af, __builtin_bit_cast(bf16x8_t, unpack_fp4x8_bf16(wj.w[mi][nt][t], sc[mi][nt])),
+                af, __builtin_bit_cast(bf16x8_t, unpack_fp4x8_bf16(wj.w[h][mi][nt][t], sc[mi][nt])),
                 tot[mi][nt], 0, 0, 0);
       }
     } else {
@@ -1401,10 +1438,10 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
       for (int mi = 0; mi < MATS; ++mi)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-          if (odd)
-            asm("v_and_b32 %0, 0xffff0000, %1" : "=v"(sc[mi][nt]) : "v"(wj.s[mi][nt]));
+          if (h)
+            asm("v_and_b32 %0, 0xffff0000, %1" : "=v"(sc[mi][nt]) : "v"(wj.s[mi][nt][0]));
           else
-            asm("v_lshlrev_b32 %0, 16, %1" : "=v"(sc[mi][nt]) : "v"(wj.s[mi][nt]));
+            asm("v_lshlrev_b32 %0, 16, %1" : "=v"(sc[mi][nt]) : "v"(wj.s[mi][nt][0]));
         }
       const f32x4_t neg = *reinterpret_cast<const f32x4_t*>(&offs[frag0 * 16 + jq * 4]);
 #pragma unroll
@@ -1416,7 +1453,7 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt)
             acc[mi][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                af, unpack_q8(wj.w[mi][nt][t]), t > 0 ? acc[mi][nt] : neg, 0, 0, 0);
+                af, unpack_q8(wj.w[h][mi][nt][t]), t > 0 ? acc[mi][nt] : neg, 0, 0, 0);
       }
 #pragma unroll
       for (int mi = 0; mi < MATS; ++mi)
@@ -1436,24 +1473,27 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
       __syncthreads();
     }
     const int seg_end = min(nseg, (p + 1) * nbuf);
-    while (ci < n_w && cseg < seg_end) {
+    while (cu < ue && cseg < seg_end) {
       const int fbase = (cseg - p * nbuf) * ksteps;
       // one round: DEPTH k-steps of the current unit (DEPTH divides the
       // k-steps); every slot is refilled, past the wave's last unit from the
       // shared zero line
 #pragma unroll
-      for (int j = 0; j < DEPTH; ++j) {
-        const int step = cr * DEPTH + j;
-        compute_step(w[j], (fbase + step) * 4, j & 1);  // DEPTH even: the parity of step
-        // slot order is kept (each slot waits for its own loads only) and the
-        // refill follows the slot's compute, so the slot's registers are reused
+      for (int j = 0; j < kPairs; ++j) {
+        const int step = cr * DEPTH + 2 * j;
+        compute_step(w[j], 0, (fbase + step) * 4);
+        compute_step(w[j], 1, (fbase + step + 1) * 4);
+        // pair order is kept (each pair waits for its own loads only) and the
+        // refill follows the pair's compute, so its registers are reused
         __builtin_amdgcn_sched_barrier(0);
-        w[j].load(lw, lsr, li < n_w ? lr * DEPTH + j : ksteps, jq, ksteps, dummy);
+        w[j].load(lw, lsr, lu < ue ? lr * DEPTH + 2 * j : ksteps, jq, ksteps, dummy);
         __builtin_amdgcn_sched_barrier(0);
       }
+      issued = lu;
       if (++lr == rounds) {
         lr = 0;
-        if (++li < n_w) set_ptrs(li);
+        lu = claim();
+        if (lu < ue) set_ptrs(lu);
       }
       if (++cr == rounds) {  // the unit is complete: store it
         const int rows = seg_rows[cseg];
@@ -1482,7 +1522,8 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt) tot[mi][nt] = zero4;
         cr = 0;
-        if (++ci < n_w) unit_tile(ci, cseg, ccg);
+        cu = issued;  // the load cursor is one round ahead: its last round's unit
+        if (cu < ue) unit_tile(cu, cseg, ccg);
       }
     }
   }
@@ -1864,6 +1905,8 @@ int persist_depth(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, 
   const int64_t ksteps = g.k / 128;
   if (ksteps >= 6 && ksteps % 6 == 0)
     return persist_one<FMT, MATS, 6, GATHER, SCATTER>(g, nbuf, lds, tiles_bound, s);
+  if (ksteps >= 8 && ksteps % 8 == 0)
+    return persist_one<FMT, MATS, 8, GATHER, SCATTER>(g, nbuf, lds, tiles_bound, s);
   if (ksteps >= 4 && ksteps % 4 == 0)
     return persist_one<FMT, MATS, 4, GATHER, SCATTER>(g, nbuf, lds, tiles_bound, s);
   return -1;

@@ -5,10 +5,10 @@ perform the same MFMA chains in the same order, so their outputs must be
 bit-identical; the per-tile kernel is itself checked against the oracle
 elsewhere, and every case here is also checked against the oracle within the
 quantized-matmul tolerance (1e-2 relative / 2e-2 absolute in bf16). Shapes
-are chosen to reach both ring depths (6 k-steps for k = 768, 4 for k = 512),
-both weight formats, routes outside the bank, and a tile list longer than the
-grid, where one block covers more tiles than its two LDS buffers and stages
-them in phases.
+are chosen to reach every ring depth (6 k-steps for k = 768, 8 for k = 1024,
+4 for k = 512), both weight formats, routes outside the bank, and a tile list
+longer than the grid, where one block covers more tiles than its two LDS
+buffers and stages them in phases.
 """
 
 from __future__ import annotations
@@ -72,7 +72,7 @@ def _both(monkeypatch, fn, *args):
 
 
 @pytest.mark.parametrize("weights", ["w4a16", "mxfp4"])
-@pytest.mark.parametrize("h,inter,tokens", [(768, 512, 40), (512, 768, 13)])
+@pytest.mark.parametrize("h,inter,tokens", [(768, 512, 40), (512, 768, 13), (1024, 512, 21)])
 def test_moe_block_persistent_matches_per_tile_and_oracle(rng, monkeypatch, weights, h, inter,
                                                           tokens):
     from local_kimi_amd.kernels import mxfp4_moe_block, w4a16_moe_forward
