@@ -1172,7 +1172,8 @@ w4a16_stream_kernel(const GemmArgs g) {
 // not wait behind the ring. Tile descriptors and output rows sit in LDS: the
 // per-unit epilogue touches no global memory but its stores.
 constexpr int kPsMaxSegs = 8;     // tiles one block may cover (checked on the host)
-constexpr int kPsStageRegs = 24;  // 16-byte staging units per thread, all loaded before the ring
+constexpr int kPsHalfMax = 12;    // staging units per thread and LDS buffer (k-steps <= 24)
+constexpr int kPsBatch = 6;       // staging units in flight per thread in a later phase
 constexpr int kPsEarlyPairs = 1;  // ring pairs issued before the first staging completes
 
 template <int FMT>
@@ -1303,27 +1304,46 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   }
   __syncthreads();
 
-  // staging of phase p: the activation rows of segments [p * nbuf, p * nbuf + nbuf)
-  // into buffers 0..; unit u = (buffer-local step index) * 256 + m * 16 + c
-  const int seg_units = ksteps * 256;
-  auto stage_load = [&](int p, int u, uint4& v) -> bool {
-    const int sb = u / seg_units;
-    const int s = p * nbuf + sb;
-    const int r = u - sb * seg_units;
-    const int m = (r >> 4) & 15;
-    if (s >= nseg || m >= seg_rows[s]) return false;
-    const int64_t k0 = static_cast<int64_t>(r >> 8) * 128 + (r & 15) * 8;
-    v = *reinterpret_cast<const uint4*>(g.a + seg_row[s][m] * K + k0);
-    return true;
+  // Staging of phase p (the activation rows of segments p * nbuf .. into
+  // buffers 0 .. nbuf - 1): thread tid owns 16-byte chunk sc of row sm at the
+  // k-steps of parity sl, so buffer sb takes half = ksteps / 2 units per
+  // thread, unit ii at k-step 2 ii + sl. Buffer and unit are compile-time in
+  // the unrolled loops, so each unit is one load at a fixed offset from the
+  // buffer's row pointer and one store: the staging runs once per block with
+  // a cold instruction cache, so its code is kept short. Rows past a tile's
+  // end (and buffers past the block's last tile) stage the block's first row:
+  // their MFMA rows are never stored. Every staged load is stored, so no load
+  // is left outstanding on any path (the compiler would otherwise wait for
+  // every load in flight inside the weight loop).
+  const int sc = tid & 15, sm = (tid >> 4) & 15, sl = tid >> 8;
+  const int half = ksteps >> 1;  // ksteps is even (DEPTH is); half <= kPsHalfMax (host-checked)
+  const uint16_t* rp[2];
+  auto stage_rows = [&](int p) {
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const int s = p * nbuf + sb;
+      const bool ok = sb < nbuf && s < nseg && sm < seg_rows[s];
+      const int64_t row = ok ? seg_row[s][sm] : seg_row[0][0];
+      rp[sb] = g.a + row * K + sl * 128 + sc * 8;
+    }
   };
-  auto stage_store = [&](int u, const uint4 v) {
-    const int sb = u / seg_units;
-    const int r = u - sb * seg_units;
-    const int frag = (sb * ksteps + (r >> 8)) * 4;
-    ps_stage_store<FMT>(afrag, offs, frag, r & 15, (r >> 4) & 15, v);
+  auto stage_loads = [&](uint4 (&v)[2][kPsHalfMax]) {
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int ii = 0; ii < kPsHalfMax; ++ii)
+        if (sb < nbuf && ii < half) v[sb][ii] = *reinterpret_cast<const uint4*>(rp[sb] + ii * 256);
   };
-  constexpr int kStageRegs = kPsStageRegs;
-  const int stage_total = nbuf * seg_units;
+  auto stage_stores = [&](const uint4 (&v)[2][kPsHalfMax]) {
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      if (sb >= nbuf) continue;
+      const int fb = sb * ksteps + sl;
+#pragma unroll
+      for (int ii = 0; ii < kPsHalfMax; ++ii)
+        if (ii < half) ps_stage_store<FMT>(afrag, offs, (fb + 2 * ii) * 4, sc, sm, v[sb][ii]);
+    }
+  };
 
   // Waves claim the block's units in order, one at a time, when their ring
   // reaches a new unit: a wave that streams faster takes more units (the waves
@@ -1364,13 +1384,9 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   // pairs of k-steps of weights; the rest of the first round goes out once the
   // activations are staged, so the activation rows that miss L2 do not queue
   // behind every CU's whole first round
-  uint4 sv[kStageRegs];
-  bool sl[kStageRegs];
-#pragma unroll
-  for (int q = 0; q < kStageRegs; ++q) {
-    const int u = q * kThreads + tid;
-    sl[q] = u < stage_total && stage_load(0, u, sv[q]);
-  }
+  stage_rows(0);
+  uint4 sv[2][kPsHalfMax];
+  stage_loads(sv);
   PsPair<FMT, MATS, NT> w[kPairs];
   int lu = claim(), lr = 0;  // load cursor: unit, round
   if (lu < ue) set_ptrs(lu);
@@ -1379,9 +1395,7 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
 #pragma unroll
   for (int j = 0; j < kPairs; ++j) {
     if (j == kPsEarlyPairs) {
-#pragma unroll
-      for (int q = 0; q < kStageRegs; ++q)  // stage_total <= kStageRegs * kThreads (host-checked)
-        if (sl[q]) stage_store(q * kThreads + tid, sv[q]);
+      stage_stores(sv);
       __syncthreads();
     }
     w[j].load(lw, lsr, lu < ue ? 2 * j : ksteps, jq, ksteps, dummy);
@@ -1466,9 +1480,21 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   for (int p = 0; p < phases; ++p) {
     if (p > 0) {  // every wave is done with the previous phase's buffers
       __syncthreads();
-      for (int u0 = 0; u0 < stage_total; u0 += kThreads) {
-        uint4 v;
-        if (stage_load(p, u0 + tid, v)) stage_store(u0 + tid, v);
+      // a later phase (blocks covering more tiles than buffers): batches of
+      // kPsBatch units, in a rolled loop to keep registers for the ring
+      stage_rows(p);
+      for (int sb = 0; sb < nbuf; ++sb) {
+        for (int i0 = 0; i0 < half; i0 += kPsBatch) {
+          uint4 pv[kPsBatch];
+#pragma unroll
+          for (int b = 0; b < kPsBatch; ++b)
+            if (i0 + b < half)
+              pv[b] = *reinterpret_cast<const uint4*>(rp[sb] + (i0 + b) * 256);
+#pragma unroll
+          for (int b = 0; b < kPsBatch; ++b)
+            if (i0 + b < half)
+              ps_stage_store<FMT>(afrag, offs, (sb * ksteps + sl + 2 * (i0 + b)) * 4, sc, sm, pv[b]);
+        }
       }
       __syncthreads();
     }
@@ -1932,7 +1958,7 @@ int persist_launch(const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_
     if (nbuf == 0) return kPsNotApplicable;
     const size_t lds = nbuf * one;
     // a phase's activations are staged from one batch of registers per thread
-    if (nbuf * (g.k / 128) * 256 > kPsStageRegs * kStWaves * kWave) return kPsNotApplicable;
+    if (g.k / 128 > 2 * kPsHalfMax) return kPsNotApplicable;
     int rc = -1;
     switch (mode) {
       case Mode::Gather: rc = persist_depth<FMT, MATS, true, false>(g, nbuf, lds, tiles_bound, s); break;
