@@ -26,10 +26,11 @@ from . import w4a16 as _w
 
 # tokens from which the MoE block runs expert-major (each expert read once).
 # Below it the token-major kernels win: at the Kimi-Linear shape with
-# Zipf(1.1) routing, 6 tokens take 67 us token-major vs 72 us expert-major,
-# 8 tokens 83 us vs 77 us (the expert-major chain has a ~50 us floor of six
-# launches: router, two schedule passes, two GEMMs, combine).
-MOE_EXPERT_MAJOR_MIN_TOKENS = 8
+# Zipf(1.1) routing, 3 tokens take 39.3 us token-major vs 44.1 us
+# expert-major, 4 tokens 47.7 us vs 46.2 us, 6 tokens 65.8 us vs 51.9 us (the
+# expert-major chain has a floor of about 40 us: router, schedule, two
+# persistent GEMMs, combine).
+MOE_EXPERT_MAJOR_MIN_TOKENS = 4
 # bank entries (routed + shared) the expert-major schedule supports
 MOE_EXPERT_MAJOR_MAX_EXPERTS = 512
 
