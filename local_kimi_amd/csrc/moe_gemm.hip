@@ -1256,7 +1256,6 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   static_assert(kPsEarlyPairs < kPairs, "the staging barrier sits inside the first round");
   constexpr int NT = MATS == 2 ? 1 : 2;
   constexpr bool kMx = FMT != kFmtW4A16;
-  constexpr int kThreads = kStWaves * kWave;
   extern __shared__ uint4 smem[];
   __shared__ int64_t seg_row[kPsMaxSegs][16];  // activation row of tile row m
   __shared__ int32_t seg_out[kPsMaxSegs][16];  // output row of tile row m
@@ -1278,7 +1277,6 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform
   const int jq = lane >> 4;
   const int ln = lane & 15;
   const int64_t rowb = K / 2;
@@ -2004,6 +2002,21 @@ int stream_launch(GemmArgs g, Mode mode, int64_t tiles, int mt, hipStream_t s, c
 // Wider column blocks once there are enough tiles to fill the machine.
 bool wide_cols_for(int64_t tiles, int64_t n) { return tiles * ((n + 63) / 64) >= 2048; }
 
+// Dense products (dense GEMM, fused QKV, MXFP4 GEMM) from 16 rows: the
+// streaming kernel with 64-row tiles (weights in a register ring, activations
+// in LDS passes) where it covers the format, else the LDS-staged GEMM. On the
+// fused QKV projection of 2048 tokens ([2048, 2304] x [2304, 3 x 4096]) the
+// streaming kernel takes 226 us, the LDS-staged GEMM 421 us. LK_DENSE_GEMM=lds
+// forces the LDS-staged GEMM (read per call).
+template <int FMT>
+int dense_launch(const GemmArgs& g, int64_t tiles, hipStream_t s, const char* what) {
+  const char* env = getenv("LK_DENSE_GEMM");
+  const bool lds = env && strcmp(env, "lds") == 0;
+  if (!lds && stream_fits(g.k, 4, g.group, FMT != kFmtW4A16))
+    return stream_launch<FMT, 1>(g, Mode::Dense, tiles, 4, s, what);
+  return gemm_launch<FMT, 1>(g, Mode::Dense, tiles, wide_cols_for(tiles * g.outputs, g.n), s, what);
+}
+
 int check_schedule_dims(int64_t tokens, int64_t routes, int64_t experts) {
   LK_REQUIRE(experts > 0 && experts + 1 <= kMaxBuckets, "expert-major schedule supports 1..%d experts",
              kMaxBuckets - 1);
@@ -2242,8 +2255,7 @@ int lk_w4a16_dense_gemm(const uint16_t* x, const uint8_t* packed, const uint16_t
   g.ws[0] = g.ws[1] = g.ws[2] = scales;
   g.out[0] = g.out[1] = g.out[2] = y;
   const int64_t tiles = (m + kTileRows - 1) / kTileRows;
-  return gemm_launch<kFmtW4A16, 1>(g, Mode::Dense, tiles, wide_cols_for(tiles, n),
-                                   as_stream(stream), "lk_w4a16_dense_gemm");
+  return dense_launch<kFmtW4A16>(g, tiles, as_stream(stream), "lk_w4a16_dense_gemm");
 }
 
 int lk_mxfp4_gemm(const uint16_t* x, const uint8_t* packed, const uint8_t* scale, uint16_t* y,
@@ -2261,10 +2273,8 @@ int lk_mxfp4_gemm(const uint16_t* x, const uint8_t* packed, const uint8_t* scale
   g.out[0] = g.out[1] = g.out[2] = y;
   const int64_t tiles = (m + kTileRows - 1) / kTileRows;
   if (act_f16)
-    return gemm_launch<kFmtMxF16, 1>(g, Mode::Dense, tiles, wide_cols_for(tiles, n),
-                                     as_stream(stream), "lk_mxfp4_gemm");
-  return gemm_launch<kFmtMxBf16, 1>(g, Mode::Dense, tiles, wide_cols_for(tiles, n),
-                                    as_stream(stream), "lk_mxfp4_gemm");
+    return dense_launch<kFmtMxF16>(g, tiles, as_stream(stream), "lk_mxfp4_gemm");
+  return dense_launch<kFmtMxBf16>(g, tiles, as_stream(stream), "lk_mxfp4_gemm");
 }
 
 int lk_mxfp4_expert_mlp(const uint16_t* x, const uint8_t* w1_packed, const uint8_t* w1_scale,
@@ -2340,8 +2350,7 @@ int lk_w4a16_fused_qkv(const uint16_t* x, const uint8_t* q_packed, const uint16_
   g.out[2] = v;
   g.outputs = 3;
   const int64_t tiles = (m + kTileRows - 1) / kTileRows;
-  return gemm_launch<kFmtW4A16, 1>(g, Mode::Dense, tiles, wide_cols_for(3 * tiles, n),
-                                   as_stream(stream), "lk_w4a16_fused_qkv");
+  return dense_launch<kFmtW4A16>(g, tiles, as_stream(stream), "lk_w4a16_fused_qkv");
 }
 
 int64_t lk_w4a16_moe_forward_workspace(int64_t tokens, int64_t experts, int64_t h, int64_t i,

@@ -106,12 +106,16 @@ def test_schedule_matches_oracle(rng, tokens, routes, experts, shared, invalid, 
 # dense GEMM and fused QKV
 
 
+@pytest.mark.parametrize("form", ["default", "lds"])  # streaming 64-row kernel / LDS-staged GEMM
 @pytest.mark.parametrize("m,n,k,g", [
     (16, 96, 256, 32), (64, 128, 512, 64), (100, 2304, 2304, 128), (130, 200, 384, 128),
     (17, 48, 96, 32), (64, 64, 512, 256), (70, 80, 320, 64),
 ])
-def test_dense_gemm_matches_oracle(rng, m, n, k, g):
+def test_dense_gemm_matches_oracle(rng, monkeypatch, m, n, k, g, form):
     from local_kimi_amd.kernels import w4a16_dense_gemm
+
+    if form == "lds":
+        monkeypatch.setenv("LK_DENSE_GEMM", "lds")
 
     p, s = OW.quantise(random_bf16_bits(rng, (n, k), 0.02), g)
     x = random_bf16_bits(rng, (m, k))
@@ -120,10 +124,13 @@ def test_dense_gemm_matches_oracle(rng, m, n, k, g):
     assert torch.equal(y, w4a16_dense_gemm(_dev(x), _dev(p), _dev(s)))
 
 
+@pytest.mark.parametrize("form", ["default", "lds"])  # streaming 64-row kernel / LDS-staged GEMM
 @pytest.mark.parametrize("m", [4, 64, 100])
-def test_fused_qkv_matches_oracle(rng, m):
+def test_fused_qkv_matches_oracle(rng, monkeypatch, m, form):
     from local_kimi_amd.kernels import fused_qkv_w4a16
 
+    if form == "lds":
+        monkeypatch.setenv("LK_DENSE_GEMM", "lds")
     n, k, g = 256, 512, 128
     mats = [OW.quantise(random_bf16_bits(rng, (n, k), 0.02), g) for _ in range(3)]
     x = random_bf16_bits(rng, (m, k))

@@ -90,11 +90,14 @@ def test_dequantise_is_bit_exact_for_every_code_and_exponent():
 # GEMM
 
 
+@pytest.mark.parametrize("form", ["default", "lds"])  # streaming 64-row kernel / LDS-staged GEMM
 @pytest.mark.parametrize("m,n,k", [(1, 96, 256), (16, 64, 512), (64, 2048, 2304), (100, 200, 1024),
                                    (37, 48, 96)])
-def test_gemm_matches_oracle(rng, m, n, k):
+def test_gemm_matches_oracle(rng, monkeypatch, m, n, k, form):
     from local_kimi_amd.kernels import mxfp4_gemm, mxfp4_gemm_reference
 
+    if form == "lds":
+        monkeypatch.setenv("LK_DENSE_GEMM", "lds")
     p, s = _encode(rng, n, k)
     x = random_bf16_bits(rng, (m, k))
     want = X.linear(x, p, s)
@@ -123,10 +126,13 @@ def test_gemm_across_scale_exponents(rng):
     assert np.all(np.abs(a - e) <= 2e-2 * mag + 1e-2 * np.abs(e))
 
 
+@pytest.mark.parametrize("form", ["default", "lds"])
 @pytest.mark.parametrize("m", [1, 64])
-def test_gemm_fp16_activations(rng, m):
+def test_gemm_fp16_activations(rng, monkeypatch, m, form):
     from local_kimi_amd.kernels import mxfp4_gemm
 
+    if form == "lds":
+        monkeypatch.setenv("LK_DENSE_GEMM", "lds")
     n, k = 128, 1024
     p, s = _encode(rng, n, k)
     xf = rng.normal(0, 1, (m, k)).astype(np.float16)
