@@ -1325,17 +1325,21 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
       rp[sb] = g.a + row * K + sl * 128 + sc * 8;
     }
   };
-  auto stage_loads = [&](uint4 (&v)[2][kPsHalfMax]) {
+  // buffers holding a tile of the block in phase p (block-uniform; the same
+  // predicate guards a buffer's loads and its stores)
+  auto stage_live = [&](int p, int sb) { return sb < nbuf && p * nbuf + sb < nseg; };
+  auto stage_loads = [&](int p, uint4 (&v)[2][kPsHalfMax]) {
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
       for (int ii = 0; ii < kPsHalfMax; ++ii)
-        if (sb < nbuf && ii < half) v[sb][ii] = *reinterpret_cast<const uint4*>(rp[sb] + ii * 256);
+        if (stage_live(p, sb) && ii < half)
+          v[sb][ii] = *reinterpret_cast<const uint4*>(rp[sb] + ii * 256);
   };
-  auto stage_stores = [&](const uint4 (&v)[2][kPsHalfMax]) {
+  auto stage_stores = [&](int p, const uint4 (&v)[2][kPsHalfMax]) {
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
-      if (sb >= nbuf) continue;
+      if (!stage_live(p, sb)) continue;
       const int fb = sb * ksteps + sl;
 #pragma unroll
       for (int ii = 0; ii < kPsHalfMax; ++ii)
@@ -1384,7 +1388,7 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   // behind every CU's whole first round
   stage_rows(0);
   uint4 sv[2][kPsHalfMax];
-  stage_loads(sv);
+  stage_loads(0, sv);
   PsPair<FMT, MATS, NT> w[kPairs];
   int lu = claim(), lr = 0;  // load cursor: unit, round
   if (lu < ue) set_ptrs(lu);
@@ -1393,7 +1397,7 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
 #pragma unroll
   for (int j = 0; j < kPairs; ++j) {
     if (j == kPsEarlyPairs) {
-      stage_stores(sv);
+      stage_stores(0, sv);
       __syncthreads();
     }
     w[j].load(lw, lsr, lu < ue ? 2 * j : ksteps, jq, ksteps, dummy);
@@ -1482,6 +1486,7 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
       // kPsBatch units, in a rolled loop to keep registers for the ring
       stage_rows(p);
       for (int sb = 0; sb < nbuf; ++sb) {
+        if (!stage_live(p, sb)) continue;
         for (int i0 = 0; i0 < half; i0 += kPsBatch) {
           uint4 pv[kPsBatch];
 #pragma unroll
