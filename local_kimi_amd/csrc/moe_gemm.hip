@@ -806,8 +806,12 @@ w4a16_stream_kernel(const GemmArgs g) {
   // zero line): the loads in flight are then the same on every path and the
   // compiler waits only for the slot it needs, not for the whole ring
   const uint8_t* const dummy = g_tail_pad;
+  // 16-row tiles issue the ring now; 64-row tiles issue it after the first
+  // pass's activation loads (below), which then do not wait behind it
+  if constexpr (MT == 1) {
 #pragma unroll
-  for (int j = 0; j < kRing; ++j) w[j].load(wrow, srow, j, jq, K, gshift, ksteps, dummy);
+    for (int j = 0; j < kRing; ++j) w[j].load(wrow, srow, j, jq, K, gshift, ksteps, dummy);
+  }
 
   // 2. the tile's activation rows (one lookup per row, shared through LDS)
   if (tid < rows) {
@@ -884,8 +888,29 @@ w4a16_stream_kernel(const GemmArgs g) {
   };
   auto pass_steps = [&](int p) { return min(ps, ksteps - p * ps); };
 
-  // 3. stage the first pass
-  {
+  // 3. stage the first pass. 64-row tiles: all of its units in one batch of
+  // loads, then the weight ring, then the stores (the stores wait for the
+  // activation loads alone)
+  if constexpr (MT > 1) {
+    uint4 v0[kPassUnits];
+    uint32_t s0[kPassUnits];
+    const int units0 = pass_steps(0) * kRows * 16;
+#pragma unroll
+    for (int q = 0; q < kPassUnits; ++q) {
+      const int u = q * kThreads + tid;
+      if (u < units0 && unit_live(u)) {
+        v0[q] = unit_load(0, u);
+        s0[q] = unit_scale(0, u);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kRing; ++j) w[j].load(wrow, srow, j, jq, K, gshift, ksteps, dummy);
+#pragma unroll
+    for (int q = 0; q < kPassUnits; ++q) {
+      const int u = q * kThreads + tid;
+      if (u < units0 && unit_live(u)) unit_store(0, u, v0[q], s0[q]);
+    }
+  } else {
     constexpr int kBatch = 6;
     const int units = pass_steps(0) * kRows * 16;
     for (int u0 = 0; u0 < units; u0 += kBatch * kThreads) {
