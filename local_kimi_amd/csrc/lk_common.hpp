@@ -51,11 +51,21 @@ __device__ inline float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f))
 // torch's F.silu on a bf16 tensor: fp32 x / (1 + exp(-x)), rounded to bf16.
 __device__ inline float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
+// silu for the fast kernels: x * 1 / (1 + 2^(-x log2 e)) on the hardware
+// exp2 and reciprocal (about 1 ulp each, against the ~25 instructions of
+// expf and an IEEE divide); the result is rounded to bf16 next, so it differs
+// from silu_f32 by at most one bf16 ulp, in rare near-tie cases. Limits
+// match: x -> +inf gives x, x -> -inf gives -0 (NaN at -inf, as x / inf).
+__device__ inline float silu_fast_f32(float x) {
+  const float e = __builtin_amdgcn_exp2f(x * -1.4426950408889634f);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 // SwiGLU contract of the reference: bf16(bf16(silu(bf16(gate))) * bf16(up)).
 __device__ inline uint16_t swiglu_bf16(float gate_acc, float up_acc) {
   const float g = round_bf16(gate_acc);
   const float u = round_bf16(up_acc);
-  const float s = round_bf16(silu_f32(g));
+  const float s = round_bf16(silu_fast_f32(g));
   return f32_to_bf16(s * u);
 }
 

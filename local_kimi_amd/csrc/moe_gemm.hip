@@ -728,7 +728,8 @@ w4a16_stream_kernel(const GemmArgs g) {
   constexpr int kNBuf = MT == 1 ? 1 : 2;
   constexpr int kPassUnits = MT == 1 ? 1 : (kRows * kStPassSteps * 16 + kThreads - 1) / kThreads;
   extern __shared__ uint4 smem[];
-  __shared__ int64_t row_index[kRows];
+  __shared__ int64_t row_index[kRows];  // activation row of each tile row
+  __shared__ int64_t out_row[kRows];    // output row of each tile row
 
   const int per_tile = g.col_blocks * g.outputs;
   const int id = blockIdx.x;
@@ -767,6 +768,10 @@ w4a16_stream_kernel(const GemmArgs g) {
     return;
   }
 
+  // the tile's sorted-position lookups, issued ahead of the weight loads so
+  // that waiting for them never waits for weights
+  int32_t pos = 0;
+  if ((GATHER || SCATTER) && tid < rows) pos = g.perm[row0 + tid];
   const int lane = tid & (kWave - 1);
   const int wv = tid / kWave;
   const int jq = lane >> 4;
@@ -813,10 +818,11 @@ w4a16_stream_kernel(const GemmArgs g) {
     for (int j = 0; j < kRing; ++j) w[j].load(wrow, srow, j, jq, K, gshift, ksteps, dummy);
   }
 
-  // 2. the tile's activation rows (one lookup per row, shared through LDS)
+  // 2. the tile's activation and output rows (one lookup per row, shared
+  // through LDS; the epilogue then reads no global memory)
   if (tid < rows) {
-    if constexpr (GATHER) row_index[tid] = g.perm[row0 + tid] / g.routes;
-    else row_index[tid] = row0 + tid;
+    row_index[tid] = GATHER ? static_cast<int64_t>(pos / g.routes) : row0 + tid;
+    out_row[tid] = SCATTER ? static_cast<int64_t>(pos) : row0 + tid;
   }
   __syncthreads();
 
@@ -1166,7 +1172,7 @@ w4a16_stream_kernel(const GemmArgs g) {
     for (int i = 0; i < 4; ++i) {
       const int m = ms * 16 + jq * 4 + i;
       if (m >= rows) continue;
-      const int64_t orow = SCATTER ? static_cast<int64_t>(g.perm[row0 + m]) : row0 + m;
+      const int64_t orow = out_row[m];
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         if (col[nt] >= N) continue;
