@@ -12,6 +12,8 @@
 
 namespace lk {
 
+constexpr int kWave = 64;  // lanes per wavefront on CDNA
+
 // ---------------------------------------------------------------------------
 // error state (per host thread)
 

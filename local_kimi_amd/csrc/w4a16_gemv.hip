@@ -18,11 +18,11 @@
 #include <stdlib.h>
 
 #include "lk_common.hpp"
+#include "lk_route.hpp"
 
 namespace lk {
 namespace {
 
-constexpr int kWave = 64;
 
 struct XStage {
   uint4* pair;  // [(tok * 4 + j) * cpr + c]
@@ -529,97 +529,7 @@ grouped_gemv_kernel(const uint16_t* __restrict__ x, const int64_t* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// sigmoid top-k router for one token, computed by one wave (all lanes).
-// EPL experts per lane (lane l holds ids l*EPL .. l*EPL+EPL-1).
-// Returns the expert id of selection `want` (-1 if want >= top_k). When
-// idx_out is non-null, lanes < top_k write the selection and its weight.
-//
-// Each lane first sorts its EPL candidates by key (descending; equal keys keep
-// the lower id first), so a selection round only compares the lanes' head
-// entries: one wave max, one ballot (the lowest lane holding the max holds the
-// lowest id, since ids grow with the lane) and the owner lane advancing its
-// head. The rounds are a short dependent chain, which is what bounds a router
-// that runs on one wave.
-
-template <int EPL>
-__device__ int64_t route_token(const float* __restrict__ logits, const float* __restrict__ bias,
-                               int ne, int top_k, int want, float scaling, int renorm,
-                               int64_t* __restrict__ idx_out, float* __restrict__ w_out) {
-  const int lane = threadIdx.x & (kWave - 1);
-  float lg[EPL], bs[EPL];
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {  // all loads first, addresses clamped in bounds
-    const int id = min(lane * EPL + j, ne - 1);
-    lg[j] = logits[id];
-    bs[j] = bias ? bias[id] : 0.0f;
-  }
-  uint32_t key[EPL];
-  float sc[EPL];
-  int slot[EPL];
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    sc[j] = 1.0f / (1.0f + expf(-lg[j]));
-    // ids past the bank sit behind every real expert: key 0 and the highest slots
-    key[j] = lane * EPL + j < ne ? orderable(sc[j] + bs[j]) : 0u;
-    slot[j] = j;
-  }
-#pragma unroll
-  for (int a = 0; a < EPL; ++a)
-#pragma unroll
-    for (int b = EPL - 1; b > a; --b) {
-      const bool sw = key[b] > key[b - 1];  // strict, so equal keys stay in id order
-      const uint32_t k0 = key[b - 1], k1 = key[b];
-      const float s0 = sc[b - 1], s1 = sc[b];
-      const int q0 = slot[b - 1], q1 = slot[b];
-      key[b - 1] = sw ? k1 : k0;
-      key[b] = sw ? k0 : k1;
-      sc[b - 1] = sw ? s1 : s0;
-      sc[b] = sw ? s0 : s1;
-      slot[b - 1] = sw ? q1 : q0;
-      slot[b] = sw ? q0 : q1;
-    }
-  const int n_live = max(0, min(EPL, ne - lane * EPL));  // real experts in this lane
-  int taken = 0;
-  uint32_t hk = key[0];
-  float hs = sc[0];
-  int hq = slot[0];
-  float ssum = 0.f;
-  int64_t mine = -1;
-  float my_score = 0.f;
-  int64_t wanted = -1;
-  for (int rr = 0; rr < top_k; ++rr) {
-    const bool has = taken < n_live;
-    const uint32_t kb = has ? hk : 0u;
-    const uint32_t kmax = wave_max_u32(kb);
-    const uint64_t holders = __builtin_amdgcn_ballot_w64(has && kb == kmax);
-    const int owner = holders ? static_cast<int>(__builtin_ctzll(holders)) : 0;
-    const int q = __builtin_amdgcn_readlane(hq, owner);
-    const float score = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hs), owner));
-    const uint32_t sel = static_cast<uint32_t>(owner * EPL + q);
-    // top_k <= ne guarantees a live candidate; stay in range regardless
-    const uint32_t safe = sel < static_cast<uint32_t>(ne) ? sel : 0u;
-    if (lane == owner) {
-      ++taken;
-#pragma unroll
-      for (int j = 1; j < EPL; ++j)
-        if (taken == j) {
-          hk = key[j];
-          hs = sc[j];
-          hq = slot[j];
-        }
-    }
-    ssum += score;
-    mine = lane == rr ? static_cast<int64_t>(safe) : mine;
-    my_score = lane == rr ? score : my_score;
-    wanted = rr == want ? static_cast<int64_t>(safe) : wanted;
-  }
-  if (idx_out != nullptr && lane < top_k) {
-    const float denom = ssum + 1e-20f;
-    idx_out[lane] = mine;
-    w_out[lane] = (renorm && top_k > 1) ? (my_score / denom) * scaling : my_score * scaling;
-  }
-  return wanted;
-}
+// sigmoid top-k router (route_token in lk_route.hpp), one wave per token
 
 template <int EPL>
 __global__ void __launch_bounds__(64)

@@ -1,0 +1,119 @@
+"""GPU parity of the one-block schedule forms of the expert-major block.
+
+With at most 256 routed experts, batches of at most 8 tokens route and
+schedule in one launch (schedule_one_kernel with routing); batches of at most
+1024 token-routes route on a grid and schedule in one launch; larger batches,
+or LK_MOE_FUSED_SCHEDULE=0 for any batch, take the router launch and the
+chunked schedule launches. All run the same selection code and the same stable
+ranking, so the selections, combine weights and block outputs must be
+bit-identical; the results are also checked against the oracle within the
+quantized-matmul tolerance (1e-2 relative / 2e-2 absolute in bf16), with the
+expert indices bit-exact. Cases: with and without a router bias, tied logits
+(equal keys keep the lower expert id first), both sides of the 8-token
+routing limit, the largest one-launch schedule (113 tokens x 9 routes = 1017
+token-routes) and one token past it, and both weight formats.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as OM
+from oracle import mxfp4 as X
+from oracle import w4a16 as OW
+from oracle.bf16 import bf16_bits_to_f32
+
+from ._helpers import assert_close_bf16, from_bits, random_bf16_bits, to_bits
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _require_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    from local_kimi_amd import _lib
+
+    _lib.load()
+
+
+def _dev(a):
+    if a.dtype == np.uint16:
+        return from_bits(a, DEV)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _w4_bank(rng, e, n, k, g=128):
+    ps, ss = [], []
+    for _ in range(e):
+        p, s = OW.quantise(random_bf16_bits(rng, (n, k), 0.02), g)
+        ps.append(p)
+        ss.append(s)
+    return np.stack(ps), np.stack(ss)
+
+
+def _mx_bank(rng, e, n, k):
+    enc = [X.quantize(bf16_bits_to_f32(random_bf16_bits(rng, (n, k), 0.02))) for _ in range(e)]
+    return np.stack([p for p, _ in enc]), np.stack([s for _, s in enc])
+
+
+def _fused_and_split(monkeypatch, fn, *args):
+    """fn(*args) on the one-launch forms, then on the router and chunked schedule."""
+    monkeypatch.delenv("LK_MOE_FUSED_SCHEDULE", raising=False)
+    a = fn(*args)
+    torch.cuda.synchronize()
+    monkeypatch.setenv("LK_MOE_FUSED_SCHEDULE", "0")
+    b = fn(*args)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("LK_MOE_FUSED_SCHEDULE")
+    return a, b
+
+
+@pytest.mark.parametrize("weights", ["w4a16", "mxfp4"])
+@pytest.mark.parametrize("tokens,top_k,bias,ties", [
+    (4, 8, False, False),
+    (8, 8, True, True),      # the largest batch routed in the schedule's block
+    (9, 8, False, False),    # routed on a grid, scheduled in one launch
+    (23, 8, True, False),
+    (64, 8, False, True),
+    (113, 8, True, False),   # 1017 token-routes: the largest one-launch schedule
+    (114, 8, False, False),  # 1026 token-routes: separate launches on both sides
+    (200, 4, True, True),    # 1000 token-routes at top-4
+])
+def test_fused_router_schedule_matches_separate_launches(rng, monkeypatch, weights, tokens, top_k,
+                                                         bias, ties):
+    from local_kimi_amd.kernels import mxfp4_moe_block, w4a16_moe_forward
+
+    e_routed, h, inter = 256, 256, 128
+    bank = _mx_bank if weights == "mxfp4" else _w4_bank
+    banks = (*bank(rng, e_routed + 1, inter, h), *bank(rng, e_routed + 1, inter, h),
+             *bank(rng, e_routed + 1, h, inter))
+    x = random_bf16_bits(rng, (tokens, h))
+    logits = rng.normal(0, 1, (tokens, e_routed)).astype(np.float32)
+    if ties:  # blocks of equal logits across the selection boundary
+        logits[:, 40:72] = logits[:, 40:41]
+        logits[::3, 200:230] = 3.0
+    b = rng.normal(0, 0.05, e_routed).astype(np.float32) if bias else None
+    args = (_dev(x), _dev(logits), None if b is None else _dev(b), *(_dev(v) for v in banks),
+            top_k, 2.446)
+    block = mxfp4_moe_block if weights == "mxfp4" else w4a16_moe_forward
+    (y, idx, w), (y0, idx0, w0) = _fused_and_split(monkeypatch, block, *args)
+    assert torch.equal(idx, idx0)
+    assert torch.equal(w, w0)
+    assert torch.equal(y, y0), "one-launch and chunked router + schedule differ"
+    # oracle on a few tokens (the selections of all of them)
+    eidx, ew = OM.route(logits, b, top_k, routed_scaling_factor=2.446)
+    assert np.array_equal(idx.cpu().numpy(), eidx)
+    np.testing.assert_allclose(w.cpu().numpy(), ew, rtol=2e-6)
+    sel = np.unique(np.array([0, tokens // 2, tokens - 1]))
+    if weights == "mxfp4":
+        ey, _, _ = X.moe_block(x[sel], logits[sel], b, *banks, top_k=top_k,
+                               routed_scaling_factor=2.446)
+    else:
+        ey, _, _ = OM.moe_block(x[sel], logits[sel], b, *banks, top_k=top_k,
+                                routed_scaling_factor=2.446, group_size=128)
+    assert_close_bf16(to_bits(y)[sel], ey, what=f"{weights} block T={tokens} k={top_k}")
