@@ -299,6 +299,7 @@ struct GemmArgs {
   int col_blocks;            // column blocks per output matrix
   int outputs;               // output matrices (3 for fused QKV, else 1)
   int act;                   // two-matrix epilogue (kActSwiglu / kActSitu)
+  int tail16;                // 64-row launches: tiles of <= 16 rows take the 16-row path
   float situ_beta, situ_linear_beta;  // SiTU parameters; linear_beta <= 0: none
 };
 
@@ -783,15 +784,10 @@ inline size_t stream_lds_bytes(int64_t k, int mt) {
   return static_cast<size_t>(nbuf * ps * mt) * (4 * kWave * sizeof(uint4) + 4 * 16 * sizeof(float));
 }
 
-// Block = 8 waves over one tile of <= 16 * MT rows x (8 * 16 * NT) columns.
-// The block stages the tile's activation rows in LDS (MT == 1: the whole
-// reduction once, one barrier; MT > 1: passes of kStPassSteps k-steps,
-// double buffered, the next pass loaded while the current one computes, one
-// barrier per pass); every wave streams its own columns over all of k with
-// kStDepth k-steps of weights in flight and stores its outputs itself.
+// One tile of <= 16 * MT rows x kBN columns of a streaming block (below).
 template <int FMT, int MATS, int NT, int MT, bool WIDE, bool GATHER, bool SCATTER, bool DENSE>
-__global__ void __launch_bounds__(kStWaves * kWave, 2)
-w4a16_stream_kernel(const GemmArgs g) {
+__device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert, const int row0,
+                                            const int rows, const int cb, const int osel) {
   constexpr bool kMx = FMT != kFmtW4A16;
   constexpr bool kF8 = FMT == kFmtMxF8;
   static_assert(!(FMT == kFmtMxF16 && WIDE), "fp16 activations use the narrow layout");
@@ -804,43 +800,9 @@ w4a16_stream_kernel(const GemmArgs g) {
   extern __shared__ uint4 smem[];
   __shared__ int64_t row_index[kRows];  // activation row of each tile row
   __shared__ int64_t out_row[kRows];    // output row of each tile row
-
-  const int per_tile = g.col_blocks * g.outputs;
-  const int id = blockIdx.x;
-  const int grp = id / (8 * per_tile);
-  const int rem = id - grp * 8 * per_tile;
-  const int tile = grp * 8 + (rem & 7);
-  const int cb_all = rem >> 3;
-  const int osel = cb_all / g.col_blocks;
-  const int cb = cb_all - osel * g.col_blocks;
-  int expert, row0, rows;
-  if constexpr (DENSE) {
-    row0 = tile * kRows;
-    if (row0 >= g.dense_rows) return;
-    rows = min(kRows, g.dense_rows - row0);
-    expert = 0;
-  } else {
-    // the descriptor load does not wait for the count (the list holds max_tiles entries)
-    const int4 d = reinterpret_cast<const int4*>(g.tiles)[tile];
-    if (tile >= *g.tile_count) return;
-    expert = d.x;
-    row0 = d.y;
-    rows = d.z;
-  }
   const int64_t N = g.n, K = g.k;
   uint16_t* const out = pick3(g.out, osel);
   const int tid = threadIdx.x;
-  if (expert < 0) {  // routes outside the bank produce zero rows
-    for (int i = tid; i < rows * kBN; i += kThreads) {
-      const int m = i / kBN;
-      const int64_t col = static_cast<int64_t>(cb) * kBN + (i - m * kBN);
-      if (col < N) {
-        const int64_t orow = SCATTER ? g.perm[row0 + m] : row0 + m;
-        out[orow * N + col] = 0;
-      }
-    }
-    return;
-  }
 
   // the tile's sorted-position lookups, issued ahead of the weight loads so
   // that waiting for them never waits for weights
@@ -1261,6 +1223,67 @@ w4a16_stream_kernel(const GemmArgs g) {
       }
     }
   }
+}
+
+// Block = 8 waves over one tile of <= 16 * MT rows x (8 * 16 * NT) columns.
+// The block stages the tile's activation rows in LDS (MT == 1: the whole
+// reduction once, one barrier; MT > 1: passes of kStPassSteps k-steps,
+// double buffered, the next pass loaded while the current one computes, one
+// barrier per pass); every wave streams its own columns over all of k with
+// kStDepth k-steps of weights in flight and stores its outputs itself.
+template <int FMT, int MATS, int NT, int MT, bool WIDE, bool GATHER, bool SCATTER, bool DENSE>
+__global__ void __launch_bounds__(kStWaves * kWave, 2)
+w4a16_stream_kernel(const GemmArgs g) {
+  constexpr int kThreads = kStWaves * kWave;
+  constexpr int kBN = kStWaves * NT * 16;
+  constexpr int kRows = 16 * MT;
+
+  const int per_tile = g.col_blocks * g.outputs;
+  const int id = blockIdx.x;
+  const int grp = id / (8 * per_tile);
+  const int rem = id - grp * 8 * per_tile;
+  const int tile = grp * 8 + (rem & 7);
+  const int cb_all = rem >> 3;
+  const int osel = cb_all / g.col_blocks;
+  const int cb = cb_all - osel * g.col_blocks;
+  int expert, row0, rows;
+  if constexpr (DENSE) {
+    row0 = tile * kRows;
+    if (row0 >= g.dense_rows) return;
+    rows = min(kRows, g.dense_rows - row0);
+    expert = 0;
+  } else {
+    // the descriptor load does not wait for the count (the list holds max_tiles entries)
+    const int4 d = reinterpret_cast<const int4*>(g.tiles)[tile];
+    if (tile >= *g.tile_count) return;
+    expert = d.x;
+    row0 = d.y;
+    rows = d.z;
+  }
+  const int64_t N = g.n;
+  uint16_t* const out = pick3(g.out, osel);
+  const int tid = threadIdx.x;
+  if (expert < 0) {  // routes outside the bank produce zero rows
+    for (int i = tid; i < rows * kBN; i += kThreads) {
+      const int m = i / kBN;
+      const int64_t col = static_cast<int64_t>(cb) * kBN + (i - m * kBN);
+      if (col < N) {
+        const int64_t orow = SCATTER ? g.perm[row0 + m] : row0 + m;
+        out[orow * N + col] = 0;
+      }
+    }
+    return;
+  }
+  // a tile of at most 16 rows (an expert's last rows) takes the 16-row path:
+  // a quarter of the MFMAs and all of its activations resident (the host
+  // sets tail16 when they fit the launch's LDS)
+  if constexpr (MT > 1) {
+    if (rows <= 16 && g.tail16) {
+      stream_tile<FMT, MATS, NT, 1, WIDE, GATHER, SCATTER, DENSE>(g, expert, row0, rows, cb, osel);
+      return;
+    }
+  }
+  stream_tile<FMT, MATS, NT, MT, WIDE, GATHER, SCATTER, DENSE>(g, expert, row0, rows, cb, osel);
 }
 
 // ---------------------------------------------------------------------------
@@ -2121,6 +2144,9 @@ int stream_launch(GemmArgs g, Mode mode, int64_t tiles, int mt, hipStream_t s, c
   constexpr bool kWideOk = FMT != kFmtMxF16;
   const size_t lds = stream_lds_bytes(g.k, mt);
   LK_REQUIRE(lds <= static_cast<size_t>(kStMaxLds), "%s: reduction width too large", what);
+  // 64-row launches: tiles of <= 16 rows run the 16-row path when all of
+  // their activations fit the LDS the launch takes anyway
+  g.tail16 = mt > 1 && stream_lds_bytes(g.k, 1) <= lds ? 1 : 0;
   g.col_blocks = static_cast<int>((g.n + kStWaves * NT * 16 - 1) / (kStWaves * NT * 16));
   const int64_t blocks = (tiles + 7) / 8 * 8 * g.col_blocks * g.outputs;
   LK_REQUIRE(blocks > 0 && blocks < (1LL << 31), "%s: too many blocks", what);

@@ -125,7 +125,7 @@ def test_dense_gemm_matches_oracle(rng, monkeypatch, m, n, k, g, form):
 
 
 @pytest.mark.parametrize("form", ["default", "lds"])  # streaming 64-row kernel / LDS-staged GEMM
-@pytest.mark.parametrize("m", [4, 64, 100])
+@pytest.mark.parametrize("m", [4, 64, 70, 100])  # 70: a last tile of 6 rows
 def test_fused_qkv_matches_oracle(rng, monkeypatch, m, form):
     from local_kimi_amd.kernels import fused_qkv_w4a16
 
