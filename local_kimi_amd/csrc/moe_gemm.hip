@@ -1934,8 +1934,11 @@ int schedule_launch(const RouteTable& rt, int64_t entries, char* ws, const Sched
   sc.tiles = tiles;
   sc.tile_count = tile_count;
   sc.tile_rows = tile_rows;
+  // one block of 16 waves where one chunk of kSchedThreads would not cover
+  // the table (otherwise the chunk kernel, at 8 waves, is the faster one launch)
   const char* one = getenv("LK_MOE_FUSED_SCHEDULE");
-  if (entries <= kFuseThreads && rt.experts + 1 <= kFuseBuckets && !(one && strcmp(one, "0") == 0)) {
+  if (entries > kSchedThreads && entries <= kFuseThreads && rt.experts + 1 <= kFuseBuckets &&
+      !(one && strcmp(one, "0") == 0)) {
     schedule_one_kernel<false><<<1, kFuseThreads, 0, s>>>(rt, entries, sc, nullptr, nullptr, nullptr,
                                                           nullptr, 0, 0.f, 0);
     return check_launch("moe schedule");
