@@ -1,0 +1,127 @@
+"""GPU parity of the model-slice callers (engine/klinear/quantized.py:160-180,
+engine/klinear/moe.py:278-334, engine/generate.py:226-306).
+
+``W4A16Linear`` and ``KLinearMoE`` are loaded from a W4A16 checkpoint written
+in the reference's layout (G = 128), run through the registry's default
+(HIP) ops, and are checked against the oracle within the quantized-matmul
+tolerance (1e-2 relative / 2e-2 absolute in bf16). The router logits are a
+torch fp32 GEMM on the GPU, whose bits are not the oracle's; the oracle block
+is therefore fed the logits the GPU computed (the selection from given
+logits is what the kernels own, and is compared bit-exactly elsewhere).
+``MoEDecodeGraph`` replays are compared with eager forwards bit for bit,
+with eager work between replays.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as OM
+from oracle import w4a16 as OW
+
+from ._helpers import assert_close_bf16, from_bits, random_bf16_bits, to_bits
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+LAYER, EXPERTS, HIDDEN, INTER, G, TOP_K = 2, 16, 256, 128, 128, 4
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _require_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    from local_kimi_amd import _lib
+
+    _lib.load()
+
+
+@pytest.fixture(scope="module")
+def ckpt(tmp_path_factory):
+    """A small W4A16 checkpoint: one linear, one MoE layer, and the oracle's copies."""
+    from local_kimi_amd.checkpoint import expert_name, save_w4a16_checkpoint, shared_expert_name
+    from local_kimi_amd.quant.w4a16 import W4A16Tensor
+
+    rng = np.random.default_rng(20260801)
+    path = tmp_path_factory.mktemp("ckpt")
+
+    def enc(n, k):
+        p, s = OW.quantise(random_bf16_bits(rng, (n, k), 0.02), G)
+        return W4A16Tensor(packed=torch.from_numpy(p), scales=from_bits(s), original_shape=(n, k),
+                           group_size=G), (p, s)
+
+    tensors, banks = {}, {"w1": [], "w3": [], "w2": []}
+    shared = {"w1": "gate_proj", "w3": "up_proj", "w2": "down_proj"}
+    for e in range(EXPERTS + 1):
+        for bank, (n, k) in (("w1", (INTER, HIDDEN)), ("w3", (INTER, HIDDEN)), ("w2", (HIDDEN, INTER))):
+            t, ps = enc(n, k)
+            name = expert_name(LAYER, e, bank) if e < EXPERTS else shared_expert_name(LAYER, shared[bank])
+            tensors[name] = t
+            banks[bank].append(ps)
+    lin, lin_ps = enc(384, HIDDEN)
+    tensors["model.layers.0.mlp.up_proj.weight"] = lin
+    prefix = f"model.layers.{LAYER}.block_sparse_moe.gate."
+    tensors[prefix + "weight"] = torch.from_numpy(rng.normal(0, 0.05, (EXPERTS, HIDDEN)).astype(np.float32))
+    tensors[prefix + "e_score_correction_bias"] = torch.from_numpy(
+        rng.normal(0, 0.02, EXPERTS).astype(np.float32))
+    save_w4a16_checkpoint(path, tensors)
+    stacked = [np.stack([ps[j] for ps in banks[b]]) for b in ("w1", "w3", "w2") for j in (0, 1)]
+    bias = tensors[prefix + "e_score_correction_bias"].numpy()
+    return path, lin_ps, stacked, bias
+
+
+def test_w4a16_linear_matches_oracle(ckpt, rng):
+    from local_kimi_amd.checkpoint import W4A16Index
+    from local_kimi_amd.kernels import w4a16_dense
+    from local_kimi_amd.klinear import W4A16Linear
+
+    path, (p, s), _, _ = ckpt
+    enc = W4A16Index(path).load_w4a16("model.layers.0.mlp.up_proj.weight", (384, HIDDEN), device=DEV)
+    lin = W4A16Linear.from_encoded(enc)
+    x = random_bf16_bits(rng, (2, 3, HIDDEN))
+    y = lin(from_bits(x, DEV))
+    assert y.shape == (2, 3, 384) and y.dtype == torch.bfloat16
+    want = OW.dense(x.reshape(6, HIDDEN), p, s, G)
+    assert_close_bf16(to_bits(y).reshape(6, 384), want, what="W4A16Linear")
+    direct = w4a16_dense(from_bits(x, DEV).reshape(6, HIDDEN), enc.packed, enc.scales)
+    assert torch.equal(y.reshape(6, 384), direct)
+    with pytest.raises(ValueError, match="does not match"):
+        lin(torch.zeros(2, HIDDEN + 1, dtype=torch.bfloat16, device=DEV))
+
+
+@pytest.mark.parametrize("tokens", [1, 3, 8, 40])  # token-major below 4 tokens, expert-major from 4
+def test_klinear_moe_from_checkpoint_matches_oracle(ckpt, rng, tokens):
+    from local_kimi_amd.checkpoint import W4A16Index
+    from local_kimi_amd.klinear import KLinearMoE
+
+    path, _, banks, bias = ckpt
+    moe = KLinearMoE.from_checkpoint(W4A16Index(path), LAYER, device=DEV, num_experts=EXPERTS,
+                                     hidden=HIDDEN, intermediate=INTER, top_k=TOP_K,
+                                     routed_scaling_factor=2.446)
+    x = random_bf16_bits(rng, (tokens, HIDDEN))
+    xd = from_bits(x, DEV)
+    y = moe(xd.reshape(1, tokens, HIDDEN))
+    assert y.shape == (1, tokens, HIDDEN)
+    logits = moe.router_logits(xd).cpu().numpy()
+    want, _, _ = OM.moe_block(x, logits, bias, *banks, top_k=TOP_K, routed_scaling_factor=2.446,
+                              group_size=G)
+    assert_close_bf16(to_bits(y.reshape(tokens, HIDDEN)), want, what=f"KLinearMoE T={tokens}")
+
+
+def test_moe_decode_graph_replays_match_eager(ckpt, rng):
+    from local_kimi_amd.checkpoint import W4A16Index
+    from local_kimi_amd.klinear import KLinearMoE, MoEDecodeGraph
+
+    path, _, _, _ = ckpt
+    moe = KLinearMoE.from_checkpoint(W4A16Index(path), LAYER, device=DEV, num_experts=EXPERTS,
+                                     hidden=HIDDEN, intermediate=INTER, top_k=TOP_K)
+    runner = MoEDecodeGraph(moe, tokens=1)
+    for _ in range(4):
+        x = from_bits(random_bf16_bits(rng, (1, HIDDEN)), DEV)
+        eager = moe(x)
+        torch.cuda.synchronize()
+        got = runner(x)
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager)
