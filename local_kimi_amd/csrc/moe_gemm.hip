@@ -1794,17 +1794,31 @@ moe_combine_kernel(const uint16_t* __restrict__ eo, const float* __restrict__ w,
   const int64_t routes = top_k + 1;
   const uint16_t* base = eo + t * routes * h + c8;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int r = 0; r < top_k; ++r) {
-    const uint4 v = *reinterpret_cast<const uint4*>(base + r * h);
-    const float wr = w[t * top_k + r];
-    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+  // routes in batches of 8 independent loads (the shared route's with the
+  // first batch), summed in route order
+  const uint4 sv = *reinterpret_cast<const uint4*>(base + top_k * h);
+  for (int r0 = 0; r0 < top_k; r0 += 8) {
+    uint4 v[8];
+    float wr[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      acc[2 * j] += bf16_to_f32(q[j] & 0xFFFFu) * wr;
-      acc[2 * j + 1] += bf16_to_f32(q[j] >> 16) * wr;
+    for (int i = 0; i < 8; ++i) {
+      const int r = min(r0 + i, top_k - 1);
+      v[i] = *reinterpret_cast<const uint4*>(base + r * h);
+      wr[i] = w[t * top_k + r];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      // a route past top_k adds +0 (acc starts at +0 and never holds -0, so
+      // this leaves every bit as the loop over top_k routes would)
+      const bool ok = r0 + i < top_k;
+      const uint32_t q[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] += ok ? bf16_to_f32(q[j] & 0xFFFFu) * wr[i] : 0.f;
+        acc[2 * j + 1] += ok ? bf16_to_f32(q[j] >> 16) * wr[i] : 0.f;
+      }
     }
   }
-  const uint4 sv = *reinterpret_cast<const uint4*>(base + top_k * h);
   const uint32_t sq[4] = {sv.x, sv.y, sv.z, sv.w};
   uint32_t o[4];
 #pragma unroll
