@@ -41,10 +41,6 @@ SCALES_SUFFIX = ".w4a16_scales"
 INDEX_NAME = "model.safetensors.index.json"
 DEFAULT_GROUP_SIZE = 32  # the reference's GROUP_SIZE (engine/quant/w4a16.py)
 
-_ST_DTYPES = {"U8": torch.uint8, "BF16": torch.bfloat16, "F32": torch.float32,
-              "F16": torch.float16, "I64": torch.int64, "I32": torch.int32}
-
-
 def _valid_group(g: object) -> bool:
     return isinstance(g, int) and not isinstance(g, bool) and g > 0 and g % 32 == 0 and not (g & (g - 1))
 
@@ -108,19 +104,31 @@ class W4A16Index:
         payload = json.loads(index_path.read_text(encoding="utf-8"))
         self._weight_map, self.quantized, self.group_size = parse_index(payload)
         self._shapes: dict[str, tuple[tuple[int, ...], str]] = {}
-        for shard in sorted(set(self._weight_map.values())):
-            path = self.directory / shard
-            if not path.is_file():
-                raise FileNotFoundError(f"safetensors shard is missing: {path}")
-            with safe_open(str(path), framework="pt", device="cpu") as f:
-                present = set(f.keys())
-                for name, s in self._weight_map.items():
-                    if s != shard:
-                        continue
-                    if name not in present:
-                        raise ValueError(f"tensor {name} is not in its shard {shard}")
-                    sl = f.get_slice(name)
-                    self._shapes[name] = (tuple(sl.get_shape()), sl.get_dtype())
+        self._handles: dict[str, object] = {}  # one open handle per shard (header parsed once)
+        by_shard: dict[str, list[str]] = {}
+        for name, shard in self._weight_map.items():
+            by_shard.setdefault(shard, []).append(name)
+        for shard in sorted(by_shard):
+            if not (self.directory / shard).is_file():
+                raise FileNotFoundError(f"safetensors shard is missing: {self.directory / shard}")
+            f = self._handle(shard)
+            present = set(f.keys())
+            for name in by_shard[shard]:
+                if name not in present:
+                    raise ValueError(f"tensor {name} is not in its shard {shard}")
+                sl = f.get_slice(name)
+                self._shapes[name] = (tuple(sl.get_shape()), sl.get_dtype())
+
+    def _handle(self, shard: str):
+        f = self._handles.get(shard)
+        if f is None:
+            f = safe_open(str(self.directory / shard), framework="pt", device="cpu")
+            self._handles[shard] = f
+        return f
+
+    def close(self) -> None:
+        """Drop the open shard handles (their memory maps)."""
+        self._handles.clear()
 
     @property
     def names(self) -> tuple[str, ...]:
@@ -137,9 +145,7 @@ class W4A16Index:
              out: torch.Tensor | None = None) -> torch.Tensor:
         """One tensor, on ``device`` or copied into ``out`` (same shape and dtype)."""
         self.spec(name)
-        path = self.directory / self._weight_map[name]
-        with safe_open(str(path), framework="pt", device="cpu") as f:
-            t = f.get_tensor(name)
+        t = self._handle(self._weight_map[name]).get_tensor(name)
         if out is not None:
             if tuple(out.shape) != tuple(t.shape) or out.dtype != t.dtype:
                 raise ValueError(f"{name}: destination {tuple(out.shape)} {out.dtype} does not match "
