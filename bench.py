@@ -13,6 +13,11 @@ and replayed; inputs are resident in HBM before the timed region.
 ``--workload dense_decode``: x [1, 2304] x W [9216, 2304] at group 128, 40
 rotated weight copies (439 MB).
 
+``--workload klinear_decode``: the model-slice caller of the same layer
+(``local_kimi_amd.klinear.KLinearMoE``: the router logits ``x Wg^T`` in fp32
+from bf16 router weights, then the MoE block), 26 layers with their own
+router weights, one token per layer step, captured in one HIP graph.
+
 Prints ONE JSON line. ``roofline`` is for the dominant kernel (gate/up +
 SwiGLU, or the dense GEMV), timed with HIP events on the stream it runs on;
 ``cpu_baseline`` times the numpy oracle of the same step on the host (one
@@ -219,6 +224,65 @@ def run_moe(args, dev) -> dict:
         log(f"[bench] timing the CPU oracle on {args.cpu_sample} tokens")
         result["cpu_baseline"] = cpu_baseline_moe(banks[0], xs, logits, args.cpu_sample)
     return result
+
+
+def run_klinear_decode(args, dev) -> dict:
+    from local_kimi_amd.checkpoint import MoeBanks
+    from local_kimi_amd.klinear import KLinearMoE
+
+    layers = args.layers
+    gen = torch.Generator(device=dev).manual_seed(20260729)
+    t0 = time.time()
+    master = (*make_bank(INTER, H, E_ROUTED + 1, gen, dev), *make_bank(INTER, H, E_ROUTED + 1, gen, dev),
+              *make_bank(H, INTER, E_ROUTED + 1, gen, dev))
+    mods = []
+    for l in range(layers):
+        b = master if l == 0 else tuple(t.clone() for t in master)
+        gate = (torch.randn((E_ROUTED, H), device=dev, generator=gen) * (1.0 / H ** 0.5)).to(torch.bfloat16)
+        bias = torch.randn((E_ROUTED,), device=dev, generator=gen) * 0.01
+        mods.append(KLinearMoE(gate, bias, MoeBanks(*b), top_k=TOP_K, routed_scaling_factor=SCALING))
+    xs = [(torch.randn((1, H), device=dev, generator=gen)).to(torch.bfloat16) for _ in range(layers)]
+    torch.cuda.synchronize()
+    log(f"[bench] {layers} KLinearMoE layers ready in {time.time() - t0:.1f}s")
+    stream = torch.cuda.Stream(device=dev)
+
+    def all_layers():
+        for l in range(layers):
+            mods[l](xs[l])
+
+    graph = capture(all_layers, stream)
+    steps = max(layers, (args.steps + layers - 1) // layers * layers)
+    warm = max(1, (args.warmup + layers - 1) // layers)
+    for _ in range(warm):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = time_graph(graph, steps // layers, stream)
+    us = ms * 1000.0 / steps
+    router_bytes = E_ROUTED * H * 2
+    step_bytes = (TOP_K + 1) * EXPERT_BYTES + TOKEN_IO_BYTES + router_bytes
+    log(f"[bench] KLinearMoE decode {us:.2f} us/token")
+    return {
+        "metric": "MoE-layer decode us/token + achieved HBM GB/s (% of peak) at W4A16",
+        "value": round(us, 3),
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm * layers,
+        "ms_per_step": round(ms / steps, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x, "
+                "N(0,1/H) bf16 router weights",
+        "config": {"workload": "klinear_moe_decode_batch1", "hidden": H, "routed_experts": E_ROUTED,
+                   "shared_experts": 1, "moe_intermediate": INTER, "top_k": TOP_K, "group_size": G,
+                   "tokens_per_step": 1, "layer_banks_rotated": layers,
+                   "router": "lk_router_logits (bf16 x, bf16 Wg [256, 2304], fp32 sums), then the MoE block"},
+        "achieved_gbps": round(step_bytes / (us * 1e3), 1),
+        "pct_hbm_peak": round(100.0 * step_bytes / (us * 1e3) / HBM_PEAK_GBPS, 2),
+        "algorithmic_bytes_per_step": step_bytes,
+    }
 
 
 def run_dense(args, dev) -> dict:
@@ -540,7 +604,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=260)
     ap.add_argument("--workload", default="moe_decode",
                     choices=["moe_decode", "dense_decode", "moe_batched", "moe_prefill",
-                             "qkv_prefill", "copy"])
+                             "qkv_prefill", "klinear_decode", "copy"])
     ap.add_argument("--tokens", type=int, default=64, help="moe_batched tokens per step")
     ap.add_argument("--moe-path", choices=["auto", "expert", "token"], default="auto",
                     help="moe_batched: the block's choice, expert-major GEMMs or token-major GEMVs")
@@ -566,7 +630,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     log(f"[bench] device {torch.cuda.get_device_name(0)}, workload {args.workload}")
     runners = {"moe_decode": run_moe, "dense_decode": run_dense, "moe_batched": run_moe_batched,
-               "moe_prefill": run_moe_prefill, "qkv_prefill": run_qkv_prefill, "copy": run_copy}
+               "moe_prefill": run_moe_prefill, "qkv_prefill": run_qkv_prefill,
+               "klinear_decode": run_klinear_decode, "copy": run_copy}
     result = runners[args.workload](args, dev)
     print(json.dumps(result), flush=True)
     return 0

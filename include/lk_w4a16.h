@@ -120,6 +120,13 @@ LK_API int lk_w4a16_w2_combine(const uint16_t* activated, const int64_t* expert_
                         int64_t routes, int64_t experts, int64_t h, int64_t i,
                         int64_t group_size, void* stream);
 
+/* ---- router logits: engine/klinear/router.py:50-51
+ * logits fp32 [T,E] = fp32(x bf16 [T,H]) . fp32(w bf16 [E,H])^T, products exact,
+ * fp32 sums in a fixed order (reruns bit-identical; not torch's order).
+ * Requires H % 8 == 0 and H <= 4096. */
+LK_API int lk_router_logits(const uint16_t* x, const uint16_t* w, float* logits, int64_t tokens,
+                            int64_t experts, int64_t h, void* stream);
+
 /* ---- router: engine/klinear/router.py:47-85 (on precomputed fp32 logits)
  * idx int64 [T,top_k] in descending choice score (sigmoid + bias), ties to the
  * lower id; weights fp32 [T,top_k] = sigmoid gathered, renormalised by

@@ -858,6 +858,60 @@ int pick_iters(int cpr) {
 
 constexpr size_t kMaxLds = 64 * 1024;
 
+// ---------------------------------------------------------------------------
+// Router logits (engine/klinear/router.py:50-51): logits[t, e] =
+// sum_k fp32(x[t, k]) * fp32(w[e, k]) for bf16 x and router weight w (each
+// product is exact in fp32). One wave per (token, expert row): lane l takes
+// the 16-byte chunks l, l + 64, ... of the row (every load issued before the
+// first FMA), sums them in order, then the wave reduces in a fixed order (DPP
+// within 8 lanes, then the 8 group sums in lane order), so reruns are
+// bit-identical.
+constexpr int kLogitWaves = 4;
+constexpr int kLogitIters = 8;  // chunks per lane: h <= 64 * 8 * 8 = 4096
+
+__global__ void __launch_bounds__(kLogitWaves * 64)
+router_logits_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                     float* __restrict__ logits, int64_t experts, int64_t h) {
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * kLogitWaves + wave;
+  const int64_t t = blockIdx.y;
+  if (e >= experts) return;  // wave-uniform
+  const int64_t chunks = h / 8;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + t * h);
+  const uint4* wr = reinterpret_cast<const uint4*>(w + e * h);
+  uint4 xv[kLogitIters], wv[kLogitIters];
+#pragma unroll
+  for (int i = 0; i < kLogitIters; ++i) {
+    const int64_t c = lane + kWave * i;
+    const int64_t cc = c < chunks ? c : 0;
+    xv[i] = xr[cc];
+    wv[i] = wr[cc];
+  }
+  // a chunk past the row keeps acc (a select, not a branch, so the loads
+  // above stay batched)
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < kLogitIters; ++i) {
+    const bool ok = lane + kWave * i < chunks;
+    const uint32_t a[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+    const uint32_t b[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+    float part = acc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      part = fmaf(bf16_to_f32(a[j] & 0xFFFFu), bf16_to_f32(b[j] & 0xFFFFu), part);
+      part = fmaf(bf16_to_f32(a[j] >> 16), bf16_to_f32(b[j] >> 16), part);
+    }
+    acc = ok ? part : acc;
+  }
+  acc = sum8(acc);
+  float total = 0.f;
+#pragma unroll
+  for (int gidx = 0; gidx < 8; ++gidx)
+    total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), gidx * 8));
+  if (lane == 0) logits[t * experts + e] = total;
+}
+
 }  // namespace
 }  // namespace lk
 
@@ -866,6 +920,22 @@ using namespace lk;
 extern "C" {
 
 constexpr int kNR = 2;  // weight rows per lane in the K-split kernels
+
+int lk_router_logits(const uint16_t* x, const uint16_t* w, float* logits, int64_t tokens,
+                     int64_t experts, int64_t h, void* stream) {
+  LK_REQUIRE(w && logits, "null pointer argument");
+  LK_REQUIRE(experts > 0 && h > 0 && tokens >= 0, "invalid router dimensions");
+  LK_REQUIRE(h % 8 == 0 && h <= 64 * 8 * kLogitIters,
+             "router logits need hidden %% 8 == 0 and hidden <= %d, got %lld", 64 * 8 * kLogitIters,
+             (long long)h);
+  LK_REQUIRE(tokens <= 65535 && experts <= 4 * 65535LL, "too many tokens or experts for one call");
+  if (tokens == 0) return LK_OK;
+  LK_REQUIRE(x != nullptr, "null activation pointer");
+  dim3 grid(static_cast<unsigned>((experts + kLogitWaves - 1) / kLogitWaves),
+            static_cast<unsigned>(tokens));
+  router_logits_kernel<<<grid, kLogitWaves * kWave, 0, as_stream(stream)>>>(x, w, logits, experts, h);
+  return check_launch("lk_router_logits");
+}
 
 int lk_w4a16_dense(const uint16_t* x, const uint8_t* packed, const uint16_t* scales, uint16_t* y,
                    int64_t m, int64_t n, int64_t k, int64_t group_size, void* stream) {

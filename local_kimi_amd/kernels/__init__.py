@@ -17,7 +17,7 @@ raises on first call.
 """
 
 from . import registry
-from .moe import (moe_router, moe_schedule, shape_stable_expert_indices, w4a16_moe_block,
+from .moe import (moe_router, moe_schedule, router_logits, shape_stable_expert_indices, w4a16_moe_block,
                   w4a16_moe_block_reference, w4a16_moe_decode, w4a16_moe_forward,
                   w4a16_moe_gateup)
 from .mxfp4 import (grouped_mxfp4_gemm, grouped_mxfp4_reference, grouped_mxfp4_swiglu_gemm,
@@ -141,7 +141,8 @@ _register_mxfp4()
 
 __all__ = [
     "registry", "W4A16_GROUPED", "W4A16_DENSE", "W4A16_SWIGLU", "W4A16_FUSED_QKV",
-    "W4A16_W2_COMBINE", "W4A16_MOE_BLOCK", "moe_router", "shape_stable_expert_indices",
+    "W4A16_W2_COMBINE", "W4A16_MOE_BLOCK", "moe_router", "router_logits",
+    "shape_stable_expert_indices",
     "w4a16_moe_block", "w4a16_moe_decode", "w4a16_moe_forward", "w4a16_moe_gateup",
     "moe_schedule", "w4a16_dense", "w4a16_dense_gemm", "grouped_w4a16_gemv",
     "grouped_w4a16_gemm", "grouped_w4a16_swiglu_gemv", "grouped_w4a16_swiglu_gemm",

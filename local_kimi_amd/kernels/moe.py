@@ -114,6 +114,36 @@ def moe_router(logits: torch.Tensor, bias: torch.Tensor | None, top_k: int, *,
     return idx, w
 
 
+ROUTER_LOGITS_MAX_TOKENS = 64  # beyond: a GEMM (torch) reads the router weight fewer times
+
+
+def router_logits(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """``fp32(hidden) @ fp32(weight).T`` -> float32 ``[T, E]`` (router.py:50-51).
+
+    bf16 ``hidden [T, H]`` and bf16 ``weight [E, H]`` with ``H % 8 == 0`` and
+    ``H <= 4096`` and up to ``ROUTER_LOGITS_MAX_TOKENS`` tokens: one HIP launch
+    (exact products, fp32 sums in a fixed order). Otherwise torch's fp32 GEMM
+    on the same device, as the reference computes it.
+    """
+    if hidden.ndim != 2 or weight.ndim != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError("router logits need hidden [T, H] and weight [E, H]")
+    if hidden.device != weight.device:
+        raise ValueError("router inputs must share one device")
+    tokens, h = hidden.shape
+    experts = weight.shape[0]
+    if (hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or h % 8 or h > 4096
+            or tokens > ROUTER_LOGITS_MAX_TOKENS or hidden.device.type != "cuda"):
+        return torch.nn.functional.linear(hidden.float(), weight.float(), None)
+    out = torch.empty((tokens, experts), dtype=torch.float32, device=hidden.device)
+    if tokens == 0:
+        return out
+    x, w = _w._c(hidden), _w._c(weight)
+    with torch.cuda.device(hidden.device):
+        _lib.call("lk_router_logits", x.data_ptr(), w.data_ptr(), out.data_ptr(), tokens, experts, h,
+                  _w._stream(hidden.device))
+    return out
+
+
 def _validate_stage1(hidden, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales, top_k):
     if hidden.ndim != 2 or hidden.dtype != torch.bfloat16:
         raise TypeError("hidden states must be a BF16 [tokens, hidden] matrix")

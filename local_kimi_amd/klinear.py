@@ -5,7 +5,8 @@
   resolved once per module, restore the shape.
 * :class:`KLinearMoE` -- the grouped W4A16 route of ``KLinearMoE``
   (engine/klinear/moe.py:278-334) with the router of
-  engine/klinear/router.py:47-85: ``logits = fp32(x) fp32(Wg)^T`` (torch GEMM),
+  engine/klinear/router.py:47-85: ``logits = fp32(x) fp32(Wg)^T`` (one HIP
+  launch for bf16 router weights and decode batches, else torch's fp32 GEMM),
   then the ``w4a16_moe_block`` op (selection, SwiGLU experts, W2, combine,
   shared expert with weight 1) over banks with the shared expert last.
 * :class:`MoEDecodeGraph` -- one MoE layer's decode step captured once in a
@@ -16,11 +17,10 @@
 from __future__ import annotations
 
 import torch
-import torch.nn.functional as F
 from torch import nn
 
 from .checkpoint import MoeBanks, W4A16Index, build_moe_banks
-from .kernels import W4A16_DENSE, W4A16_MOE_BLOCK, registry
+from .kernels import W4A16_DENSE, W4A16_MOE_BLOCK, registry, router_logits
 from .quant.w4a16 import W4A16Tensor
 
 HIDDEN = 2304         # Kimi-Linear hidden size (engine/klinear/config.py:42)
@@ -78,8 +78,9 @@ class KLinearMoE(nn.Module):
         self.top_k = top_k
         self.routed_scaling_factor = routed_scaling_factor
         self.renormalize = renormalize
-        # the router runs in fp32 (router.py:51); kept as fp32 once, not per call
-        self.register_buffer("gate_weight", gate_weight.float().contiguous(), persistent=False)
+        # the router computes in fp32 (router.py:51) from the weight as stored
+        # (bf16 in the checkpoint layout, exact in fp32)
+        self.register_buffer("gate_weight", gate_weight.contiguous(), persistent=False)
         bias = None if e_score_correction_bias is None else e_score_correction_bias.float().contiguous()
         self.register_buffer("e_score_correction_bias", bias, persistent=False)
         self.banks = banks
@@ -100,7 +101,7 @@ class KLinearMoE(nn.Module):
         return cls(gate, bias, banks, top_k=top_k, routed_scaling_factor=routed_scaling_factor)
 
     def router_logits(self, flat: torch.Tensor) -> torch.Tensor:
-        return F.linear(flat.float(), self.gate_weight, None)
+        return router_logits(flat, self.gate_weight)
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
         if hidden_states.shape[-1] != self.hidden_size:

@@ -2,12 +2,14 @@
 engine/klinear/moe.py:278-334, engine/generate.py:226-306).
 
 ``W4A16Linear`` and ``KLinearMoE`` are loaded from a W4A16 checkpoint written
-in the reference's layout (G = 128), run through the registry's default
-(HIP) ops, and are checked against the oracle within the quantized-matmul
-tolerance (1e-2 relative / 2e-2 absolute in bf16). The router logits are a
-torch fp32 GEMM on the GPU, whose bits are not the oracle's; the oracle block
-is therefore fed the logits the GPU computed (the selection from given
-logits is what the kernels own, and is compared bit-exactly elsewhere).
+in the reference's layout (G = 128, bf16 router weight), run through the
+registry's default (HIP) ops, and are checked against the oracle within the
+quantized-matmul tolerance (1e-2 relative / 2e-2 absolute in bf16). The
+router logits (router.py:50-51) are fp32 sums of exact bf16 products in this
+build's fixed order, not the oracle's or torch's: they are checked against a
+float64 sum within 2e-6 relative, and the oracle block is fed the logits the
+GPU computed (the selection from given logits is what the kernels own, and
+is compared bit-exactly elsewhere).
 ``MoEDecodeGraph`` replays are compared with eager forwards bit for bit,
 with eager work between replays.
 """
@@ -21,7 +23,7 @@ import torch
 from oracle import moe as OM
 from oracle import w4a16 as OW
 
-from ._helpers import assert_close_bf16, from_bits, random_bf16_bits, to_bits
+from ._helpers import assert_close_bf16, bf16_values, from_bits, random_bf16_bits, to_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -63,13 +65,37 @@ def ckpt(tmp_path_factory):
     lin, lin_ps = enc(384, HIDDEN)
     tensors["model.layers.0.mlp.up_proj.weight"] = lin
     prefix = f"model.layers.{LAYER}.block_sparse_moe.gate."
-    tensors[prefix + "weight"] = torch.from_numpy(rng.normal(0, 0.05, (EXPERTS, HIDDEN)).astype(np.float32))
+    tensors[prefix + "weight"] = torch.from_numpy(
+        rng.normal(0, 0.05, (EXPERTS, HIDDEN)).astype(np.float32)).to(torch.bfloat16)
     tensors[prefix + "e_score_correction_bias"] = torch.from_numpy(
         rng.normal(0, 0.02, EXPERTS).astype(np.float32))
     save_w4a16_checkpoint(path, tensors)
     stacked = [np.stack([ps[j] for ps in banks[b]]) for b in ("w1", "w3", "w2") for j in (0, 1)]
     bias = tensors[prefix + "e_score_correction_bias"].numpy()
     return path, lin_ps, stacked, bias
+
+
+@pytest.mark.parametrize("tokens,experts,h", [(1, 256, 2304), (5, 16, 256), (64, 40, 4096), (3, 7, 8)])
+def test_router_logits(rng, tokens, experts, h):
+    from local_kimi_amd.kernels import router_logits
+
+    x = random_bf16_bits(rng, (tokens, h))
+    w = random_bf16_bits(rng, (experts, h), 0.05)
+    got = router_logits(from_bits(x, DEV), from_bits(w, DEV))
+    assert got.dtype == torch.float32 and got.shape == (tokens, experts)
+    want = bf16_values(x).astype(np.float64) @ bf16_values(w).astype(np.float64).T
+    np.testing.assert_allclose(got.cpu().numpy(), want, rtol=2e-6, atol=2e-6 * np.abs(want).max())
+    assert torch.equal(got, router_logits(from_bits(x, DEV), from_bits(w, DEV)))
+
+
+def test_router_logits_past_the_decode_path_is_torch(rng):
+    from local_kimi_amd.kernels import router_logits
+
+    x = from_bits(random_bf16_bits(rng, (65, 256)), DEV)
+    w = from_bits(random_bf16_bits(rng, (16, 256), 0.05), DEV)
+    assert torch.equal(router_logits(x, w), torch.nn.functional.linear(x.float(), w.float()))
+    with pytest.raises(ValueError, match="router logits need"):
+        router_logits(x, w[:, :128])
 
 
 def test_w4a16_linear_matches_oracle(ckpt, rng):
