@@ -663,9 +663,12 @@ moe_gateup_ksplit_kernel(const uint16_t* __restrict__ x, const float* __restrict
 
 // ---------------------------------------------------------------------------
 // W2 + combine: blockIdx.y = token, blockIdx.x = 8 rows of H. The block's
-// kW2Waves waves split the routes (wave w takes routes w, w + kW2Waves, ...),
-// so each wave keeps at most RPW routes of weight loads in flight; all waves
-// share the staged activations of every route. Route outputs are rounded to
+// W waves split the routes (wave w takes routes w, w + W, ...), so each wave
+// keeps at most RPW routes of weight loads in flight; all waves share the
+// staged activations of every route. A wave issues its routes' loads last
+// route first: the last route (the shared expert when shared_id >= 0) needs
+// no expert id, so its weights are requested before the ids written by the
+// gate/up kernel arrive. Route outputs are rounded to
 // bf16 and combined by one wave in route order: weighted fp32 sum of routes
 // 0..R-2, rounded to bf16, plus the last route (the shared expert) with
 // weight 1. Route r's expert is idx[t * idx_stride + r]; when shared_id >= 0
@@ -674,8 +677,8 @@ moe_gateup_ksplit_kernel(const uint16_t* __restrict__ x, const float* __restrict
 
 constexpr int kW2Waves = 4;
 
-template <int ITERS, int RPW>
-__global__ void __launch_bounds__(256)
+template <int ITERS, int RPW, int W>
+__global__ void __launch_bounds__(W * kWave)
 w2_combine_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ idx,
                   int64_t idx_stride, int64_t shared_id, const float* __restrict__ cw,
                   int64_t cw_stride, const uint8_t* __restrict__ w2p,
@@ -687,12 +690,15 @@ w2_combine_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ 
   const Shape sh = make_shape(inter, group);
   const XStage st = make_stage(smem, routes, sh.cpr);
   // expert ids of this wave's routes: wave-uniform scalar loads, all issued
-  // before any weight load
+  // before any weight load; the shared expert's id is known without a load
   int64_t e_of[RPW];
 #pragma unroll
   for (int q = 0; q < RPW; ++q) {
-    const int r = min(wave + kW2Waves * q, routes - 1);
-    e_of[q] = (shared_id >= 0 && r == routes - 1) ? shared_id : idx[t * idx_stride + r];
+    const int r = min(wave + W * q, routes - 1);
+    if (shared_id >= 0 && r == routes - 1)  // wave-uniform branch
+      e_of[q] = shared_id;
+    else
+      e_of[q] = idx[t * idx_stride + r];
   }
   float* eo_lds = reinterpret_cast<float*>(st.off + static_cast<size_t>(routes) * sh.cpr);
   const uint16_t* xa = act + t * routes * inter;
@@ -712,7 +718,7 @@ w2_combine_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ 
   Batch<1, 1, ITERS> b[RPW];
   bool valid[RPW];
 #pragma unroll
-  for (int q = 0; q < RPW; ++q) {
+  for (int q = RPW - 1; q >= 0; --q) {
     valid[q] = e_of[q] >= 0 && e_of[q] < experts;
     const int64_t e = valid[q] ? e_of[q] : 0;
     const uint8_t* const wp[1] = {w2p + e * wstride};
@@ -724,8 +730,8 @@ w2_combine_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ 
   __syncthreads();
 
 #pragma unroll
-  for (int q = 0; q < RPW; ++q) {
-    const int r = wave + kW2Waves * q;
+  for (int q = RPW - 1; q >= 0; --q) {  // in load order
+    const int r = wave + W * q;
     if (r < routes) {  // wave-uniform
       const int64_t e = valid[q] ? e_of[q] : 0;
       const uint8_t* const wp[1] = {w2p + e * wstride};
@@ -804,6 +810,98 @@ w2_ksplit_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ i
 }
 
 // ---------------------------------------------------------------------------
+// W2 + combine, one wave per route (reduction width inter = 32 chunks of 32):
+// the block is `routes` waves (wave r = route r), blockIdx.x covers rows
+// row0 .. row0 + rb - 1 of H and blockIdx.y is the token. The host picks
+// rb = H / CUs rounded up, so a batch-1 grid is one block per CU: with 8-row
+// blocks (288 for H = 2304) some CUs run two blocks and finish last. Lane
+// (hf, c) = (lane >> 5, lane & 31) owns chunk c of its route's activation row,
+// loaded straight into registers before the expert id arrives (no LDS
+// staging), and rows row0 + 2j + hf (j < J) of the route's expert. A row sum
+// is reduced over the 32 lanes of its half-wave in a fixed order; route
+// outputs pass through LDS to the combine, which rounds as the other W2
+// kernels do.
+constexpr int kW2RouteCpr = 32;
+
+template <int J>
+__global__ void __launch_bounds__(1024)
+w2_route_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ idx,
+                int64_t idx_stride, int64_t shared_id, const float* __restrict__ cw,
+                int64_t cw_stride, const uint8_t* __restrict__ w2p,
+                const uint16_t* __restrict__ w2s, uint16_t* __restrict__ y, int routes,
+                int64_t experts, int64_t h, int64_t inter, int64_t group, int rb) {
+  __shared__ float eo_lds[kMaxKWaves][2 * J];
+  __shared__ float cw_lds[kMaxKWaves];
+  const int r = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int hf = lane >> 5, c = lane & 31;
+  const int64_t t = blockIdx.y;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * rb;
+  const int64_t row_end = min(row0 + rb, h);
+  // loads that do not depend on the expert ids go first
+  const uint4* xs = reinterpret_cast<const uint4*>(act + (t * routes + r) * inter + c * 32);
+  uint4 xv[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) xv[q] = xs[q];
+  const float cw_mine =
+      static_cast<int>(threadIdx.x) + 1 < routes ? cw[t * cw_stride + threadIdx.x] : 0.f;
+  int64_t e;
+  if (shared_id >= 0 && r == routes - 1)  // wave-uniform: the shared expert needs no load
+    e = shared_id;
+  else
+    e = idx[t * idx_stride + r];
+  const bool valid = e >= 0 && e < experts;
+  const int64_t ec = valid ? e : 0;
+  const int64_t bytes_row = inter >> 1;
+  const int spr = static_cast<int>(inter / group);
+  const int gshift = __ffs(static_cast<int>(group >> 5)) - 1;
+  const uint8_t* wb = w2p + ec * h * bytes_row + c * 16;
+  const uint16_t* sb = w2s + ec * h * spr + (c >> gshift);
+  uint4 w[J];
+  uint16_t sc[J];
+  bool ok[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int64_t row = row0 + 2 * j + hf;
+    ok[j] = row < row_end;
+    const int64_t rc = ok[j] ? row : row_end - 1;  // in bounds, branch-free
+    w[j] = load_stream_u4(wb + rc * bytes_row);
+    sc[j] = sb[rc * spr];
+  }
+  if (static_cast<int>(threadIdx.x) + 1 < routes) cw_lds[threadIdx.x] = cw_mine;
+  uint32_t xp[4][4];
+  float xsum = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    pair_x8(xv[q], xp[q]);
+    xsum += sum_x8(xv[q]);
+  }
+  const float xo = kCodeOffset * xsum;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    float a0 = dot8_int4(w[j].x, xp[0], 0.f);
+    float a1 = dot8_int4(w[j].y, xp[1], 0.f);
+    a0 = dot8_int4(w[j].z, xp[2], a0);
+    a1 = dot8_int4(w[j].w, xp[3], a1);
+    float v = bf16_to_f32(sc[j]) * ((a0 + a1) - xo);
+    v = sum8(v);                    // 8 lanes
+    v += dpp_f32<kRowMirror>(v);    // 16 lanes
+    v += __shfl_xor(v, 16);         // the 32 lanes of the half-wave
+    if (c == 0 && ok[j]) eo_lds[r][2 * j + hf] = valid ? round_bf16(v) : 0.f;
+  }
+  __syncthreads();
+  if (static_cast<int>(threadIdx.x) < rb) {
+    const int i = threadIdx.x;
+    const int64_t row = row0 + i;
+    if (row < h) {
+      float routed = 0.f;
+      for (int q = 0; q + 1 < routes; ++q) routed += eo_lds[q][i] * cw_lds[q];
+      y[t * h + row] = f32_to_bf16(round_bf16(routed) + eo_lds[routes - 1][i]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host-side dispatch
 
 int waves_per_block() {
@@ -824,6 +922,28 @@ bool w2_ksplit_enabled() {
     return v && atoi(v) == 1;
   }();
   return on;
+}
+
+// One wave per route with one block per CU is the batch-1 W2 form; LK_W2_ROUTE=0
+// selects the LDS-staged 8-row kernel instead.
+bool w2_route_enabled() {
+  static bool on = [] {
+    const char* v = getenv("LK_W2_ROUTE");
+    return !(v && atoi(v) == 0);
+  }();
+  return on;
+}
+
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64 && cache[dev] > 0) return cache[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  if (dev < 64) cache[dev] = cus;
+  return cus;
 }
 
 int w2_rows_per_lane() {
@@ -1079,15 +1199,34 @@ static int w2_combine_launch(const uint16_t* act, const int64_t* idx, int64_t id
 #undef LK_W2_KS
     return check_launch("w2_combine");
   }
+  const int cus = device_cus();
+  if (w2_route_enabled() && cpr == kW2RouteCpr && routes <= kMaxKWaves && cus > 0 &&
+      h <= 16LL * cus) {
+    const int rb = static_cast<int>((h + cus - 1) / cus);  // 1 .. 16
+    const int jn = (rb + 1) / 2;
+    dim3 g3(static_cast<unsigned>((h + rb - 1) / rb), static_cast<unsigned>(tokens));
+    const int threads = static_cast<int>(routes) * kWave;
+    const int rr = static_cast<int>(routes);
+#define LK_W2_RT(JV)                                                                         \
+  w2_route_kernel<JV><<<g3, threads, 0, s>>>(act, idx, idx_stride, shared_id, cw, cw_stride, \
+                                             w2p, w2s, y, rr, experts, h, inter, group, rb)
+    if (jn <= 1) LK_W2_RT(1);
+    else if (jn <= 2) LK_W2_RT(2);
+    else if (jn <= 3) LK_W2_RT(3);
+    else if (jn <= 5) LK_W2_RT(5);
+    else LK_W2_RT(8);
+#undef LK_W2_RT
+    return check_launch("w2_combine");
+  }
   dim3 grid(static_cast<unsigned>((h + 7) / 8), static_cast<unsigned>(tokens));
   const int iters = pick_iters(cpr);
   const int r = static_cast<int>(routes);
   if (routes <= 3 * kW2Waves) {
-    LK_ITERS_CASES(iters, (w2_combine_kernel<IT, 3><<<grid, kW2Waves * kWave, lds, s>>>(
+    LK_ITERS_CASES(iters, (w2_combine_kernel<IT, 3, kW2Waves><<<grid, kW2Waves * kWave, lds, s>>>(
                               act, idx, idx_stride, shared_id, cw, cw_stride, w2p, w2s, y, r,
                               experts, h, inter, group)));
   } else {
-    LK_ITERS_CASES(iters, (w2_combine_kernel<IT, 8><<<grid, kW2Waves * kWave, lds, s>>>(
+    LK_ITERS_CASES(iters, (w2_combine_kernel<IT, 8, kW2Waves><<<grid, kW2Waves * kWave, lds, s>>>(
                               act, idx, idx_stride, shared_id, cw, cw_stride, w2p, w2s, y, r,
                               experts, h, inter, group)));
   }

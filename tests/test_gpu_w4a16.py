@@ -241,6 +241,43 @@ def test_w2_combine_matches_oracle(rng, g):
     assert_close_bf16(to_bits(yr), expected, what="w2 combine reference")
 
 
+# H / CUs rounded up gives the rows per block of the one-wave-per-route W2 form
+# (reduction width 1024): 2, 3, 9 (last block partial) and 16 rows on 256 CUs
+@pytest.mark.parametrize("h,r", [(300, 9), (700, 5), (2300, 9), (4096, 16)])
+def test_w2_combine_route_form_row_splits(rng, h, r):
+    from local_kimi_amd.kernels import fused_w2_combine
+
+    e, i, t, g = 3, 1024, 2, 128
+    w2p, w2s = _bank(rng, e, h, i, g)
+    act = random_bf16_bits(rng, (t, r, i), 0.1)
+    idx = rng.integers(0, e, (t, r)).astype(np.int64)
+    cw = rng.random((t, r)).astype(np.float32)
+    expected = OM.w2_combine(act, idx, cw, w2p, w2s, g)
+    args = (_dev_bf16(act), torch.from_numpy(idx).to(DEV), torch.from_numpy(cw).to(DEV),
+            _dev_u8(w2p), _dev_bf16(w2s))
+    y = fused_w2_combine(*args)
+    assert torch.equal(y, fused_w2_combine(*args))
+    assert_close_bf16(to_bits(y), expected, what=f"w2 combine h={h} routes={r}")
+
+
+def test_w2_combine_out_of_range_index_counts_zero(rng):
+    """Routes whose expert id lies outside the bank contribute nothing."""
+    from local_kimi_amd.kernels import fused_w2_combine
+
+    e, h, i, t, r, g = 3, 512, 1024, 2, 9, 128
+    w2p, w2s = _bank(rng, e, h, i, g)
+    act = random_bf16_bits(rng, (t, r, i), 0.1)
+    idx = rng.integers(0, e, (t, r)).astype(np.int64)
+    idx[0, 2], idx[1, 5], idx[1, 0] = -1, e, 1000
+    cw = rng.random((t, r)).astype(np.float32)
+    bad = (idx < 0) | (idx >= e)
+    expected = OM.w2_combine(act, np.where(bad, 0, idx), np.where(bad, 0.0, cw).astype(np.float32),
+                             w2p, w2s, g)
+    y = fused_w2_combine(_dev_bf16(act), torch.from_numpy(idx).to(DEV), torch.from_numpy(cw).to(DEV),
+                         _dev_u8(w2p), _dev_bf16(w2s))
+    assert_close_bf16(to_bits(y), expected, what="w2 combine, routes outside the bank")
+
+
 # ---------------------------------------------------------------------------
 # router
 
