@@ -43,8 +43,10 @@ __device__ inline int64_t route_select(const float (&lg)[EPL], const float (&bs)
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     sc[j] = 1.0f / (1.0f + expf(-lg[j]));
-    // ids past the bank sit behind every real expert: key 0 and the highest slots
-    key[j] = lane * EPL + j < ne ? orderable(sc[j] + bs[j]) : 0u;
+    // ids past the bank sit behind every real expert: key 0 and the highest
+    // slots; live keys are at least 1 (orderable() gives 0 only for one NaN
+    // bit pattern, which then ties with the key above it)
+    key[j] = lane * EPL + j < ne ? max(orderable(sc[j] + bs[j]), 1u) : 0u;
     slot[j] = j;
   }
 #pragma unroll
@@ -62,36 +64,33 @@ __device__ inline int64_t route_select(const float (&lg)[EPL], const float (&bs)
       slot[b - 1] = sw ? q1 : q0;
       slot[b] = sw ? q0 : q1;
     }
-  const int n_live = max(0, min(EPL, ne - lane * EPL));  // real experts in this lane
-  int taken = 0;
-  uint32_t hk = key[0];
-  float hs = sc[0];
-  int hq = slot[0];
+  // Selection rounds. A lane's head is entry 0; the owner of a round shifts
+  // its entries down and fills key 0 behind them. Live keys are at least 1
+  // (set above), so a lane whose entries are used up, or that holds only ids
+  // past the bank, never matches the round's maximum while a live candidate
+  // is left (top_k <= ne). The shift is branch-free: one v_cndmask per entry.
   float ssum = 0.f;
   int64_t mine = -1;
   float my_score = 0.f;
   int64_t wanted = -1;
   for (int rr = 0; rr < top_k; ++rr) {
-    const bool has = taken < n_live;
-    const uint32_t kb = has ? hk : 0u;
+    const uint32_t kb = key[0];
     const uint32_t kmax = wave_max_u32(kb);
-    const uint64_t holders = __builtin_amdgcn_ballot_w64(has && kb == kmax);
-    const int owner = holders ? static_cast<int>(__builtin_ctzll(holders)) : 0;
-    const int q = __builtin_amdgcn_readlane(hq, owner);
-    const float score = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hs), owner));
+    const uint64_t holders = __builtin_amdgcn_ballot_w64(kb == kmax);
+    const int owner = static_cast<int>(__builtin_ctzll(holders | (1ull << 63)));
+    const int q = __builtin_amdgcn_readlane(slot[0], owner);
+    const float score = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc[0]), owner));
     const uint32_t sel = static_cast<uint32_t>(owner * EPL + q);
     // top_k <= ne guarantees a live candidate; stay in range regardless
     const uint32_t safe = sel < static_cast<uint32_t>(ne) ? sel : 0u;
-    if (lane == owner) {
-      ++taken;
+    const bool own = lane == owner;
 #pragma unroll
-      for (int j = 1; j < EPL; ++j)
-        if (taken == j) {
-          hk = key[j];
-          hs = sc[j];
-          hq = slot[j];
-        }
+    for (int j = 0; j + 1 < EPL; ++j) {
+      key[j] = own ? key[j + 1] : key[j];
+      sc[j] = own ? sc[j + 1] : sc[j];
+      slot[j] = own ? slot[j + 1] : slot[j];
     }
+    key[EPL - 1] = own ? 0u : key[EPL - 1];
     ssum += score;
     mine = lane == rr ? static_cast<int64_t>(safe) : mine;
     my_score = lane == rr ? score : my_score;
@@ -106,19 +105,28 @@ __device__ inline int64_t route_select(const float (&lg)[EPL], const float (&bs)
   return wanted;
 }
 
+// The lane's logits and biases (zeros without a bias), every load issued
+// before any is used.
 template <int EPL>
-__device__ inline int64_t route_token(const float* __restrict__ logits,
-                                      const float* __restrict__ bias, int ne, int top_k, int want,
-                                      float scaling, int renorm, int64_t* __restrict__ idx_out,
-                                      float* __restrict__ w_out, int32_t* sel_out = nullptr) {
-  float lg[EPL], bs[EPL];
-  route_load<EPL>(logits, ne, lg);  // all loads first
+__device__ inline void route_load_all(const float* __restrict__ logits,
+                                      const float* __restrict__ bias, int ne, float (&lg)[EPL],
+                                      float (&bs)[EPL]) {
+  route_load<EPL>(logits, ne, lg);
   if (bias) {
     route_load<EPL>(bias, ne, bs);
   } else {
 #pragma unroll
     for (int j = 0; j < EPL; ++j) bs[j] = 0.0f;
   }
+}
+
+template <int EPL>
+__device__ inline int64_t route_token(const float* __restrict__ logits,
+                                      const float* __restrict__ bias, int ne, int top_k, int want,
+                                      float scaling, int renorm, int64_t* __restrict__ idx_out,
+                                      float* __restrict__ w_out, int32_t* sel_out = nullptr) {
+  float lg[EPL], bs[EPL];
+  route_load_all<EPL>(logits, bias, ne, lg, bs);  // all loads first
   return route_select<EPL>(lg, bs, ne, top_k, want, scaling, renorm, idx_out, w_out, sel_out);
 }
 

@@ -125,11 +125,13 @@ struct Shape {
   int cpr;            // chunks per row (k / 32)
 };
 
+// group is a power of two >= 32 (host-checked): shifts, not a 64-bit divide
+// in every kernel's prologue ahead of its first load
 __device__ inline Shape make_shape(int64_t k, int64_t group) {
   Shape s;
   s.bytes_row = k >> 1;
-  s.spr = static_cast<int>(k / group);
   s.gshift = __ffs(static_cast<int>(group >> 5)) - 1;
+  s.spr = static_cast<int>(k >> (s.gshift + 5));
   s.cpr = static_cast<int>(k >> 5);
   return s;
 }
@@ -417,7 +419,7 @@ grouped_ksplit_kernel(const uint16_t* __restrict__ x, const int64_t* __restrict_
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const Shape sh = make_shape(k, group);
   const int64_t pair = blockIdx.y;
-  const int64_t t = pair / routes;
+  const int64_t t = static_cast<uint32_t>(pair) / static_cast<uint32_t>(routes);
   KSplit<MATS, NR, 1, CI> ks;
   ks.load_x(x + t * k, k, 1, wave, kw, sh.cpr);
   // an index outside the bank is an empty route: read expert 0, write zeros
@@ -499,7 +501,7 @@ grouped_gemv_kernel(const uint16_t* __restrict__ x, const int64_t* __restrict__ 
   const Shape sh = make_shape(k, group);
   const XStage st = make_stage(smem, 1, sh.cpr);
   const int64_t pair = blockIdx.y;
-  const int64_t t = pair / routes;
+  const int64_t t = static_cast<uint32_t>(pair) / static_cast<uint32_t>(routes);
   // An index outside the bank is an empty route: it reads expert 0 (always
   // in bounds) and writes zeros, rather than reading past the bank.
   const int64_t e_raw = idx[pair];
@@ -559,7 +561,7 @@ moe_gateup_kernel(const uint16_t* __restrict__ x, const float* __restrict__ logi
   extern __shared__ uint4 smem[];
   const int routes = top_k + 1;
   const int64_t pair = blockIdx.y;
-  const int64_t t = pair / routes;
+  const int64_t t = static_cast<uint32_t>(pair) / static_cast<uint32_t>(routes);
   const int r = static_cast<int>(pair - t * routes);
   const int ne = static_cast<int>(experts - 1);
   const Shape sh = make_shape(h, group);
@@ -620,20 +622,25 @@ moe_gateup_ksplit_kernel(const uint16_t* __restrict__ x, const float* __restrict
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int routes = top_k + 1;
   const int64_t pair = blockIdx.y;
-  const int64_t t = pair / routes;
+  const int64_t t = static_cast<uint32_t>(pair) / static_cast<uint32_t>(routes);
   const int r = static_cast<int>(pair - t * routes);
   const int ne = static_cast<int>(experts - 1);
   const Shape sh = make_shape(h, group);
   __shared__ int64_t routed_expert;
+  // the router's logits are the first loads of the routing wave, then every
+  // wave's activation chunks (they do not depend on routing)
+  const bool router = r < top_k && wave == 0;  // wave-uniform
+  float lg[EPL], bs[EPL];
+  if (router) route_load_all<EPL>(logits + t * ne, bias, ne, lg, bs);
   KSplit<2, NR, 1, CI> ks;
   ks.load_x(x + t * h, h, 1, wave, kw, sh.cpr);
   int64_t e;
   if (r < top_k) {  // block-uniform
-    if (wave == 0) {  // one wave routes; the others wait at the barrier
+    if (router) {  // one wave routes; the others wait at the barrier
       const bool writer = (r == 0 && blockIdx.x == 0);
-      const int64_t sel = route_token<EPL>(logits + t * ne, bias, ne, top_k, r, scaling, renorm,
-                                           writer ? idx_out + t * top_k : nullptr,
-                                           writer ? w_out + t * top_k : nullptr);
+      const int64_t sel = route_select<EPL>(lg, bs, ne, top_k, r, scaling, renorm,
+                                            writer ? idx_out + t * top_k : nullptr,
+                                            writer ? w_out + t * top_k : nullptr, nullptr);
       if ((threadIdx.x & (kWave - 1)) == 0) routed_expert = sel;
     }
     __syncthreads();
@@ -853,8 +860,8 @@ w2_route_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ id
   const bool valid = e >= 0 && e < experts;
   const int64_t ec = valid ? e : 0;
   const int64_t bytes_row = inter >> 1;
-  const int spr = static_cast<int>(inter / group);
   const int gshift = __ffs(static_cast<int>(group >> 5)) - 1;
+  const int spr = static_cast<int>(inter >> (gshift + 5));
   const uint8_t* wb = w2p + ec * h * bytes_row + c * 16;
   const uint16_t* sb = w2s + ec * h * spr + (c >> gshift);
   uint4 w[J];
