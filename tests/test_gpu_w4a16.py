@@ -129,6 +129,17 @@ def test_dense_decode_shape_full_size(rng):
     assert worst < 0.75
 
 
+# decode GEMV at output widths that leave a partial last 16-row block
+@pytest.mark.parametrize("n", [5000, 9000, 10000])
+def test_dense_decode_partial_row_blocks(rng, n):
+    from local_kimi_amd.kernels import w4a16_dense
+
+    _, p, s = _layer(rng, n, 2304, 128)
+    x = random_bf16_bits(rng, (1, 2304))
+    y = w4a16_dense(_dev_bf16(x), _dev_u8(p), _dev_bf16(s))
+    assert_close_bf16(to_bits(y), OW.dense(x, p, s, 128), what=f"dense n={n}")
+
+
 # ---------------------------------------------------------------------------
 # grouped / swiglu
 
