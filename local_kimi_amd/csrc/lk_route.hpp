@@ -73,7 +73,10 @@ __device__ inline int64_t route_select(const float (&lg)[EPL], const float (&bs)
   int64_t mine = -1;
   float my_score = 0.f;
   int64_t wanted = -1;
-  for (int rr = 0; rr < top_k; ++rr) {
+  // a caller that writes no outputs needs only the rounds up to `want`
+  const bool outputs = idx_out != nullptr || sel_out != nullptr;
+  const int rounds = outputs ? top_k : min(top_k, max(want + 1, 0));
+  for (int rr = 0; rr < rounds; ++rr) {
     const uint32_t kb = key[0];
     const uint32_t kmax = wave_max_u32(kb);
     const uint64_t holders = __builtin_amdgcn_ballot_w64(kb == kmax);
