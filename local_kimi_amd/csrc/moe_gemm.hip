@@ -215,9 +215,10 @@ schedule_place_kernel(const RouteTable rt, int64_t n, int chunks, Schedule sc) {
 // selections to LDS, and schedules from LDS: one launch instead of the
 // router's and the schedule's. The routing then runs on one CU, where each
 // token's selection rounds are a dependent chain: 4 tokens take 7.3 us here
-// against 9.7 us for the two launches, 16 tokens 9.7 us against 9.9 us, so
-// ROUTE serves batches of at most kFuseRouteTokens; larger ones route on a
-// grid of one block per token.
+// against 9.7 us for the two launches; at 8 tokens the whole step is the same
+// either way (52.3 against 52.7 us) and at 16 the two launches win (70.8
+// against 72.0 us), so ROUTE serves batches of at most kFuseRouteTokens;
+// larger ones route on a grid of one block per token.
 constexpr int kFuseThreads = 1024;
 constexpr int kFuseWaves = kFuseThreads / kWave;
 constexpr int kFuseRouteTokens = 8;

@@ -254,11 +254,12 @@ def test_w2_combine_matches_oracle(rng, g):
 
 # H / CUs rounded up gives the rows per block of the one-wave-per-route W2 form
 # (reduction width 1024): 2, 3, 9 (last block partial) and 16 rows on 256 CUs
-@pytest.mark.parametrize("h,r", [(300, 9), (700, 5), (2300, 9), (4096, 16)])
-def test_w2_combine_route_form_row_splits(rng, h, r):
+@pytest.mark.parametrize("h,r,g", [(300, 9, 128), (700, 5, 64), (2300, 9, 128), (2300, 9, 256),
+                                   (4096, 16, 128)])
+def test_w2_combine_route_form_row_splits(rng, h, r, g):
     from local_kimi_amd.kernels import fused_w2_combine
 
-    e, i, t, g = 3, 1024, 2, 128
+    e, i, t = 3, 1024, 2
     w2p, w2s = _bank(rng, e, h, i, g)
     act = random_bf16_bits(rng, (t, r, i), 0.1)
     idx = rng.integers(0, e, (t, r)).astype(np.int64)
@@ -354,9 +355,11 @@ def test_moe_block_matches_oracle_small_bank(rng, tokens):
     assert_close_bf16(to_bits(yr), ey, what="moe block reference")
 
 
-def test_moe_block_decode_full_size(rng):
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_moe_block_decode_full_size(rng, with_bias):
     """Batch-1 decode at the Kimi-Linear MoE shape: hidden 2304, 256 routed +
-    1 shared expert, intermediate 1024, top-8, G=128, weights N(0, 0.02)."""
+    1 shared expert, intermediate 1024, top-8, G=128, weights N(0, 0.02);
+    with a router bias, and logits with exact ties near the top-8 boundary."""
     from local_kimi_amd.kernels import w4a16_moe_block
     from local_kimi_amd.quant import quantise
 
@@ -378,10 +381,16 @@ def test_moe_block_decode_full_size(rng):
     w2p, w2s = bank(h, i)
     x = random_bf16_bits(rng, (1, h))
     logits = rng.normal(0, 1, (1, e_total - 1)).astype(np.float32)
-    y, idx, w = w4a16_moe_block(_dev_bf16(x), torch.from_numpy(logits).to(DEV), None,
+    bias = rng.normal(0, 0.05, e_total - 1).astype(np.float32) if with_bias else None
+    if not with_bias:  # ties: copies of the 6th..9th largest logits at other ids
+        order = np.argsort(-logits[0], kind="stable")
+        logits[0, order[100:104]] = logits[0, order[5:9]]
+    y, idx, w = w4a16_moe_block(_dev_bf16(x), torch.from_numpy(logits).to(DEV),
+                                None if bias is None else torch.from_numpy(bias).to(DEV),
                                 w1p, w1s, w3p, w3s, w2p, w2s, 8, 2.446)
-    eidx, ew = OM.route(logits, None, 8, routed_scaling_factor=2.446)
+    eidx, ew = OM.route(logits, bias, 8, routed_scaling_factor=2.446)
     assert np.array_equal(idx.cpu().numpy(), eidx)
+    np.testing.assert_allclose(w.cpu().numpy(), ew, rtol=2e-6, atol=1e-7)
     # the oracle needs only the 9 experts this token uses
     used = list(eidx[0]) + [e_total - 1]
     sub = [t[used].cpu().numpy() if t.dtype == torch.uint8 else to_bits(t[used])
