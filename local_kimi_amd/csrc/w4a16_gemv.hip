@@ -817,21 +817,26 @@ w2_ksplit_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ i
 }
 
 // ---------------------------------------------------------------------------
-// W2 + combine, one wave per route (reduction width inter = 32 chunks of 32):
-// the block is `routes` waves (wave r = route r), blockIdx.x covers rows
-// row0 .. row0 + rb - 1 of H and blockIdx.y is the token. The host picks
-// rb = H / CUs rounded up, so a batch-1 grid is one block per CU: with 8-row
-// blocks (288 for H = 2304) some CUs run two blocks and finish last. Lane
-// (hf, c) = (lane >> 5, lane & 31) owns chunk c of its route's activation row,
-// loaded straight into registers before the expert id arrives (no LDS
-// staging), and rows row0 + 2j + hf (j < J) of the route's expert. A row sum
-// is reduced over the 32 lanes of its half-wave in a fixed order; route
-// outputs pass through LDS to the combine, which rounds as the other W2
-// kernels do.
+// W2 + combine for reduction width inter = 32 chunks of 32, one block per CU:
+// blockIdx.x covers rows row0 .. row0 + rb - 1 of H (the host picks
+// rb = H / CUs rounded up; with 8-row blocks, 288 for H = 2304, some CUs run
+// two blocks and finish last) and blockIdx.y is the token. The block's W
+// waves take routes w, w + W, ... (RPW at most); the decode launch uses one
+// wave per route. (The waves sharing a SIMD issue their loads later: per-wave
+// timestamps show routes 4-7 and 8 finishing 0.8 and 1.5 us after routes 0-3;
+// three or four waves with three or four routes each measured slower still,
+// 15.9 and 16.5 against 14.65 us per decode step.) Lane (hf, c) =
+// (lane >> 5, lane & 31) owns chunk c of each route's activation row, loaded
+// straight into registers before the expert ids arrive (no LDS staging), and
+// rows row0 + 2j + hf (j < J) of the route's expert; a wave issues its last
+// route first, which is the shared expert's (no id needed) when it has it.
+// A row sum is reduced over the 32 lanes of its half-wave in a fixed order;
+// route outputs pass through LDS to the combine, which rounds as the other
+// W2 kernels do.
 constexpr int kW2RouteCpr = 32;
 
-template <int J>
-__global__ void __launch_bounds__(1024)
+template <int J, int W, int RPW>
+__global__ void __launch_bounds__(W * kWave)
 w2_route_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ idx,
                 int64_t idx_stride, int64_t shared_id, const float* __restrict__ cw,
                 int64_t cw_stride, const uint8_t* __restrict__ w2p,
@@ -839,62 +844,82 @@ w2_route_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ id
                 int64_t experts, int64_t h, int64_t inter, int64_t group, int rb) {
   __shared__ float eo_lds[kMaxKWaves][2 * J];
   __shared__ float cw_lds[kMaxKWaves];
-  const int r = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x & (kWave - 1);
   const int hf = lane >> 5, c = lane & 31;
   const int64_t t = blockIdx.y;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * rb;
   const int64_t row_end = min(row0 + rb, h);
-  // loads that do not depend on the expert ids go first
-  const uint4* xs = reinterpret_cast<const uint4*>(act + (t * routes + r) * inter + c * 32);
-  uint4 xv[4];
+  // loads that do not depend on the expert ids go first: every route's
+  // activation chunk, the combine weights
+  uint4 xv[RPW][4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) xv[q] = xs[q];
+  for (int q = RPW - 1; q >= 0; --q) {
+    const int r = min(wave + W * q, routes - 1);
+    const uint4* xs = reinterpret_cast<const uint4*>(act + (t * routes + r) * inter + c * 32);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) xv[q][u] = xs[u];
+  }
   const float cw_mine =
       static_cast<int>(threadIdx.x) + 1 < routes ? cw[t * cw_stride + threadIdx.x] : 0.f;
-  int64_t e;
-  if (shared_id >= 0 && r == routes - 1)  // wave-uniform: the shared expert needs no load
-    e = shared_id;
-  else
-    e = idx[t * idx_stride + r];
-  const bool valid = e >= 0 && e < experts;
-  const int64_t ec = valid ? e : 0;
   const int64_t bytes_row = inter >> 1;
   const int gshift = __ffs(static_cast<int>(group >> 5)) - 1;
   const int spr = static_cast<int>(inter >> (gshift + 5));
-  const uint8_t* wb = w2p + ec * h * bytes_row + c * 16;
-  const uint16_t* sb = w2s + ec * h * spr + (c >> gshift);
-  uint4 w[J];
-  uint16_t sc[J];
+  uint4 w[RPW][J];
+  uint16_t sc[RPW][J];
+  bool valid[RPW];
   bool ok[J];
+  int64_t rc[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int64_t row = row0 + 2 * j + hf;
     ok[j] = row < row_end;
-    const int64_t rc = ok[j] ? row : row_end - 1;  // in bounds, branch-free
-    w[j] = load_stream_u4(wb + rc * bytes_row);
-    sc[j] = sb[rc * spr];
+    rc[j] = ok[j] ? row : row_end - 1;  // in bounds, branch-free
+  }
+#pragma unroll
+  for (int q = RPW - 1; q >= 0; --q) {
+    const int r = min(wave + W * q, routes - 1);
+    int64_t e;
+    if (shared_id >= 0 && r == routes - 1)  // wave-uniform: the shared expert needs no load
+      e = shared_id;
+    else
+      e = idx[t * idx_stride + r];
+    valid[q] = e >= 0 && e < experts;
+    const int64_t ec = valid[q] ? e : 0;
+    const uint8_t* wb = w2p + ec * h * bytes_row + c * 16;
+    const uint16_t* sb = w2s + ec * h * spr + (c >> gshift);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      w[q][j] = load_stream_u4(wb + rc[j] * bytes_row);
+      sc[q][j] = sb[rc[j] * spr];
+    }
   }
   if (static_cast<int>(threadIdx.x) + 1 < routes) cw_lds[threadIdx.x] = cw_mine;
-  uint32_t xp[4][4];
-  float xsum = 0.f;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    pair_x8(xv[q], xp[q]);
-    xsum += sum_x8(xv[q]);
-  }
-  const float xo = kCodeOffset * xsum;
+  for (int q = RPW - 1; q >= 0; --q) {  // in load order
+    const int r = wave + W * q;
+    if (r < routes) {  // wave-uniform
+      uint32_t xp[4][4];
+      float xsum = 0.f;
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    float a0 = dot8_int4(w[j].x, xp[0], 0.f);
-    float a1 = dot8_int4(w[j].y, xp[1], 0.f);
-    a0 = dot8_int4(w[j].z, xp[2], a0);
-    a1 = dot8_int4(w[j].w, xp[3], a1);
-    float v = bf16_to_f32(sc[j]) * ((a0 + a1) - xo);
-    v = sum8(v);                    // 8 lanes
-    v += dpp_f32<kRowMirror>(v);    // 16 lanes
-    v += __shfl_xor(v, 16);         // the 32 lanes of the half-wave
-    if (c == 0 && ok[j]) eo_lds[r][2 * j + hf] = valid ? round_bf16(v) : 0.f;
+      for (int u = 0; u < 4; ++u) {
+        pair_x8(xv[q][u], xp[u]);
+        xsum += sum_x8(xv[q][u]);
+      }
+      const float xo = kCodeOffset * xsum;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        float a0 = dot8_int4(w[q][j].x, xp[0], 0.f);
+        float a1 = dot8_int4(w[q][j].y, xp[1], 0.f);
+        a0 = dot8_int4(w[q][j].z, xp[2], a0);
+        a1 = dot8_int4(w[q][j].w, xp[3], a1);
+        float v = bf16_to_f32(sc[q][j]) * ((a0 + a1) - xo);
+        v = sum8(v);                    // 8 lanes
+        v += dpp_f32<kRowMirror>(v);    // 16 lanes
+        v += __shfl_xor(v, 16);         // the 32 lanes of the half-wave
+        if (c == 0 && ok[j]) eo_lds[r][2 * j + hf] = valid[q] ? round_bf16(v) : 0.f;
+      }
+    }
   }
   __syncthreads();
   if (static_cast<int>(threadIdx.x) < rb) {
@@ -1212,16 +1237,21 @@ static int w2_combine_launch(const uint16_t* act, const int64_t* idx, int64_t id
     const int rb = static_cast<int>((h + cus - 1) / cus);  // 1 .. 16
     const int jn = (rb + 1) / 2;
     dim3 g3(static_cast<unsigned>((h + rb - 1) / rb), static_cast<unsigned>(tokens));
-    const int threads = static_cast<int>(routes) * kWave;
     const int rr = static_cast<int>(routes);
-#define LK_W2_RT(JV)                                                                         \
-  w2_route_kernel<JV><<<g3, threads, 0, s>>>(act, idx, idx_stride, shared_id, cw, cw_stride, \
-                                             w2p, w2s, y, rr, experts, h, inter, group, rb)
-    if (jn <= 1) LK_W2_RT(1);
-    else if (jn <= 2) LK_W2_RT(2);
-    else if (jn <= 3) LK_W2_RT(3);
-    else if (jn <= 5) LK_W2_RT(5);
-    else LK_W2_RT(8);
+#define LK_W2_RT(JV, WV, RV, THREADS)                                                          \
+  w2_route_kernel<JV, WV, RV><<<g3, THREADS, 0, s>>>(act, idx, idx_stride, shared_id, cw,     \
+                                                     cw_stride, w2p, w2s, y, rr, experts, h, \
+                                                     inter, group, rb)
+#define LK_W2_RT_J(WV, RV, THREADS)          \
+  do {                                      \
+    if (jn <= 1) LK_W2_RT(1, WV, RV, THREADS);      \
+    else if (jn <= 2) LK_W2_RT(2, WV, RV, THREADS); \
+    else if (jn <= 3) LK_W2_RT(3, WV, RV, THREADS); \
+    else if (jn <= 5) LK_W2_RT(5, WV, RV, THREADS); \
+    else LK_W2_RT(8, WV, RV, THREADS);              \
+  } while (0)
+    LK_W2_RT_J(kMaxKWaves, 1, rr * kWave);  // one wave per route
+#undef LK_W2_RT_J
 #undef LK_W2_RT
     return check_launch("w2_combine");
   }
