@@ -447,7 +447,9 @@ def run_moe_batched(args, dev) -> dict:
         "achieved_gbps": round(gbps, 1),
         "pct_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
         "algorithmic_bytes_per_step": int(step_bytes),
-        "roofline": {"kernel": ("whole block (router, schedule, gate/up GEMM, down GEMM, combine)"
+        "roofline": {"kernel": (("whole block (router + schedule, gate/up GEMM, W2 + combine GEMV)"
+                                 if args.weights == "w4a16" and m <= 4 else
+                                 "whole block (router, schedule, gate/up GEMM, down GEMM, combine)")
                                 if path == "expert" else
                                 "whole block (router + gate/up GEMV, W2 + combine GEMV)"),
                      "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,

@@ -20,6 +20,15 @@ constexpr int kWave = 64;  // lanes per wavefront on CDNA
 void set_error(const char* fmt, ...);
 int fail_arg(const char* fmt, ...);
 int check_launch(const char* what);
+
+// W2 for every (token, route) row of `act` [tokens, routes, inter] plus the
+// route-weighted combine and the shared expert (the last route; bank entry
+// shared_id when shared_id >= 0), one launch: the token-major W2 kernels of
+// the decode path (w4a16_gemv.hip).
+int w2_combine_rows(const uint16_t* act, const int64_t* idx, int64_t idx_stride,
+                    int64_t shared_id, const float* cw, int64_t cw_stride, const uint8_t* w2p,
+                    const uint16_t* w2s, uint16_t* y, int64_t tokens, int64_t routes,
+                    int64_t experts, int64_t h, int64_t inter, int64_t group, hipStream_t s);
 // LK_OK when k > 0 and group is a positive multiple of 32 that divides k.
 int check_group(int64_t k, int64_t group);
 // check_group, and group is a power of two.

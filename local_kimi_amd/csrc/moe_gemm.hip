@@ -2571,6 +2571,20 @@ int lk_mxfp4_split_activations(const uint16_t* x, uint8_t* hi, uint8_t* lo, uint
   return split_launch(x, hi, lo, scales, rows, k, as_stream(stream));
 }
 
+// Largest batch whose expert-major block ends in the token-major W2 + combine
+// launch instead of the down GEMM and the combine kernel. Measured at the
+// Kimi-Linear shape (Zipf routing): 4 tokens 40.96 -> 39.34 us; 6, 8 and 12
+// tokens slower (46.96 -> 48.85, 52.32 -> 56.93, 62.88 -> 74.37 us), the
+// experts' W2 rows then being read once per route. LK_MOE_W2_ROWS_TOKENS
+// overrides (0: never).
+int64_t moe_w2_rows_tokens() {
+  static const int64_t v = [] {
+    const char* e = getenv("LK_MOE_W2_ROWS_TOKENS");
+    return e ? static_cast<int64_t>(atoi(e)) : int64_t{4};
+  }();
+  return v;
+}
+
 static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, const float* bias,
                               const uint8_t* w1_packed, const void* w1_scales,
                               const uint8_t* w3_packed, const void* w3_scales,
@@ -2658,11 +2672,21 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.wstride = i * h / 2;
   g.sstride = i * (h / group);
   const int64_t tb = max_tiles_for(entries, experts, tr);
+  // Few tokens (W4A16): the activations go to (token, route) rows and one
+  // token-major launch does W2, the combine and the shared expert, instead of
+  // the down GEMM and the combine kernel; it reads an expert's W2 once per
+  // route that uses it rather than once per call.
+  const bool w2_rows = !mx && tokens <= moe_w2_rows_tokens();
+  const Mode gu_mode = w2_rows ? Mode::GatherScatter : Mode::Gather;
   if (int rc = f8 ? stream_launch<kFmtMxF8, 2>(g, Mode::Gather, tb, mt, s, "moe gate/up gemm")
-               : mt ? stream_fmt<2>(mx, g, Mode::Gather, tb, mt, s, "moe gate/up gemm")
-                    : launch_fmt<2>(mx, g, Mode::Gather, tb, wide_cols_for(tb, i), s,
+               : mt ? stream_fmt<2>(mx, g, gu_mode, tb, mt, s, "moe gate/up gemm")
+                    : launch_fmt<2>(mx, g, gu_mode, tb, wide_cols_for(tb, i), s,
                                     "moe gate/up gemm"))
     return rc;
+  if (w2_rows)
+    return w2_combine_rows(act, expert_indices, top_k, experts - 1, weights, top_k, w2_packed,
+                           static_cast<const uint16_t*>(w2_scales), y, tokens, routes, experts,
+                           h, i, group, s);
   // down projection: sorted activation rows, outputs scattered to (token, route) rows
   if (f8) {
     if (int rc = split_launch(act, as.hi, as.lo, as.sc, entries, i, s)) return rc;

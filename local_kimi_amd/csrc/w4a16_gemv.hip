@@ -1270,6 +1270,20 @@ static int w2_combine_launch(const uint16_t* act, const int64_t* idx, int64_t id
   return check_launch("w2_combine");
 }
 
+}  // extern "C"
+
+namespace lk {
+int w2_combine_rows(const uint16_t* act, const int64_t* idx, int64_t idx_stride,
+                    int64_t shared_id, const float* cw, int64_t cw_stride, const uint8_t* w2p,
+                    const uint16_t* w2s, uint16_t* y, int64_t tokens, int64_t routes,
+                    int64_t experts, int64_t h, int64_t inter, int64_t group, hipStream_t s) {
+  return w2_combine_launch(act, idx, idx_stride, shared_id, cw, cw_stride, w2p, w2s, y, tokens,
+                           routes, experts, h, inter, group, s);
+}
+}  // namespace lk
+
+extern "C" {
+
 int lk_w4a16_w2_combine(const uint16_t* activated, const int64_t* expert_indices,
                         const float* combine_weights, const uint8_t* w2_packed,
                         const uint16_t* w2_scales, uint16_t* y, int64_t tokens, int64_t routes,

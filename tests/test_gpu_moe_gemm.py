@@ -198,8 +198,9 @@ def _moe_inputs(rng, e_routed, h, i, g, tokens, zipf=False):
     return x, logits, banks
 
 
-@pytest.mark.parametrize("tokens,g,zipf", [(2, 128, False), (5, 128, True), (37, 32, False),
-                                           (64, 128, True)])
+# up to 4 tokens the block ends in the token-major W2 + combine launch
+@pytest.mark.parametrize("tokens,g,zipf", [(2, 128, False), (3, 32, True), (4, 128, True),
+                                           (5, 128, True), (37, 32, False), (64, 128, True)])
 def test_moe_forward_matches_oracle_small_bank(rng, tokens, g, zipf):
     from local_kimi_amd.kernels import w4a16_moe_decode, w4a16_moe_forward
 
