@@ -45,6 +45,23 @@ LK_API const char* lk_last_error(void);
 /* ABI version of this library. */
 LK_API int lk_abi_version(void);
 
+/* Kernel-form selection for this process. No reference counterpart: the
+ * reference selects whole ops through its registry (KIMI_KERNELS), which this
+ * library's Python layer keeps; these knobs choose among this library's own
+ * forms of one op, so tests and measurements can run every form. Every knob
+ * starts at "auto" (the library's measured choice) and the library reads no
+ * environment variable. Knobs and choices:
+ *   "moe_gemm"           auto | lds | stream16 | stream64  (expert-major GEMM)
+ *   "moe_persist"        auto | off       (persistent 16-row expert GEMM)
+ *   "dense_gemm"         auto | lds       (dense GEMM / fused QKV from 16 rows)
+ *   "mxfp4_mfma"         auto | fp4 | bf16 (MXFP4 expert GEMM MFMA form)
+ *   "moe_fused_schedule" auto | off       (router + schedule in one launch)
+ * Process-wide; set it between calls, not while another thread launches.
+ * lk_get_path returns the current choice's index (0 = auto), -1 for an
+ * unknown knob. */
+LK_API int lk_set_path(const char* knob, const char* choice);
+LK_API int lk_get_path(const char* knob);
+
 /* ---- codec: engine/quant/w4a16.py:68-105 (quantise), :108-129 (dequantise) */
 
 /* weight bf16 [N,K] -> packed [N,K/2], scales bf16 [N,K/G]; bit-exact with
@@ -153,7 +170,14 @@ LK_API int lk_w4a16_moe_gateup(const uint16_t* x, const float* logits, const flo
  * Banks hold routed experts 0..E-2 and the shared expert at E-1.
  * Writes y bf16 [T,H], expert_indices int64 [T,top_k], weights fp32
  * [T,top_k] and the SwiGLU activations into activated bf16 [T,top_k+1,I]
- * (caller-owned workspace). */
+ * (caller-owned workspace of lk_w4a16_moe_decode_workspace() bytes).
+ * Route limit of this token-major path: R = top_k + 1 routes with either
+ * I == 1024 and R <= 16, or R <= 32 and R * (I/32 * 68 + 32) <= 65536; other
+ * shapes are rejected before anything is launched (the expert-major
+ * lk_w4a16_moe_forward has no such limit). The workspace query returns -1 for
+ * them. */
+LK_API int64_t lk_w4a16_moe_decode_workspace(int64_t tokens, int64_t experts, int64_t h,
+                                             int64_t i, int64_t top_k);
 LK_API int lk_w4a16_moe_decode(const uint16_t* x, const float* logits, const float* bias,
                         const uint8_t* w1_packed, const uint16_t* w1_scales,
                         const uint8_t* w3_packed, const uint16_t* w3_scales,

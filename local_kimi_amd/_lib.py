@@ -8,6 +8,7 @@ fallback: if the library is missing, every kernel call raises.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -63,6 +64,7 @@ SIGNATURES: dict[str, list] = {
 
 # name -> argument types of the size queries (they return int64, -1 on bad input)
 QUERIES: dict[str, list] = {
+    "lk_w4a16_moe_decode_workspace": [_I64, _I64, _I64, _I64, _I64],
     "lk_w4a16_grouped_gemm_workspace": [_I64, _I64, _I64],
     "lk_w4a16_moe_forward_workspace": [_I64, _I64, _I64, _I64, _I64],
     "lk_mxfp4_moe_forward_workspace": [_I64, _I64, _I64, _I64, _I64],
@@ -101,6 +103,10 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = ctypes.c_int
                 fn.argtypes = argtypes
+            lib.lk_set_path.restype = ctypes.c_int
+            lib.lk_set_path.argtypes = [ctypes.c_char_p, ctypes.c_char_p]
+            lib.lk_get_path.restype = ctypes.c_int
+            lib.lk_get_path.argtypes = [ctypes.c_char_p]
             for name, argtypes in QUERIES.items():
                 fn = getattr(lib, name)
                 fn.restype = ctypes.c_int64
@@ -133,6 +139,42 @@ def schedule_sizes(tokens: int, routes: int, experts: int) -> tuple[int, int]:
     return max_tiles.value, ws.value
 
 
+# kernel-form knobs of lk_set_path and their choices ("auto" first)
+PATH_KNOBS: dict[str, tuple[str, ...]] = {
+    "moe_gemm": ("auto", "lds", "stream16", "stream64"),
+    "moe_persist": ("auto", "off"),
+    "dense_gemm": ("auto", "lds"),
+    "mxfp4_mfma": ("auto", "fp4", "bf16"),
+    "moe_fused_schedule": ("auto", "off"),
+}
+
+
+def set_path(knob: str, choice: str) -> None:
+    """Force one of the library's kernel forms for this process (see lk_set_path)."""
+    lib = load()
+    if lib.lk_set_path(knob.encode(), choice.encode()) != 0:
+        raise ValueError(lib.lk_last_error().decode(errors="replace"))
+
+
+def get_path(knob: str) -> str:
+    index = load().lk_get_path(knob.encode())
+    if index < 0:
+        raise ValueError(f"unknown path knob {knob!r}")
+    return PATH_KNOBS[knob][index]
+
+
+@contextlib.contextmanager
+def forced_path(knob: str, choice: str):
+    """Run the body with one kernel form forced, then restore the previous choice."""
+    previous = get_path(knob)
+    set_path(knob, choice)
+    try:
+        yield
+    finally:
+        set_path(knob, previous)
+
+
 def exported_symbols() -> list[str]:
     """Entry points this binding expects the library to export."""
-    return ["lk_last_error", "lk_abi_version", *SIGNATURES, *QUERIES]
+    return ["lk_last_error", "lk_abi_version", "lk_set_path", "lk_get_path", *SIGNATURES,
+            *QUERIES]

@@ -21,6 +21,23 @@ void set_error(const char* fmt, ...);
 int fail_arg(const char* fmt, ...);
 int check_launch(const char* what);
 
+// Kernel-form selection of this process (lk_set_path). Every knob is 0
+// ("auto") unless a caller forces a form; the library reads no environment.
+enum Knob : int {
+  kKnobMoeGemm = 0,       // 0 auto, 1 lds, 2 stream16, 3 stream64
+  kKnobMoePersist,        // 0 auto, 1 off
+  kKnobDenseGemm,         // 0 auto, 1 lds
+  kKnobMxfp4Mfma,         // 0 auto, 1 fp4, 2 bf16
+  kKnobMoeFusedSchedule,  // 0 auto, 1 off
+  kKnobCount
+};
+int path_choice(Knob knob);
+
+// Whether the token-major W2 + combine launch (w2_combine_rows) takes this
+// shape: LK_OK, or LK_ERR_ARGUMENT with the reason set as the last error.
+int w2_rows_check(int64_t routes, int64_t h, int64_t inter);
+bool w2_rows_fits(int64_t routes, int64_t inter);
+
 // W2 for every (token, route) row of `act` [tokens, routes, inter] plus the
 // route-weighted combine and the shared expert (the last route; bank entry
 // shared_id when shared_id >= 0), one launch: the token-major W2 kernels of

@@ -1920,11 +1920,10 @@ MoeLayout moe_layout(int64_t entries, int64_t experts, int64_t act_cols, int64_t
 
 // Whether one block routes and schedules the batch (schedule_one_kernel with
 // routing): at most kFuseRouteTokens tokens, 256 routed experts (four per
-// lane) and kFuseThreads token-routes. LK_MOE_FUSED_SCHEDULE=0 takes the router and
-// schedule launches instead (the same tables; read per call).
+// lane) and kFuseThreads token-routes. The path knob moe_fused_schedule=off
+// takes the router and schedule launches instead (the same tables).
 bool route_schedule_fits(int64_t tokens, int64_t routed, int64_t top_k) {
-  const char* v = getenv("LK_MOE_FUSED_SCHEDULE");
-  if (v && strcmp(v, "0") == 0) return false;
+  if (path_choice(kKnobMoeFusedSchedule) == 1) return false;
   return routed >= 1 && routed <= 256 && top_k >= 1 && top_k <= 32 && top_k <= routed &&
          tokens <= kFuseRouteTokens && tokens * (top_k + 1) <= kFuseThreads;
 }
@@ -1959,9 +1958,8 @@ int schedule_launch(const RouteTable& rt, int64_t entries, char* ws, const Sched
   sc.tile_rows = tile_rows;
   // one block of 16 waves where one chunk of kSchedThreads would not cover
   // the table (otherwise the chunk kernel, at 8 waves, is the faster one launch)
-  const char* one = getenv("LK_MOE_FUSED_SCHEDULE");
   if (entries > kSchedThreads && entries <= kFuseThreads && rt.experts + 1 <= kFuseBuckets &&
-      !(one && strcmp(one, "0") == 0)) {
+      path_choice(kKnobMoeFusedSchedule) != 1) {
     schedule_one_kernel<false><<<1, kFuseThreads, 0, s>>>(rt, entries, sc, nullptr, nullptr, nullptr,
                                                           nullptr, 0, 0.f, 0);
     return check_launch("moe schedule");
@@ -2048,12 +2046,8 @@ void stream_one(const GemmArgs& g, unsigned blocks, size_t lds, hipStream_t s) {
   fn<<<blocks, kStWaves * kWave, lds, s>>>(g);
 }
 
-// LK_MOE_PERSIST=0 takes the per-tile streaming kernel for 16-row tiles (read
-// per call, like LK_MOE_GEMM).
-bool persist_disabled() {
-  const char* v = getenv("LK_MOE_PERSIST");
-  return v && strcmp(v, "0") == 0;
-}
+// moe_persist=off takes the per-tile streaming kernel for 16-row tiles.
+bool persist_disabled() { return path_choice(kKnobMoePersist) == 1; }
 
 template <int FMT, int MATS, int MT, bool WIDE>
 void stream_dispatch(const GemmArgs& g, Mode mode, unsigned blocks, size_t lds, hipStream_t s) {
@@ -2202,12 +2196,11 @@ bool wide_cols_for(int64_t tiles, int64_t n) { return tiles * ((n + 63) / 64) >=
 // streaming kernel with 64-row tiles (weights in a register ring, activations
 // in LDS passes) where it covers the format, else the LDS-staged GEMM. On the
 // fused QKV projection of 2048 tokens ([2048, 2304] x [2304, 3 x 4096]) the
-// streaming kernel takes 226 us, the LDS-staged GEMM 421 us. LK_DENSE_GEMM=lds
-// forces the LDS-staged GEMM (read per call).
+// streaming kernel takes 226 us, the LDS-staged GEMM 421 us. The path knob
+// dense_gemm=lds forces the LDS-staged GEMM.
 template <int FMT>
 int dense_launch(const GemmArgs& g, int64_t tiles, hipStream_t s, const char* what) {
-  const char* env = getenv("LK_DENSE_GEMM");
-  const bool lds = env && strcmp(env, "lds") == 0;
+  const bool lds = path_choice(kKnobDenseGemm) == 1;
   if (!lds && stream_fits(g.k, 4, g.group, FMT != kFmtW4A16))
     return stream_launch<FMT, 1>(g, Mode::Dense, tiles, 4, s, what);
   return gemm_launch<FMT, 1>(g, Mode::Dense, tiles, wide_cols_for(tiles * g.outputs, g.n), s, what);
@@ -2237,8 +2230,8 @@ int stream_fmt(bool mx, const GemmArgs& g, Mode mode, int64_t tiles, int mt, hip
 
 // Expert-major calls use the streaming kernel: 16-row tiles up to
 // kStreamSmallEntries token-routes (decode batches, few rows per expert),
-// 64-row tiles above (prefill). LK_MOE_GEMM=lds selects the LDS-staged
-// kernel instead, LK_MOE_GEMM=stream16|stream64 forces a tile height.
+// 64-row tiles above (prefill). The path knob moe_gemm=lds selects the
+// LDS-staged kernel instead, moe_gemm=stream16|stream64 forces a tile height.
 constexpr int64_t kStreamSmallEntries = 2048;
 
 // Which MFMA form the MXFP4 expert GEMMs take. The scaled fp4 MFMA (raw fp4
@@ -2246,21 +2239,22 @@ constexpr int64_t kStreamSmallEntries = 2048;
 // (782 vs 831 us for a 2048-token Kimi-Linear layer); on 16-row decode tiles
 // the GEMMs are weight-bandwidth bound and bf16 MFMA on decoded weights is
 // faster (175 vs 198 us at 64 tokens: no split launches, fewer registers).
-// LK_MXFP4_MFMA=fp4 or =bf16 forces one form for every tile height.
+// The path knob mxfp4_mfma=fp4 or =bf16 forces one form for every tile height.
 bool mxfp4_scaled_mfma(int mt) {
-  const char* env = getenv("LK_MXFP4_MFMA");
-  if (env && strcmp(env, "bf16") == 0) return false;
-  if (env && strcmp(env, "fp4") == 0) return true;
+  const int c = path_choice(kKnobMxfp4Mfma);
+  if (c == 2) return false;
+  if (c == 1) return true;
   return mt == 4;
 }
 
 // 16-row tiles -> 1, 64-row tiles -> 4, the LDS-staged kernel -> 0.
 int stream_tile_mt(int64_t entries) {
-  const char* env = getenv("LK_MOE_GEMM");
-  if (env && strcmp(env, "lds") == 0) return 0;
-  if (env && strcmp(env, "stream16") == 0) return 1;
-  if (env && strcmp(env, "stream64") == 0) return 4;
-  return entries <= kStreamSmallEntries ? 1 : 4;
+  switch (path_choice(kKnobMoeGemm)) {
+    case 1: return 0;
+    case 2: return 1;
+    case 3: return 4;
+    default: return entries <= kStreamSmallEntries ? 1 : 4;
+  }
 }
 
 // W4A16: a power-of-two group (multiple of 32) dividing k; MXFP4: 32.
@@ -2575,15 +2569,8 @@ int lk_mxfp4_split_activations(const uint16_t* x, uint8_t* hi, uint8_t* lo, uint
 // launch instead of the down GEMM and the combine kernel. Measured at the
 // Kimi-Linear shape (Zipf routing): 4 tokens 40.96 -> 39.34 us; 6, 8 and 12
 // tokens slower (46.96 -> 48.85, 52.32 -> 56.93, 62.88 -> 74.37 us), the
-// experts' W2 rows then being read once per route. LK_MOE_W2_ROWS_TOKENS
-// overrides (0: never).
-int64_t moe_w2_rows_tokens() {
-  static const int64_t v = [] {
-    const char* e = getenv("LK_MOE_W2_ROWS_TOKENS");
-    return e ? static_cast<int64_t>(atoi(e)) : int64_t{4};
-  }();
-  return v;
-}
+// experts' W2 rows then being read once per route.
+constexpr int64_t kW2RowsMaxTokens = 4;
 
 static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, const float* bias,
                               const uint8_t* w1_packed, const void* w1_scales,
@@ -2676,7 +2663,7 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   // token-major launch does W2, the combine and the shared expert, instead of
   // the down GEMM and the combine kernel; it reads an expert's W2 once per
   // route that uses it rather than once per call.
-  const bool w2_rows = !mx && tokens <= moe_w2_rows_tokens();
+  const bool w2_rows = !mx && tokens <= kW2RowsMaxTokens && w2_rows_fits(routes, i);
   const Mode gu_mode = w2_rows ? Mode::GatherScatter : Mode::Gather;
   if (int rc = f8 ? stream_launch<kFmtMxF8, 2>(g, Mode::Gather, tb, mt, s, "moe gate/up gemm")
                : mt ? stream_fmt<2>(mx, g, gu_mode, tb, mt, s, "moe gate/up gemm")

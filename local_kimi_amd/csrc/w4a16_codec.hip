@@ -9,6 +9,9 @@
 
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
+
+#include <atomic>
 
 #include "lk_common.hpp"
 
@@ -40,6 +43,27 @@ int check_launch(const char* what) {
   g_error[0] = '\0';
   return LK_OK;
 }
+
+namespace {
+
+struct KnobSpec {
+  const char* name;
+  const char* choices[4];  // index = value; choice 0 is "auto"
+};
+
+constexpr KnobSpec kKnobs[kKnobCount] = {
+    {"moe_gemm", {"auto", "lds", "stream16", "stream64"}},
+    {"moe_persist", {"auto", "off", nullptr, nullptr}},
+    {"dense_gemm", {"auto", "lds", nullptr, nullptr}},
+    {"mxfp4_mfma", {"auto", "fp4", "bf16", nullptr}},
+    {"moe_fused_schedule", {"auto", "off", nullptr, nullptr}},
+};
+
+std::atomic<int> g_knobs[kKnobCount];  // zero-initialised: "auto"
+
+}  // namespace
+
+int path_choice(Knob knob) { return g_knobs[knob].load(std::memory_order_relaxed); }
 
 namespace {
 
@@ -237,7 +261,30 @@ extern "C" {
 
 const char* lk_last_error(void) { return lk::g_error; }
 
-int lk_abi_version(void) { return 1; }
+int lk_abi_version(void) { return 2; }
+
+int lk_set_path(const char* knob, const char* choice) {
+  LK_REQUIRE(knob && choice, "null knob or choice");
+  for (int k = 0; k < lk::kKnobCount; ++k) {
+    const lk::KnobSpec& spec = lk::kKnobs[k];
+    if (strcmp(knob, spec.name) != 0) continue;
+    for (int v = 0; v < 4 && spec.choices[v]; ++v) {
+      if (strcmp(choice, spec.choices[v]) == 0) {
+        lk::g_knobs[k].store(v, std::memory_order_relaxed);
+        return LK_OK;
+      }
+    }
+    return lk::fail_arg("unknown choice '%s' for path knob '%s'", choice, knob);
+  }
+  return lk::fail_arg("unknown path knob '%s'", knob);
+}
+
+int lk_get_path(const char* knob) {
+  if (!knob) return -1;
+  for (int k = 0; k < lk::kKnobCount; ++k)
+    if (strcmp(knob, lk::kKnobs[k].name) == 0) return lk::path_choice(static_cast<lk::Knob>(k));
+  return -1;
+}
 
 int lk_w4a16_quantise(const uint16_t* weight, uint8_t* packed, uint16_t* scales, int64_t n,
                       int64_t k, int64_t group_size, void* stream) {

@@ -769,54 +769,6 @@ w2_combine_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// W2 + combine, K-split form for routes <= 16: wave r of the block handles
-// route r for the block's 8*NR rows of H; lane (rg, ph) owns chunks ph + 8*i
-// (i < CI) of the route's activations and rows rg + 8*j. Route sums go through
-// LDS once and are combined by the block in route order (bit-reproducible):
-// bf16 route outputs, fp32 weighted sum of routes 0..R-2, bf16, plus the last
-// route (the shared expert) with weight 1.
-
-template <int NR, int CI>
-__global__ void __launch_bounds__(1024)
-w2_ksplit_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ idx,
-                 int64_t idx_stride, int64_t shared_id, const float* __restrict__ cw,
-                 int64_t cw_stride, const uint8_t* __restrict__ w2p,
-                 const uint16_t* __restrict__ w2s, uint16_t* __restrict__ y, int routes,
-                 int64_t experts, int64_t h, int64_t inter, int64_t group) {
-  __shared__ float red[kMaxKWaves][NR * 8];
-  const int r = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // this wave's route
-  const int64_t t = blockIdx.y;
-  const Shape sh = make_shape(inter, group);
-  KSplit<1, NR, 1, CI> ks;
-  ks.load_x(act + (t * routes + r) * inter, inter, 1, /*wave=*/0, /*kw=*/1, sh.cpr);
-  const int64_t e_raw = (shared_id >= 0 && r == routes - 1) ? shared_id : idx[t * idx_stride + r];
-  const bool valid = e_raw >= 0 && e_raw < experts;
-  const int64_t e = valid ? e_raw : 0;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 8 * NR;
-  const Rows<NR> rows(row0, h);
-  const uint8_t* const wp[1] = {w2p + e * h * sh.bytes_row};
-  const uint16_t* const ws[1] = {w2s + e * h * sh.spr};
-  ks.load_w(wp, ws, rows, sh, 0, 1);
-  ks.compute(rows, 1, 0, 1, sh.cpr);
-  ks.reduce_to_lds(red, r);
-  const int o = threadIdx.x;
-  if (o < NR * 8) {
-    const int64_t row = row0 + (o & 7) + 8 * (o >> 3);
-    if (row < h) {
-      float routed = 0.f;
-      for (int q = 0; q + 1 < routes; ++q) {
-        const int64_t eq = idx[t * idx_stride + q];
-        const float eo = (eq >= 0 && eq < experts) ? round_bf16(red[q][o]) : 0.f;
-        routed += eo * cw[t * cw_stride + q];
-      }
-      const int64_t el = (shared_id >= 0) ? shared_id : idx[t * idx_stride + routes - 1];
-      const float last = (el >= 0 && el < experts) ? round_bf16(red[routes - 1][o]) : 0.f;
-      y[t * h + row] = f32_to_bf16(round_bf16(routed) + last);
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // W2 + combine for reduction width inter = 32 chunks of 32, one block per CU:
 // blockIdx.x covers rows row0 .. row0 + rb - 1 of H (the host picks
 // rb = H / CUs rounded up; with 8-row blocks, 288 for H = 2304, some CUs run
@@ -936,35 +888,9 @@ w2_route_kernel(const uint16_t* __restrict__ act, const int64_t* __restrict__ id
 // ---------------------------------------------------------------------------
 // host-side dispatch
 
-int waves_per_block() {
-  static int w = [] {
-    const char* v = getenv("LK_GEMV_WAVES");
-    int n = v ? atoi(v) : 1;
-    return (n == 1 || n == 2 || n == 4) ? n : 1;
-  }();
-  return w;
-}
-
-// The route-per-wave W2 variant measured slower than the LDS-staged kernel at
-// the decode shape (11.5 / 9.3 us vs 8.8 us at 1 / 2 rows per lane); it stays
-// selectable for experiments with LK_W2_KSPLIT=1.
-bool w2_ksplit_enabled() {
-  static bool on = [] {
-    const char* v = getenv("LK_W2_KSPLIT");
-    return v && atoi(v) == 1;
-  }();
-  return on;
-}
-
-// One wave per route with one block per CU is the batch-1 W2 form; LK_W2_ROUTE=0
-// selects the LDS-staged 8-row kernel instead.
-bool w2_route_enabled() {
-  static bool on = [] {
-    const char* v = getenv("LK_W2_ROUTE");
-    return !(v && atoi(v) == 0);
-  }();
-  return on;
-}
+// The LDS-staged GEMVs (reductions wider than 8192) run one wave of 8 rows per
+// block; 2 and 4 waves measured no faster.
+constexpr int kGemvWaves = 1;
 
 int device_cus() {
   static int cache[64] = {0};
@@ -978,12 +904,20 @@ int device_cus() {
   return cus;
 }
 
-int w2_rows_per_lane() {
-  static int nr = [] {
-    const char* v = getenv("LK_W2_NR");
-    return (v && atoi(v) == 2) ? 2 : 1;
-  }();
-  return nr;
+// The token-major W2 + combine kernels and the shapes each takes: the
+// route-per-wave kernel for reduction width 1024 (32 chunks) and up to 16
+// routes; the LDS-staged kernel for up to 8 * kW2Waves routes whose staged
+// activations and route outputs fit one block's 64 KiB of LDS.
+enum W2Form { kW2None = 0, kW2Route, kW2Lds };
+
+int w2_rows_form(int64_t routes, int64_t inter) {
+  if (routes <= 0 || inter <= 0 || inter % 32) return kW2None;
+  const int64_t cpr = inter / 32;
+  if (cpr == kW2RouteCpr && routes <= kMaxKWaves) return kW2Route;
+  const int64_t lds = routes * cpr * static_cast<int64_t>(4 * sizeof(uint4) + sizeof(float)) +
+                      routes * 8 * static_cast<int64_t>(sizeof(float));
+  if (routes <= 8 * kW2Waves && lds <= static_cast<int64_t>(64 * 1024)) return kW2Lds;
+  return kW2None;
 }
 
 int pick_iters(int cpr) {
@@ -1013,35 +947,22 @@ constexpr size_t kMaxLds = 64 * 1024;
 // ---------------------------------------------------------------------------
 // Router logits (engine/klinear/router.py:50-51): logits[t, e] =
 // sum_k fp32(x[t, k]) * fp32(w[e, k]) for bf16 x and router weight w (each
-// product is exact in fp32). One wave per (token, expert row): lane l takes
-// the 16-byte chunks l, l + 64, ... of the row (every load issued before the
-// first FMA), sums them in order, then the wave reduces in a fixed order (DPP
-// within 8 lanes, then the 8 group sums in lane order), so reruns are
-// bit-identical.
+// product is exact in fp32). One wave per (expert row, tile of up to
+// kLogitTokens tokens): lane l holds the 16-byte chunks l, l + 64, ... of the
+// expert's row (loaded once for the tile), and for each token of the tile
+// loads the same chunks of x, sums them in chunk order, then the wave reduces
+// in a fixed order (DPP within 8 lanes, then the 8 group sums in lane order).
+// Every output therefore has the same summation order whatever the batch
+// size, so a token's logits (and its routing) do not depend on the batch, and
+// reruns are bit-identical.
 constexpr int kLogitWaves = 4;
-constexpr int kLogitIters = 8;  // chunks per lane: h <= 64 * 8 * 8 = 4096
+constexpr int kLogitIters = 8;   // chunks per lane: h <= 64 * 8 * 8 = 4096
+constexpr int kLogitTokens = 16;  // tokens per wave (the weight row is reused)
 
-__global__ void __launch_bounds__(kLogitWaves * 64)
-router_logits_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                     float* __restrict__ logits, int64_t experts, int64_t h) {
-  const int wave = static_cast<int>(threadIdx.x) / kWave;
-  const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
-  const int64_t e = static_cast<int64_t>(blockIdx.x) * kLogitWaves + wave;
-  const int64_t t = blockIdx.y;
-  if (e >= experts) return;  // wave-uniform
-  const int64_t chunks = h / 8;
-  const uint4* xr = reinterpret_cast<const uint4*>(x + t * h);
-  const uint4* wr = reinterpret_cast<const uint4*>(w + e * h);
-  uint4 xv[kLogitIters], wv[kLogitIters];
-#pragma unroll
-  for (int i = 0; i < kLogitIters; ++i) {
-    const int64_t c = lane + kWave * i;
-    const int64_t cc = c < chunks ? c : 0;
-    xv[i] = xr[cc];
-    wv[i] = wr[cc];
-  }
+__device__ inline float logit_dot(const uint4 (&xv)[kLogitIters], const uint4 (&wv)[kLogitIters],
+                                  int lane, int64_t chunks) {
   // a chunk past the row keeps acc (a select, not a branch, so the loads
-  // above stay batched)
+  // stay batched)
   float acc = 0.f;
 #pragma unroll
   for (int i = 0; i < kLogitIters; ++i) {
@@ -1061,7 +982,41 @@ router_logits_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict_
 #pragma unroll
   for (int gidx = 0; gidx < 8; ++gidx)
     total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), gidx * 8));
-  if (lane == 0) logits[t * experts + e] = total;
+  return total;
+}
+
+__global__ void __launch_bounds__(kLogitWaves * 64)
+router_logits_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                     float* __restrict__ logits, int64_t tokens, int64_t experts, int64_t h) {
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * kLogitWaves + wave;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kLogitTokens;
+  if (e >= experts) return;  // wave-uniform
+  const int64_t chunks = h / 8;
+  const int nt = static_cast<int>(min<int64_t>(kLogitTokens, tokens - t0));
+  const uint4* wr = reinterpret_cast<const uint4*>(w + e * h);
+  uint4 wv[kLogitIters], xv[kLogitIters];
+  const uint4* xr = reinterpret_cast<const uint4*>(x + t0 * h);
+#pragma unroll
+  for (int i = 0; i < kLogitIters; ++i) {
+    const int64_t c = lane + kWave * i;
+    const int64_t cc = c < chunks ? c : 0;
+    xv[i] = xr[cc];
+    wv[i] = wr[cc];
+  }
+  for (int t = 0; t < nt; ++t) {
+    const float total = logit_dot(xv, wv, lane, chunks);
+    if (t + 1 < nt) {  // the next token's chunks (wave-uniform)
+      const uint4* xn = reinterpret_cast<const uint4*>(x + (t0 + t + 1) * h);
+#pragma unroll
+      for (int i = 0; i < kLogitIters; ++i) {
+        const int64_t c = lane + kWave * i;
+        xv[i] = xn[c < chunks ? c : 0];
+      }
+    }
+    if (lane == 0) logits[(t0 + t) * experts + e] = total;
+  }
 }
 
 }  // namespace
@@ -1080,12 +1035,15 @@ int lk_router_logits(const uint16_t* x, const uint16_t* w, float* logits, int64_
   LK_REQUIRE(h % 8 == 0 && h <= 64 * 8 * kLogitIters,
              "router logits need hidden %% 8 == 0 and hidden <= %d, got %lld", 64 * 8 * kLogitIters,
              (long long)h);
-  LK_REQUIRE(tokens <= 65535 && experts <= 4 * 65535LL, "too many tokens or experts for one call");
+  const int64_t token_tiles = (tokens + kLogitTokens - 1) / kLogitTokens;
+  LK_REQUIRE(token_tiles <= 65535 && experts <= 4 * 65535LL,
+             "too many tokens or experts for one call");
   if (tokens == 0) return LK_OK;
   LK_REQUIRE(x != nullptr, "null activation pointer");
   dim3 grid(static_cast<unsigned>((experts + kLogitWaves - 1) / kLogitWaves),
-            static_cast<unsigned>(tokens));
-  router_logits_kernel<<<grid, kLogitWaves * kWave, 0, as_stream(stream)>>>(x, w, logits, experts, h);
+            static_cast<unsigned>(token_tiles));
+  router_logits_kernel<<<grid, kLogitWaves * kWave, 0, as_stream(stream)>>>(x, w, logits, tokens,
+                                                                            experts, h);
   return check_launch("lk_router_logits");
 }
 
@@ -1120,7 +1078,7 @@ int lk_w4a16_dense(const uint16_t* x, const uint8_t* packed, const uint16_t* sca
   int nt2 = m >= 8 ? 8 : m >= 4 ? 4 : m >= 2 ? 2 : 1;
   while (nt2 > 1 && stage_bytes(nt2, cpr) > kMaxLds) nt2 /= 2;
   LK_REQUIRE(stage_bytes(nt2, cpr) <= kMaxLds, "reduction width %lld too large", (long long)k);
-  const int nw = waves_per_block();
+  const int nw = kGemvWaves;
   dim3 grid(static_cast<unsigned>((n + nw * 8 - 1) / (nw * 8)),
             static_cast<unsigned>((m + nt2 - 1) / nt2));
   const size_t lds = stage_bytes(nt2, cpr);
@@ -1170,7 +1128,7 @@ static int grouped_common(const uint16_t* x, const int64_t* idx, const uint8_t* 
   }
   const int cpr = static_cast<int>(k / 32);
   LK_REQUIRE(stage_bytes(1, cpr) <= kMaxLds, "reduction width %lld too large", (long long)k);
-  const int nw = waves_per_block();
+  const int nw = kGemvWaves;
   const int64_t rows_per_block = nw * 8;
   dim3 grid(static_cast<unsigned>((n + rows_per_block - 1) / rows_per_block),
             static_cast<unsigned>(pairs));
@@ -1207,54 +1165,30 @@ static int w2_combine_launch(const uint16_t* act, const int64_t* idx, int64_t id
                              const uint8_t* w2p, const uint16_t* w2s, uint16_t* y,
                              int64_t tokens, int64_t routes, int64_t experts, int64_t h,
                              int64_t inter, int64_t group, hipStream_t s) {
-  const int cpr = static_cast<int>(inter / 32);
-  const size_t lds = stage_bytes(static_cast<int>(routes), cpr) + routes * 8 * sizeof(float);
-  LK_REQUIRE(lds <= kMaxLds, "routes x reduction width too large for one block (%lld x %lld)",
-             (long long)routes, (long long)inter);
-  LK_REQUIRE(routes <= 8 * kW2Waves, "at most %d routes per token", 8 * kW2Waves);
+  const int form = w2_rows_form(routes, inter);
+  if (form == kW2None) return w2_rows_check(routes, h, inter);
   LK_REQUIRE(tokens <= 65535, "at most 65535 tokens per call");
-  const int ci = (cpr + 7) / 8;
-  if (w2_ksplit_enabled() && routes <= kMaxKWaves && ci <= 4) {
-    const int nr = w2_rows_per_lane();
-    dim3 g2(static_cast<unsigned>((h + 8 * nr - 1) / (8 * nr)), static_cast<unsigned>(tokens));
-    const int threads = static_cast<int>(routes) * kWave;
-    const int rr = static_cast<int>(routes);
-#define LK_W2_KS(NRV, CIV)                                                                   \
-  w2_ksplit_kernel<NRV, CIV><<<g2, threads, 0, s>>>(act, idx, idx_stride, shared_id, cw,    \
-                                                    cw_stride, w2p, w2s, y, rr, experts, h, \
-                                                    inter, group)
-    if (nr == 1) {
-      if (ci == 1) LK_W2_KS(1, 1); else if (ci == 2) LK_W2_KS(1, 2); else LK_W2_KS(1, 4);
-    } else {
-      if (ci == 1) LK_W2_KS(2, 1); else if (ci == 2) LK_W2_KS(2, 2); else LK_W2_KS(2, 4);
-    }
-#undef LK_W2_KS
-    return check_launch("w2_combine");
-  }
-  const int cus = device_cus();
-  if (w2_route_enabled() && cpr == kW2RouteCpr && routes <= kMaxKWaves && cus > 0 &&
-      h <= 16LL * cus) {
-    const int rb = static_cast<int>((h + cus - 1) / cus);  // 1 .. 16
+  const int cpr = static_cast<int>(inter / 32);
+  if (form == kW2Route) {
+    // rows of H per block: one block per CU where 16 rows per block cover H
+    const int cus = device_cus();
+    const int64_t per_cu = cus > 0 ? (h + cus - 1) / cus : int64_t{16};
+    const int rb = static_cast<int>(per_cu < 16 ? per_cu : 16);
     const int jn = (rb + 1) / 2;
     dim3 g3(static_cast<unsigned>((h + rb - 1) / rb), static_cast<unsigned>(tokens));
     const int rr = static_cast<int>(routes);
-#define LK_W2_RT(JV, WV, RV, THREADS)                                                          \
-  w2_route_kernel<JV, WV, RV><<<g3, THREADS, 0, s>>>(act, idx, idx_stride, shared_id, cw,     \
-                                                     cw_stride, w2p, w2s, y, rr, experts, h, \
-                                                     inter, group, rb)
-#define LK_W2_RT_J(WV, RV, THREADS)          \
-  do {                                      \
-    if (jn <= 1) LK_W2_RT(1, WV, RV, THREADS);      \
-    else if (jn <= 2) LK_W2_RT(2, WV, RV, THREADS); \
-    else if (jn <= 3) LK_W2_RT(3, WV, RV, THREADS); \
-    else if (jn <= 5) LK_W2_RT(5, WV, RV, THREADS); \
-    else LK_W2_RT(8, WV, RV, THREADS);              \
-  } while (0)
-    LK_W2_RT_J(kMaxKWaves, 1, rr * kWave);  // one wave per route
-#undef LK_W2_RT_J
+#define LK_W2_RT(JV)                                                                        \
+  w2_route_kernel<JV, kMaxKWaves, 1><<<g3, rr * kWave, 0, s>>>(                            \
+      act, idx, idx_stride, shared_id, cw, cw_stride, w2p, w2s, y, rr, experts, h, inter, group, rb)
+    if (jn <= 1) LK_W2_RT(1);
+    else if (jn <= 2) LK_W2_RT(2);
+    else if (jn <= 3) LK_W2_RT(3);
+    else if (jn <= 5) LK_W2_RT(5);
+    else LK_W2_RT(8);
 #undef LK_W2_RT
     return check_launch("w2_combine");
   }
+  const size_t lds = stage_bytes(static_cast<int>(routes), cpr) + routes * 8 * sizeof(float);
   dim3 grid(static_cast<unsigned>((h + 7) / 8), static_cast<unsigned>(tokens));
   const int iters = pick_iters(cpr);
   const int r = static_cast<int>(routes);
@@ -1273,6 +1207,18 @@ static int w2_combine_launch(const uint16_t* act, const int64_t* idx, int64_t id
 }  // extern "C"
 
 namespace lk {
+int w2_rows_check(int64_t routes, int64_t h, int64_t inter) {
+  LK_REQUIRE(h > 0, "invalid hidden size %lld", (long long)h);
+  LK_REQUIRE(w2_rows_form(routes, inter) != kW2None,
+             "token-major W2 + combine takes up to %d routes at intermediate size 1024, or up "
+             "to %d routes with routes x (intermediate / 32 x 68 + 32) <= 65536 bytes; got %lld "
+             "routes at intermediate size %lld",
+             kMaxKWaves, 8 * kW2Waves, (long long)routes, (long long)inter);
+  return LK_OK;
+}
+
+bool w2_rows_fits(int64_t routes, int64_t inter) { return w2_rows_form(routes, inter) != kW2None; }
+
 int w2_combine_rows(const uint16_t* act, const int64_t* idx, int64_t idx_stride,
                     int64_t shared_id, const float* cw, int64_t cw_stride, const uint8_t* w2p,
                     const uint16_t* w2s, uint16_t* y, int64_t tokens, int64_t routes,
@@ -1351,7 +1297,7 @@ static int moe_gateup_launch(const uint16_t* x, const float* logits, const float
   }
   const int cpr = static_cast<int>(h / 32);
   LK_REQUIRE(stage_bytes(1, cpr) <= kMaxLds, "hidden size %lld too large", (long long)h);
-  const int nw = waves_per_block();
+  const int nw = kGemvWaves;
   const int64_t rows_per_block = nw * 8;
   dim3 grid(static_cast<unsigned>((i + rows_per_block - 1) / rows_per_block),
             static_cast<unsigned>(tokens * routes));
@@ -1405,6 +1351,15 @@ int lk_w4a16_moe_gateup(const uint16_t* x, const float* logits, const float* bia
                            routed_scaling_factor, renormalize, group_size, as_stream(stream));
 }
 
+int64_t lk_w4a16_moe_decode_workspace(int64_t tokens, int64_t experts, int64_t h, int64_t i,
+                                      int64_t top_k) {
+  if (tokens < 0 || experts < 2 || h <= 0 || i <= 0 || top_k <= 0 || top_k > 32 ||
+      top_k > experts - 1)
+    return -1;
+  if (w2_rows_form(top_k + 1, i) == kW2None) return -1;
+  return tokens * (top_k + 1) * i * static_cast<int64_t>(sizeof(uint16_t));
+}
+
 int lk_w4a16_moe_decode(const uint16_t* x, const float* logits, const float* bias,
                         const uint8_t* w1_packed, const uint16_t* w1_scales,
                         const uint8_t* w3_packed, const uint16_t* w3_scales,
@@ -1417,6 +1372,8 @@ int lk_w4a16_moe_decode(const uint16_t* x, const float* logits, const float* bia
                          activated, tokens, experts, h, i, top_k, group_size))
     return rc;
   LK_REQUIRE(w2_packed && w2_scales && y, "null pointer argument");
+  // checked before any launch: the second stage must take this shape
+  if (int rc = w2_rows_check(top_k + 1, h, i)) return rc;
   if (tokens == 0) return LK_OK;
   LK_REQUIRE(x && logits, "null pointer argument");
   hipStream_t s = as_stream(stream);

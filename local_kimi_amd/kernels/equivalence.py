@@ -94,7 +94,7 @@ def check_equivalence(op: str, make_inputs: Callable[..., object], *, rtol: floa
         n for n in registry.variants(op) if n != reference.name)
     reports: list[EquivalenceReport] = []
     for name in names:
-        cand = registry._variant_of(op, name)
+        cand = registry.get_variant(op, name)
         skip = ""
         if cand.requires_cuda and not torch.cuda.is_available():
             skip = "CUDA is not available"

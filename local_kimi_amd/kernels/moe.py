@@ -114,26 +114,28 @@ def moe_router(logits: torch.Tensor, bias: torch.Tensor | None, top_k: int, *,
     return idx, w
 
 
-ROUTER_LOGITS_MAX_TOKENS = 64  # beyond: a GEMM (torch) reads the router weight fewer times
-
-
 def router_logits(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """``fp32(hidden) @ fp32(weight).T`` -> float32 ``[T, E]`` (router.py:50-51).
 
     bf16 ``hidden [T, H]`` and bf16 ``weight [E, H]`` with ``H % 8 == 0`` and
-    ``H <= 4096`` and up to ``ROUTER_LOGITS_MAX_TOKENS`` tokens: one HIP launch
-    (exact products, fp32 sums in a fixed order). Otherwise torch's fp32 GEMM
-    on the same device, as the reference computes it.
+    ``H <= 4096``, on the GPU: one HIP launch for any token count. Products
+    are exact in fp32 and every logit is summed in the same fixed order
+    whatever the batch size, so a token's logits, and therefore its expert
+    selection, do not depend on how many tokens share the call.
     """
     if hidden.ndim != 2 or weight.ndim != 2 or hidden.shape[1] != weight.shape[1]:
         raise ValueError("router logits need hidden [T, H] and weight [E, H]")
+    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("router logits need BF16 hidden states and a BF16 router weight")
     if hidden.device != weight.device:
         raise ValueError("router inputs must share one device")
+    if hidden.device.type != "cuda":
+        raise ValueError("the HIP router logits require CUDA")
     tokens, h = hidden.shape
     experts = weight.shape[0]
-    if (hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or h % 8 or h > 4096
-            or tokens > ROUTER_LOGITS_MAX_TOKENS or hidden.device.type != "cuda"):
-        return torch.nn.functional.linear(hidden.float(), weight.float(), None)
+    if h % 8 or h > 4096 or experts == 0:
+        raise ValueError(f"router logits need 0 < experts and hidden % 8 == 0, hidden <= 4096; "
+                         f"got hidden {h}, experts {experts}")
     out = torch.empty((tokens, experts), dtype=torch.float32, device=hidden.device)
     if tokens == 0:
         return out
@@ -191,12 +193,25 @@ def w4a16_moe_block(hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Tens
     (:func:`w4a16_moe_forward`).
     Returns ``(y bf16 [T, H], expert_indices int64 [T, k], weights float32 [T, k])``.
     """
-    if hidden.ndim == 2 and hidden.shape[0] >= MOE_EXPERT_MAJOR_MIN_TOKENS and \
-            w1_packed.ndim == 3 and w1_packed.shape[0] <= MOE_EXPERT_MAJOR_MAX_EXPERTS:
+    expert_major_fits = hidden.ndim == 2 and w1_packed.ndim == 3 and \
+        w1_packed.shape[0] <= MOE_EXPERT_MAJOR_MAX_EXPERTS
+    if expert_major_fits and (hidden.shape[0] >= MOE_EXPERT_MAJOR_MIN_TOKENS or
+                              not decode_supported(w1_packed, top_k)):
         return w4a16_moe_forward(hidden, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
                                  w2_packed, w2_scales, top_k, routed_scaling_factor, renormalize)
     return w4a16_moe_decode(hidden, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
                             w2_packed, w2_scales, top_k, routed_scaling_factor, renormalize)
+
+
+def decode_supported(w1_packed: torch.Tensor, top_k: int) -> bool:
+    """Whether the token-major decode path takes ``top_k + 1`` routes at this bank's
+    intermediate size (its W2 + combine launch has a route limit; the
+    expert-major path has none)."""
+    if w1_packed.ndim != 3:
+        return False
+    experts, inter, packed_h = w1_packed.shape
+    return int(_lib.load().lk_w4a16_moe_decode_workspace(1, experts, packed_h * 2, inter,
+                                                          top_k)) >= 0
 
 
 def w4a16_moe_forward(hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor | None,
@@ -229,9 +244,18 @@ def w4a16_moe_forward(hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Te
 def w4a16_moe_decode(hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor | None,
                      w1_packed, w1_scales, w3_packed, w3_scales, w2_packed, w2_scales, top_k: int,
                      routed_scaling_factor: float = 1.0, renormalize: bool = True):
-    """The token-major block in two launches (any token count; fastest at one)."""
+    """The token-major block in two launches (any token count; fastest at one).
+
+    Its W2 + combine launch takes ``top_k + 1`` routes with either intermediate
+    size 1024 and at most 16 routes, or at most 32 routes whose staged
+    activations fit 64 KiB (``routes * (I / 32 * 68 + 32)`` bytes); other
+    shapes raise ValueError (``w4a16_moe_block`` sends them expert-major).
+    """
     tokens, e_total, h, inter, g = _validate_block(hidden, logits, bias, w1_packed, w1_scales,
                                                    w3_packed, w3_scales, w2_packed, w2_scales, top_k)
+    if _lib.load().lk_w4a16_moe_decode_workspace(tokens, e_total, h, inter, top_k) < 0:
+        raise ValueError(f"the token-major decode path does not take top_k={top_k} at "
+                         f"intermediate size {inter}; use w4a16_moe_forward")
     dev = hidden.device
     y = torch.empty((tokens, h), dtype=torch.bfloat16, device=dev)
     idx = torch.empty((tokens, top_k), dtype=torch.long, device=dev)

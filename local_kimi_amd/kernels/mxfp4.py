@@ -13,7 +13,7 @@ last). At prefill sizes its expert GEMMs run on the gfx950 scaled fp4 MFMA:
 raw E2M1 weights with their E8M0 exponents, activations split into fp8 hi +
 lo (:func:`split_activations_fp8`) so the product keeps bf16 activation
 precision; decode sizes (bandwidth bound) use bf16 MFMA on decoded weights
-(``LK_MXFP4_MFMA=fp4|bf16`` forces one form).
+(the path knob ``mxfp4_mfma=fp4|bf16`` forces one form).
 ``mxfp4_expert_mlp`` is the K3 packed expert with SiTU
 (engine/kernels/moe_grouped.py:163-194).
 """

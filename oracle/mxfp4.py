@@ -116,14 +116,13 @@ def grouped(x_bits, expert_indices, packed_bank, scale_bank) -> np.ndarray:
     t_count, r_count = idx.shape
     n = packed_bank.shape[1]
     out = np.empty((t_count, r_count, n), dtype=np.uint16)
-    cache: dict[int, np.ndarray] = {}
-    for t in range(t_count):
-        for r in range(r_count):
-            e = int(idx[t, r])
-            if e not in cache:
-                cache[e] = bf16_bits_to_f32(f32_to_bf16_bits(dequantize(packed_bank[e], scale_bank[e])))
-            acc = bf16_bits_to_f32(x[t:t + 1]).astype(np.float64) @ cache[e].astype(np.float64).T
-            out[t, r] = f32_to_bf16_bits(acc.astype(np.float32))[0]
+    # each output row is its own float64 dot product; rows that share an
+    # expert are evaluated together (one decode of the expert per call)
+    for e in np.unique(idx):
+        tok, slot = np.nonzero(idx == e)
+        w = bf16_bits_to_f32(f32_to_bf16_bits(dequantize(packed_bank[int(e)], scale_bank[int(e)])))
+        acc = bf16_bits_to_f32(x[tok]).astype(np.float64) @ w.astype(np.float64).T
+        out[tok, slot] = f32_to_bf16_bits(acc.astype(np.float32))
     return out
 
 

@@ -112,13 +112,12 @@ def grouped(x_bits: np.ndarray, expert_indices: np.ndarray, packed: np.ndarray,
     t_count, r_count = idx.shape
     n = packed.shape[1]
     out = np.empty((t_count, r_count, n), dtype=np.uint16)
-    cache: dict[int, np.ndarray] = {}
-    for t in range(t_count):
-        for r in range(r_count):
-            e = int(idx[t, r])
-            if e not in cache:
-                cache[e] = bf16_bits_to_f32(dequantise(packed[e], scales_bits[e], group_size))
-            out[t, r] = _matmul_bf16_out(x[t:t + 1], cache[e])[0]
+    # each output row is its own float64 dot product; rows that share an
+    # expert are evaluated together (one decode of the expert per call)
+    for e in np.unique(idx):
+        tok, slot = np.nonzero(idx == e)
+        w = bf16_bits_to_f32(dequantise(packed[int(e)], scales_bits[int(e)], group_size))
+        out[tok, slot] = _matmul_bf16_out(x[tok], w)
     return out
 
 

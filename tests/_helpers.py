@@ -47,3 +47,37 @@ def random_bf16_bits(rng: np.random.Generator, shape, std: float = 1.0) -> np.nd
     from oracle.bf16 import f32_to_bf16_bits
 
     return f32_to_bf16_bits(rng.normal(0, std, shape).astype(np.float32))
+
+
+def designed_counts(tokens: int, experts: int, top_k: int) -> np.ndarray:
+    """Per-expert route counts for a prefill-sized batch whose expert tiles take
+    every shape: unused, a handful of rows, exactly one 64-row tile, a full
+    tile plus a tail of 1..16 rows (the 16-row path) or 17..63 rows (a partial
+    64-row tile), and several hundred rows with assorted tails."""
+    head = [1, 16, 17, 0, 64, 65, 80, 81, 127, 128]
+    assert experts > len(head)
+    rest = experts - len(head)
+    counts = np.array(head + [550 + 13 * j for j in range(rest)], dtype=np.int64)
+    counts[-1] += tokens * top_k - int(counts.sum())
+    assert counts.min() >= 0 and counts.max() <= tokens and counts.sum() == tokens * top_k
+    return counts
+
+
+def designed_router_logits(rng: np.random.Generator, counts: np.ndarray, tokens: int,
+                           top_k: int) -> np.ndarray:
+    """fp32 logits [tokens, experts] whose sigmoid top-k selection gives exactly
+    ``counts[e]`` routes to expert e: each token takes the top_k experts with the
+    most routes left (a feasible assignment when sum(counts) = tokens * top_k
+    and no count exceeds tokens); chosen experts get logits in [2, 4], the
+    others in [-4, -2]."""
+    experts = counts.size
+    left = counts.astype(np.int64).copy()
+    logits = rng.uniform(-4.0, -2.0, (tokens, experts)).astype(np.float32)
+    ids = np.arange(experts)
+    for t in range(tokens):
+        order = np.lexsort((ids, -left))[:top_k]
+        assert (left[order] > 0).all()
+        left[order] -= 1
+        logits[t, order] = rng.uniform(2.0, 4.0, top_k).astype(np.float32)
+    assert not left.any()
+    return logits

@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.lk_abi_version() == 1
+    assert lib.lk_abi_version() == 2
     assert isinstance(lib.lk_last_error(), bytes)
 
 
@@ -72,3 +72,29 @@ def test_expert_major_sizes_and_argument_errors(lib):
         _lib.call("lk_moe_schedule", 1, 4, 8, 16, -1, 32, 1, 1, 1, 1, 1, 1 << 20, None)
     with pytest.raises(RuntimeError, match="divisible"):
         _lib.call("lk_w4a16_dense_gemm", 1, 1, 1, 1, 16, 8, 100, 32, None)
+
+
+def test_path_knobs_select_and_reject(lib):
+    for knob, choices in _lib.PATH_KNOBS.items():
+        assert _lib.get_path(knob) == "auto"
+        for choice in choices:
+            with _lib.forced_path(knob, choice):
+                assert _lib.get_path(knob) == choice
+        assert _lib.get_path(knob) == "auto"
+    with pytest.raises(ValueError, match="unknown path knob"):
+        _lib.set_path("no_such_knob", "auto")
+    with pytest.raises(ValueError, match="unknown choice"):
+        _lib.set_path("moe_gemm", "fastest")
+    assert lib.lk_get_path(b"no_such_knob") == -1
+
+
+def test_token_major_decode_route_limit_is_checked_before_any_launch(lib):
+    # top_k = 32 -> 33 routes at intermediate 1024: the token-major W2 launch
+    # cannot take it; the call is refused on the host (null device pointers are
+    # never dereferenced) and the workspace query reports -1
+    assert lib.lk_w4a16_moe_decode_workspace(1, 257, 2304, 1024, 32) == -1
+    assert lib.lk_w4a16_moe_decode_workspace(4, 257, 2304, 1024, 8) == 4 * 9 * 1024 * 2
+    assert lib.lk_w4a16_moe_decode_workspace(1, 257, 2304, 4096, 8) == -1  # I = 4096: LDS
+    with pytest.raises(RuntimeError, match="token-major W2"):
+        _lib.call("lk_w4a16_moe_decode", 1, 1, None, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1,
+                  1, 257, 2304, 1024, 32, 1.0, 1, 128, None)

@@ -6,10 +6,12 @@ in the reference's layout (G = 128, bf16 router weight), run through the
 registry's default (HIP) ops, and are checked against the oracle within the
 quantized-matmul tolerance (1e-2 relative / 2e-2 absolute in bf16). The
 router logits (router.py:50-51) are fp32 sums of exact bf16 products in this
-build's fixed order, not the oracle's or torch's: they are checked against a
-float64 sum within 2e-6 relative, and the oracle block is fed the logits the
-GPU computed (the selection from given logits is what the kernels own, and
-is compared bit-exactly elsewhere).
+build's fixed order, the same for every batch size, not the oracle's or
+torch's: they are checked against a float64 sum within 2e-6 relative and
+against torch's F.linear, whose selections they reproduce (near-ties within
+the two summation orders' rounding counted); the oracle block is fed the
+logits the GPU computed (the selection from given logits is what the kernels
+own, and is compared bit-exactly elsewhere).
 ``MoEDecodeGraph`` replays are compared with eager forwards bit for bit,
 with eager work between replays.
 """
@@ -88,14 +90,67 @@ def test_router_logits(rng, tokens, experts, h):
     assert torch.equal(got, router_logits(from_bits(x, DEV), from_bits(w, DEV)))
 
 
-def test_router_logits_past_the_decode_path_is_torch(rng):
+def test_router_logits_do_not_depend_on_the_batch(rng):
+    """Every token's logits are summed in the same order whatever the batch size
+    (decode T=1, a 64-token tile boundary, a 300-token prefill)."""
     from local_kimi_amd.kernels import router_logits
 
-    x = from_bits(random_bf16_bits(rng, (65, 256)), DEV)
-    w = from_bits(random_bf16_bits(rng, (16, 256), 0.05), DEV)
-    assert torch.equal(router_logits(x, w), torch.nn.functional.linear(x.float(), w.float()))
+    x = from_bits(random_bf16_bits(rng, (300, 2304)), DEV)
+    w = from_bits(random_bf16_bits(rng, (256, 2304), 2304 ** -0.5), DEV)
+    full = router_logits(x, w)
+    for lo, hi in ((0, 1), (5, 6), (0, 16), (3, 67), (64, 65), (100, 300)):
+        assert torch.equal(router_logits(x[lo:hi].contiguous(), w), full[lo:hi]), (lo, hi)
     with pytest.raises(ValueError, match="router logits need"):
         router_logits(x, w[:, :128])
+    with pytest.raises(TypeError, match="BF16"):
+        router_logits(x.float(), w)
+
+
+@pytest.mark.parametrize("tokens", [1, 64, 2048])
+def test_selection_from_hip_logits_matches_torch_linear_logits(rng, tokens):
+    """The reference computes logits with F.linear(x.float(), W.float())
+    (klinear/router.py:50-51). The HIP logits differ from torch's only in the
+    fp32 summation order; the selections made from the two must be identical
+    except at a near-tie within that rounding, which the check counts."""
+    from local_kimi_amd.kernels import moe_router, router_logits
+
+    x = from_bits(random_bf16_bits(rng, (tokens, 2304)), DEV)
+    w = from_bits(random_bf16_bits(rng, (256, 2304), 2304 ** -0.5), DEV)
+    bias = torch.from_numpy(rng.normal(0, 0.01, 256).astype(np.float32)).to(DEV)
+    ours = router_logits(x, w)
+    theirs = torch.nn.functional.linear(x.float(), w.float())
+    # both are fp32 sums of 2304 exact products (error ~ sqrt(K) * eps * |terms|)
+    mag = theirs.abs().amax(dim=1, keepdim=True)
+    assert ((ours - theirs).abs() <= 1e-5 * mag).all()
+    idx_a, w_a = moe_router(ours, bias, 8, routed_scaling_factor=2.446)
+    idx_b, w_b = moe_router(theirs, bias, 8, routed_scaling_factor=2.446)
+    # near-ties: 8th and 9th choice scores closer than the logits' disagreement
+    # can take (sigmoid' <= 1/4, so 1e-5 * |logits| <= 1e-5 in score)
+    choice = torch.sigmoid(theirs) + bias
+    top9 = choice.topk(9, dim=1).values
+    near = (top9[:, 7] - top9[:, 8]) < 2e-5
+    same = (idx_a == idx_b).all(dim=1)
+    assert bool((same | near).all())
+    assert int((~same).sum()) <= max(1, tokens // 1000)
+    torch.testing.assert_close(w_a[same], w_b[same], rtol=1e-5, atol=0)
+    # the oracle router on torch's logits selects what the GPU router selects
+    eidx, ew = OM.route(theirs.cpu().numpy(), bias.cpu().numpy(), 8, routed_scaling_factor=2.446)
+    assert np.array_equal(idx_b.cpu().numpy(), eidx)
+
+
+def test_router_weights_match_torch_sigmoid(rng):
+    """Combine weights: torch.sigmoid gathered, renormalised by sum + 1e-20 and
+    scaled (klinear/router.py:52-85), computed by torch on the same device."""
+    from local_kimi_amd.kernels import moe_router
+
+    logits = torch.from_numpy(rng.normal(0, 1.5, (512, 256)).astype(np.float32)).to(DEV)
+    idx, got = moe_router(logits, None, 8, routed_scaling_factor=2.446)
+    s = torch.sigmoid(logits)
+    want_idx = s.topk(8, dim=1).indices
+    assert torch.equal(idx.sort(dim=1).values, want_idx.sort(dim=1).values)
+    picked = s.gather(1, idx)
+    want = picked / (picked.sum(dim=1, keepdim=True) + 1e-20) * 2.446
+    torch.testing.assert_close(got, want, rtol=4e-7 * 8, atol=0)
 
 
 def test_w4a16_linear_matches_oracle(ckpt, rng):

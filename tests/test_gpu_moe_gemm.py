@@ -17,6 +17,8 @@ import torch
 from oracle import moe as OM
 from oracle import w4a16 as OW
 
+from local_kimi_amd._lib import forced_path
+
 from ._helpers import assert_close_bf16, from_bits, random_bf16_bits, to_bits
 
 pytestmark = pytest.mark.gpu
@@ -114,14 +116,13 @@ def test_schedule_matches_oracle(rng, tokens, routes, experts, shared, invalid, 
 def test_dense_gemm_matches_oracle(rng, monkeypatch, m, n, k, g, form):
     from local_kimi_amd.kernels import w4a16_dense_gemm
 
-    if form == "lds":
-        monkeypatch.setenv("LK_DENSE_GEMM", "lds")
-
     p, s = OW.quantise(random_bf16_bits(rng, (n, k), 0.02), g)
     x = random_bf16_bits(rng, (m, k))
-    y = w4a16_dense_gemm(_dev(x), _dev(p), _dev(s))
+    with forced_path("dense_gemm", "lds" if form == "lds" else "auto"):
+        y = w4a16_dense_gemm(_dev(x), _dev(p), _dev(s))
+        again = w4a16_dense_gemm(_dev(x), _dev(p), _dev(s))
     assert_close_bf16(to_bits(y), OW.dense(x, p, s, g), what=f"dense gemm {m}x{n}x{k} G{g}")
-    assert torch.equal(y, w4a16_dense_gemm(_dev(x), _dev(p), _dev(s)))
+    assert torch.equal(y, again)
 
 
 @pytest.mark.parametrize("form", ["default", "lds"])  # streaming 64-row kernel / LDS-staged GEMM
@@ -129,13 +130,12 @@ def test_dense_gemm_matches_oracle(rng, monkeypatch, m, n, k, g, form):
 def test_fused_qkv_matches_oracle(rng, monkeypatch, m, form):
     from local_kimi_amd.kernels import fused_qkv_w4a16
 
-    if form == "lds":
-        monkeypatch.setenv("LK_DENSE_GEMM", "lds")
     n, k, g = 256, 512, 128
     mats = [OW.quantise(random_bf16_bits(rng, (n, k), 0.02), g) for _ in range(3)]
     x = random_bf16_bits(rng, (m, k))
     flat = [a for pair in mats for a in pair]
-    got = fused_qkv_w4a16(_dev(x), *(_dev(a) for a in flat))
+    with forced_path("dense_gemm", "lds" if form == "lds" else "auto"):
+        got = fused_qkv_w4a16(_dev(x), *(_dev(a) for a in flat))
     want = OW.fused_qkv(x, *flat, g)
     for name, a, e in zip("qkv", got, want):
         assert_close_bf16(to_bits(a), e, what=f"fused qkv {name} m={m}")
@@ -309,3 +309,143 @@ def test_moe_forward_under_graph_replay(rng):
         torch.cuda.synchronize()
         assert torch.equal(gy, eager) and torch.equal(gidx, eidx)
         _ = (xd.float() * 2).sum().item()
+
+
+# ---------------------------------------------------------------------------
+# config-4 sizes: fused QKV [2048, 2304] x [2304, 3 x 4096] and a 2048-token
+# prefill whose expert tiles take every shape
+
+
+def _gpu_w4a16(gen, n, k, g=128):
+    from local_kimi_amd.quant import quantise
+
+    enc = quantise((torch.randn(n, k, device=DEV, generator=gen) * 0.02).to(torch.bfloat16),
+                   group_size=g)
+    return enc.packed, enc.scales
+
+
+def _host(t):
+    return t.cpu().numpy() if t.dtype == torch.uint8 else to_bits(t)
+
+
+@pytest.mark.parametrize("form", ["default", "lds"])  # streaming 64-row kernel / LDS-staged GEMM
+def test_fused_qkv_config4_size_on_sampled_rows(rng, form):
+    """[2048, 2304] x [2304, 3 x 4096] at G = 128, all three outputs, against the
+    oracle on 72 rows (tile boundaries, both ends, the rest random); every
+    column of each sampled row is compared."""
+    from local_kimi_amd.kernels import fused_qkv_w4a16
+
+    m, n, k, g = 2048, 4096, 2304, 128
+    gen = torch.Generator(device=DEV).manual_seed(20260804)
+    mats = [a for _ in range(3) for a in _gpu_w4a16(gen, n, k, g)]
+    x = random_bf16_bits(rng, (m, k))
+    with forced_path("dense_gemm", "lds" if form == "lds" else "auto"):
+        got = fused_qkv_w4a16(_dev(x), *mats)
+    edges = [0, 1, 15, 16, 63, 64, 65, 127, 128, 1023, 1024, 2046, 2047]
+    rows = np.unique(np.concatenate((edges, rng.choice(m, 64, replace=False))))
+    assert rows.size >= 64
+    for j, name in enumerate("qkv"):
+        want = OW.dense(x[rows], _host(mats[2 * j]), _host(mats[2 * j + 1]), g)
+        assert_close_bf16(to_bits(got[j])[rows], want, what=f"fused qkv {name} (config 4)")
+
+
+@pytest.fixture(scope="module")
+def designed_prefill():
+    """2048 tokens at the Kimi-Linear H = 2304, I = 1024, G = 128 with 32 routed
+    experts + 1 shared, routed so that expert tiles take every shape (see
+    designed_counts); the oracle output of every token."""
+    from ._helpers import designed_counts, designed_router_logits
+
+    tokens, routed, h, i, g = 2048, 32, 2304, 1024, 128
+    rng = np.random.default_rng(20260805)
+    gen = torch.Generator(device=DEV).manual_seed(20260805)
+
+    def bank(n, k):
+        pairs = [_gpu_w4a16(gen, n, k, g) for _ in range(routed + 1)]
+        return torch.stack([p for p, _ in pairs]), torch.stack([s for _, s in pairs])
+
+    banks = (*bank(i, h), *bank(i, h), *bank(h, i))
+    counts = designed_counts(tokens, routed, 8)
+    logits = designed_router_logits(rng, counts, tokens, 8)
+    x = random_bf16_bits(rng, (tokens, h))
+    ey, eidx, _ = OM.moe_block(x, logits, None, *(_host(b) for b in banks), top_k=8,
+                               routed_scaling_factor=2.446, group_size=g)
+    return x, logits, banks, counts, ey, eidx
+
+
+def test_prefill_every_token_matches_oracle(designed_prefill):
+    """Expert-major prefill (64-row tiles; tails of 1..16 rows on the 16-row
+    path, 17..63 rows as partial 64-row tiles): every token against the oracle."""
+    from local_kimi_amd.kernels import w4a16_moe_forward
+
+    x, logits, banks, counts, ey, eidx = designed_prefill
+    tails = counts % 64
+    assert ((tails >= 1) & (tails <= 16)).sum() >= 4 and ((tails > 16)).sum() >= 4
+    y, idx, _ = w4a16_moe_forward(_dev(x), _dev(logits), None, *banks, 8, 2.446)
+    assert np.array_equal(idx.cpu().numpy(), eidx)
+    assert np.array_equal(np.bincount(idx.cpu().numpy().reshape(-1), minlength=counts.size),
+                          counts)
+    assert_close_bf16(to_bits(y), ey, what="prefill, every token")
+
+
+# ---------------------------------------------------------------------------
+# the reference caller's own op sequence (engine/klinear/moe.py:278-334):
+# w4a16_swiglu on [T, 9] routes, w4a16_grouped on [T*9, I] rows with
+# idx [T*9, 1], then the torch combine
+
+
+@pytest.mark.parametrize("tokens", [1, 64, 2048])
+def test_reference_caller_sequence(rng, kimi_banks, tokens):
+    from local_kimi_amd.kernels import (W4A16_GROUPED, W4A16_SWIGLU, moe_router, registry,
+                                        shape_stable_expert_indices, w4a16_moe_block)
+    from local_kimi_amd.workloads import normal_router_logits
+
+    w1p, w1s, w3p, w3s, w2p, w2s = kimi_banks
+    x = random_bf16_bits(rng, (tokens, 2304))
+    logits = normal_router_logits(rng, tokens, 256)
+    xd, ld = _dev(x), _dev(logits)
+    idx, w = moe_router(ld, None, 8, routed_scaling_factor=2.446)
+    stable = shape_stable_expert_indices(idx, 256)
+    act = registry.resolve(W4A16_SWIGLU)(xd, stable, w1p, w1s, w3p, w3s)
+    eo = registry.resolve(W4A16_GROUPED)(act.reshape(-1, 1024), stable.reshape(-1, 1), w2p,
+                                         w2s).reshape(tokens, 9, 2304)
+    routed = eo[:, :8].float().mul(w.float().unsqueeze(-1)).sum(dim=1).to(torch.bfloat16)
+    y = routed + eo[:, 8]
+    yb, idxb, _ = w4a16_moe_block(xd, ld, None, *kimi_banks, 8, 2.446)
+    assert torch.equal(idx, idxb)
+    assert_close_bf16(to_bits(y), to_bits(yb), what="caller sequence vs block")
+    # the W2 call's single-route rows against the oracle (rows of assorted experts)
+    stable_h = stable.cpu().numpy()
+    rows = np.unique(rng.choice(tokens * 9, size=min(tokens * 9, 48), replace=False))
+    act_h = to_bits(act.reshape(-1, 1024))
+    for r in rows:
+        e = int(stable_h.reshape(-1)[r])
+        want = OW.dense(act_h[r:r + 1], _host(w2p[e]), _host(w2s[e]), 128)
+        assert_close_bf16(to_bits(eo.reshape(-1, 2304)[r:r + 1]), want, what=f"W2 row {r}")
+    sel = np.unique(rng.choice(tokens, size=min(tokens, 4), replace=False))
+    ey, _ = _oracle_tokens(x, logits, kimi_banks, sel)
+    assert_close_bf16(to_bits(y)[sel], ey, what=f"caller sequence T={tokens}")
+
+
+# ---------------------------------------------------------------------------
+# shapes the token-major W2 + combine launch does not take
+
+
+@pytest.mark.parametrize("tokens,top_k,inter", [(4, 32, 1024), (2, 32, 1024), (1, 8, 4096),
+                                                (4, 8, 4096)])
+def test_block_beyond_the_token_major_route_limit(rng, tokens, top_k, inter):
+    """top_k = 32 (33 routes) or intermediate 4096 at <= 4 tokens: the block
+    runs expert-major end to end and matches the oracle; the token-major
+    decode entry point refuses the shape up front."""
+    from local_kimi_amd.kernels import w4a16_moe_block, w4a16_moe_decode
+
+    h, g, e_routed = 256, 128, 40
+    x, logits, banks = _moe_inputs(rng, e_routed, h, inter, g, tokens)
+    ey, eidx, _ = OM.moe_block(x, logits, None, *banks, top_k=top_k, routed_scaling_factor=2.446,
+                               group_size=g)
+    args = (_dev(x), _dev(logits), None, *(_dev(b) for b in banks), top_k, 2.446)
+    y, idx, _ = w4a16_moe_block(*args)
+    assert np.array_equal(idx.cpu().numpy(), eidx)
+    assert_close_bf16(to_bits(y), ey, what=f"block T={tokens} top_k={top_k} I={inter}")
+    with pytest.raises(ValueError, match="token-major"):
+        w4a16_moe_decode(*args)

@@ -17,6 +17,8 @@ from oracle import moe as OM
 from oracle import mxfp4 as X
 from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
 
+from local_kimi_amd._lib import forced_path
+
 from ._helpers import assert_close_bf16, from_bits, random_bf16_bits, to_bits
 
 pytestmark = pytest.mark.gpu
@@ -96,14 +98,14 @@ def test_dequantise_is_bit_exact_for_every_code_and_exponent():
 def test_gemm_matches_oracle(rng, monkeypatch, m, n, k, form):
     from local_kimi_amd.kernels import mxfp4_gemm, mxfp4_gemm_reference
 
-    if form == "lds":
-        monkeypatch.setenv("LK_DENSE_GEMM", "lds")
     p, s = _encode(rng, n, k)
     x = random_bf16_bits(rng, (m, k))
     want = X.linear(x, p, s)
-    y = mxfp4_gemm(_dev(x), _dev(p), _dev(s))
+    with forced_path("dense_gemm", "lds" if form == "lds" else "auto"):
+        y = mxfp4_gemm(_dev(x), _dev(p), _dev(s))
+        again = mxfp4_gemm(_dev(x), _dev(p), _dev(s))
     assert_close_bf16(to_bits(y), want, what=f"mxfp4 gemm {m}x{n}x{k}")
-    assert torch.equal(y, mxfp4_gemm(_dev(x), _dev(p), _dev(s)))
+    assert torch.equal(y, again)
     yr = mxfp4_gemm_reference(_dev(x), _dev(p), _dev(s))
     assert_close_bf16(to_bits(yr), want, what="mxfp4 reference variant")
 
@@ -131,12 +133,11 @@ def test_gemm_across_scale_exponents(rng):
 def test_gemm_fp16_activations(rng, monkeypatch, m, form):
     from local_kimi_amd.kernels import mxfp4_gemm
 
-    if form == "lds":
-        monkeypatch.setenv("LK_DENSE_GEMM", "lds")
     n, k = 128, 1024
     p, s = _encode(rng, n, k)
     xf = rng.normal(0, 1, (m, k)).astype(np.float16)
-    y = mxfp4_gemm(torch.from_numpy(xf).to(DEV), _dev(p), _dev(s))
+    with forced_path("dense_gemm", "lds" if form == "lds" else "auto"):
+        y = mxfp4_gemm(torch.from_numpy(xf).to(DEV), _dev(p), _dev(s))
     assert y.dtype == torch.float16
     got = y.cpu().numpy().astype(np.float64)
     want = X.linear_f16(xf.view(np.uint16), p, s).view(np.float16).astype(np.float64)
@@ -311,13 +312,58 @@ def test_split_activations_bit_exact(rng):
 def test_moe_block_both_mfma_forms_match_oracle(rng, monkeypatch, form, tokens):
     from local_kimi_amd.kernels import mxfp4_moe_block
 
-    monkeypatch.setenv("LK_MXFP4_MFMA", "bf16" if form == "bf16" else "fp4")
     e_routed, h, inter, k = 12, 384, 256, 4
     banks = (*_bank(rng, e_routed + 1, inter, h), *_bank(rng, e_routed + 1, inter, h),
              *_bank(rng, e_routed + 1, h, inter))
     x = random_bf16_bits(rng, (tokens, h))
     logits = rng.normal(0, 1, (tokens, e_routed)).astype(np.float32)
     ey, eidx, _ = X.moe_block(x, logits, None, *banks, top_k=k, routed_scaling_factor=2.446)
-    y, idx, _ = mxfp4_moe_block(_dev(x), _dev(logits), None, *(_dev(b) for b in banks), k, 2.446)
+    with forced_path("mxfp4_mfma", "bf16" if form == "bf16" else "fp4"):
+        y, idx, _ = mxfp4_moe_block(_dev(x), _dev(logits), None, *(_dev(b) for b in banks), k,
+                                    2.446)
     assert np.array_equal(idx.cpu().numpy(), eidx)
     assert_close_bf16(to_bits(y), ey, what=f"mxfp4 moe block ({form}, T={tokens})")
+
+
+@pytest.fixture(scope="module")
+def designed_mx_prefill():
+    """2048 tokens at H = 2304, I = 1024 with 32 routed + 1 shared MXFP4
+    experts, routed so that expert tiles take every shape (designed_counts);
+    the oracle output of every token."""
+    from local_kimi_amd.quant import quantize_mxfp4
+
+    from ._helpers import designed_counts, designed_router_logits
+
+    tokens, routed, h, i = 2048, 32, 2304, 1024
+    rng = np.random.default_rng(20260806)
+    gen = torch.Generator(device=DEV).manual_seed(20260806)
+
+    def bank(n, k):
+        pairs = [quantize_mxfp4((torch.randn(n, k, device=DEV, generator=gen) * 0.02)
+                                .to(torch.bfloat16)) for _ in range(routed + 1)]
+        return torch.stack([p for p, _ in pairs]), torch.stack([s for _, s in pairs])
+
+    banks = (*bank(i, h), *bank(i, h), *bank(h, i))
+    counts = designed_counts(tokens, routed, 8)
+    logits = designed_router_logits(rng, counts, tokens, 8)
+    x = random_bf16_bits(rng, (tokens, h))
+    ey, eidx, _ = X.moe_block(x, logits, None, *(b.cpu().numpy() for b in banks), top_k=8,
+                              routed_scaling_factor=2.446)
+    return x, logits, banks, counts, ey, eidx
+
+
+@pytest.mark.parametrize("form", ["scaled-fp4", "bf16"])
+def test_prefill_every_token_matches_oracle(designed_mx_prefill, form):
+    """MXFP4 prefill on 64-row tiles in both MFMA forms (scaled fp4 with the
+    fp8 hi + lo activation split, and bf16 on decoded weights): every token,
+    so every tile shape of both kernels (full, partial 64-row, the 16-row
+    tail path) is under the oracle."""
+    from local_kimi_amd.kernels import mxfp4_moe_block
+
+    x, logits, banks, counts, ey, eidx = designed_mx_prefill
+    with forced_path("mxfp4_mfma", "bf16" if form == "bf16" else "auto"):
+        y, idx, _ = mxfp4_moe_block(_dev(x), _dev(logits), None, *banks, 8, 2.446)
+    assert np.array_equal(idx.cpu().numpy(), eidx)
+    assert np.array_equal(np.bincount(idx.cpu().numpy().reshape(-1), minlength=counts.size),
+                          counts)
+    assert_close_bf16(to_bits(y), ey, what=f"mxfp4 prefill ({form}), every token")

@@ -1,6 +1,6 @@
 """GPU parity of the persistent 16-row expert GEMM (decode batches).
 
-The persistent kernel and the per-tile streaming kernel (LK_MOE_PERSIST=0)
+The persistent kernel and the per-tile streaming kernel (path knob moe_persist=off)
 perform the same MFMA chains in the same order, so their outputs must be
 bit-identical; the per-tile kernel is itself checked against the oracle
 elsewhere, and every case here is also checked against the oracle within the
@@ -60,14 +60,14 @@ def _mx_bank(rng, e, n, k):
 
 def _both(monkeypatch, fn, *args):
     """fn(*args) with the persistent kernel, then with the per-tile kernel."""
-    monkeypatch.delenv("LK_MOE_PERSIST", raising=False)
-    monkeypatch.delenv("LK_MOE_GEMM", raising=False)
-    a = fn(*args)
-    torch.cuda.synchronize()
-    monkeypatch.setenv("LK_MOE_PERSIST", "0")
-    b = fn(*args)
-    torch.cuda.synchronize()
-    monkeypatch.delenv("LK_MOE_PERSIST")
+    from local_kimi_amd._lib import forced_path
+
+    with forced_path("moe_gemm", "auto"):
+        a = fn(*args)
+        torch.cuda.synchronize()
+        with forced_path("moe_persist", "off"):
+            b = fn(*args)
+            torch.cuda.synchronize()
     return a, b
 
 

@@ -3,7 +3,7 @@
 With at most 256 routed experts, batches of at most 8 tokens route and
 schedule in one launch (schedule_one_kernel with routing); batches of at most
 1024 token-routes route on a grid and schedule in one launch; larger batches,
-or LK_MOE_FUSED_SCHEDULE=0 for any batch, take the router launch and the
+or the path knob moe_fused_schedule=off for any batch, take the router launch and the
 chunked schedule launches. All run the same selection code and the same stable
 ranking, so the selections, combine weights and block outputs must be
 bit-identical; the results are also checked against the oracle within the
@@ -63,13 +63,13 @@ def _mx_bank(rng, e, n, k):
 
 def _fused_and_split(monkeypatch, fn, *args):
     """fn(*args) on the one-launch forms, then on the router and chunked schedule."""
-    monkeypatch.delenv("LK_MOE_FUSED_SCHEDULE", raising=False)
+    from local_kimi_amd._lib import forced_path
+
     a = fn(*args)
     torch.cuda.synchronize()
-    monkeypatch.setenv("LK_MOE_FUSED_SCHEDULE", "0")
-    b = fn(*args)
-    torch.cuda.synchronize()
-    monkeypatch.delenv("LK_MOE_FUSED_SCHEDULE")
+    with forced_path("moe_fused_schedule", "off"):
+        b = fn(*args)
+        torch.cuda.synchronize()
     return a, b
 
 

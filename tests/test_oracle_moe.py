@@ -39,6 +39,34 @@ def test_router_matches_brute_force_full_sort(rng):
         np.testing.assert_allclose(w[t], g / g.sum() * 2.446, rtol=2e-6)
 
 
+def test_sigmoid_matches_torch_sigmoid():
+    """The oracle's fp32 sigmoid (1 / (1 + exp(-x)) in fp32, the HIP router's
+    formula) against torch.sigmoid (the reference's call, klinear/router.py:52)
+    and against the correctly rounded value, over a dense sweep: within 2 ulp
+    of torch for x >= 0 (where top-k selections are made), 4 ulp in the
+    negative tail, and the selection made from either is the same."""
+    import torch
+
+    def ulps(a, b):
+        return np.abs(a.view(np.int32).astype(np.int64) - b.view(np.int32).astype(np.int64))
+
+    x = np.linspace(-30, 30, 2_000_001, dtype=np.float32)
+    ours = M.sigmoid_f32(x)
+    theirs = torch.sigmoid(torch.from_numpy(x)).numpy()
+    exact = (1.0 / (1.0 + np.exp(-x.astype(np.float64)))).astype(np.float32)
+    assert ulps(ours, theirs).max() <= 4
+    assert ulps(ours, theirs)[x >= 0].max() <= 2
+    assert ulps(ours, exact).max() <= 4
+    assert ulps(ours, exact)[x >= 0].max() <= 1
+    assert (ulps(ours, theirs)[x >= 0] == 0).mean() > 0.95
+    rng = np.random.default_rng(7)
+    logits = rng.normal(0, 1, (256, 256)).astype(np.float32)
+    idx, _ = M.route(logits, None, 8)
+    choice = torch.sigmoid(torch.from_numpy(logits))
+    want = torch.topk(choice, 8, dim=1).indices.numpy()
+    assert np.array_equal(np.sort(idx, axis=1), np.sort(want, axis=1))
+
+
 def test_router_ties_break_to_lower_expert_id():
     logits = np.zeros((1, 16), dtype=np.float32)
     logits[0, [3, 9, 12]] = 1.0
