@@ -263,6 +263,29 @@ LK_API int lk_w4a16_moe_forward(const uint16_t* x, const float* logits, const fl
                                 float routed_scaling_factor, int renormalize, int64_t group_size,
                                 void* stream);
 
+/* ---- the block of lk_w4a16_moe_forward for callers that cannot allocate:
+ * no reference counterpart. For code under HIP graph capture, tight serving
+ * loops and harnesses that forbid hipMalloc: the same arguments minus the
+ * workspace, which here is a static device array of
+ * lk_w4a16_moe_forward_static_capacity() bytes (8 MiB) per GPU, held until
+ * the process ends. Calls whose lk_w4a16_moe_forward_workspace() exceeds it
+ * are rejected before anything is launched (up to 139 tokens at the
+ * Kimi-Linear shape: hidden 2304, intermediate 1024, 257 experts, top-8).
+ * Nothing is allocated or freed; the scratch needs no clearing (every table
+ * and row in it is written before it is read). Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (two streams, two host
+ * threads) race and must be serialised by the caller. Outputs are
+ * bit-identical to lk_w4a16_moe_forward's (the same kernels). */
+LK_API int64_t lk_w4a16_moe_forward_static_capacity(void);
+LK_API int lk_w4a16_moe_forward_static(const uint16_t* x, const float* logits, const float* bias,
+                                       const uint8_t* w1_packed, const uint16_t* w1_scales,
+                                       const uint8_t* w3_packed, const uint16_t* w3_scales,
+                                       const uint8_t* w2_packed, const uint16_t* w2_scales,
+                                       uint16_t* y, int64_t* expert_indices, float* weights,
+                                       int64_t tokens, int64_t experts, int64_t h, int64_t i,
+                                       int64_t top_k, float routed_scaling_factor,
+                                       int renormalize, int64_t group_size, void* stream);
+
 /* ---- MXFP4 (OCP MX): E2M1 codes low nibble first, one E8M0 exponent per
  *      32 values along K; value = e2m1 * 2**(e8m0 - 127).
  *      engine/k3ref/dequant.py:18-73 (codec), engine/kernels/reference.py:29-80

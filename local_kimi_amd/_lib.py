@@ -49,6 +49,8 @@ SIGNATURES: dict[str, list] = {
     "lk_w4a16_fused_qkv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "lk_w4a16_moe_forward": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                              _I64, _I64, _I64, _I64, _I64, _F, _I, _I64, _P],
+    "lk_w4a16_moe_forward_static": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                    _I64, _I64, _I64, _I64, _I64, _F, _I, _I64, _P],
     "lk_mxfp4_quantise": [_P, _P, _P, _I64, _I64, _P],
     "lk_mxfp4_dequantise": [_P, _P, _P, _I64, _I64, _I, _P],
     "lk_mxfp4_gemm": [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P],
@@ -65,6 +67,7 @@ SIGNATURES: dict[str, list] = {
 # name -> argument types of the size queries (they return int64, -1 on bad input)
 QUERIES: dict[str, list] = {
     "lk_w4a16_moe_decode_workspace": [_I64, _I64, _I64, _I64, _I64],
+    "lk_w4a16_moe_forward_static_capacity": [],
     "lk_w4a16_grouped_gemm_workspace": [_I64, _I64, _I64],
     "lk_w4a16_moe_forward_workspace": [_I64, _I64, _I64, _I64, _I64],
     "lk_mxfp4_moe_forward_workspace": [_I64, _I64, _I64, _I64, _I64],

@@ -28,6 +28,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "lk_common.hpp"
 #include "lk_route.hpp"
 
@@ -2712,6 +2714,83 @@ int lk_w4a16_moe_forward(const uint16_t* x, const float* logits, const float* bi
                             w2_packed, w2_scales, y, expert_indices, weights, workspace,
                             workspace_bytes, tokens, experts, h, i, top_k, routed_scaling_factor,
                             renormalize, group_size, stream);
+}
+
+}  // extern "C"
+
+// Device scratch of lk_w4a16_moe_forward_static: one array per GPU, held until
+// the process ends. Host code never passes the array's name to a kernel (on
+// the host it is a stand-in, not a device address); it uses the address
+// hipGetSymbolAddress returns for the current device.
+constexpr size_t kStaticScratchBytes = size_t{8} << 20;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+namespace lk {
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The current device's scratch address, looked up once per device.
+int static_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+    set_error("static scratch: no usable current device (%s)", hipGetErrorString(e));
+    return LK_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error("static scratch: hipGetSymbolAddress failed on device %d (%s)", dev,
+                hipGetErrorString(e));
+      return LK_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return LK_OK;
+}
+
+}  // namespace
+}  // namespace lk
+
+extern "C" {
+
+int64_t lk_w4a16_moe_forward_static_capacity(void) {
+  return static_cast<int64_t>(kStaticScratchBytes);
+}
+
+int lk_w4a16_moe_forward_static(const uint16_t* x, const float* logits, const float* bias,
+                                const uint8_t* w1_packed, const uint16_t* w1_scales,
+                                const uint8_t* w3_packed, const uint16_t* w3_scales,
+                                const uint8_t* w2_packed, const uint16_t* w2_scales, uint16_t* y,
+                                int64_t* expert_indices, float* weights, int64_t tokens,
+                                int64_t experts, int64_t h, int64_t i, int64_t top_k,
+                                float routed_scaling_factor, int renormalize, int64_t group_size,
+                                void* stream) {
+  const int64_t need = lk_w4a16_moe_forward_workspace(tokens, experts, h, i, top_k);
+  LK_REQUIRE(need >= 0, "invalid MoE dimensions (tokens %lld, experts %lld, top_k %lld)",
+             (long long)tokens, (long long)experts, (long long)top_k);
+  LK_REQUIRE(need <= static_cast<int64_t>(kStaticScratchBytes),
+             "lk_w4a16_moe_forward_static: this call needs %lld bytes of scratch, the static "
+             "scratch holds %lld; use lk_w4a16_moe_forward with a workspace",
+             (long long)need, (long long)kStaticScratchBytes);
+  if (tokens == 0) {  // nothing to launch; the usual argument checks still apply
+    return lk_w4a16_moe_forward(x, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
+                                w2_packed, w2_scales, y, expert_indices, weights, nullptr, 0,
+                                tokens, experts, h, i, top_k, routed_scaling_factor, renormalize,
+                                group_size, stream);
+  }
+  void* ws = nullptr;
+  if (int rc = static_scratch(&ws)) return rc;
+  return lk_w4a16_moe_forward(x, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
+                              w2_packed, w2_scales, y, expert_indices, weights, ws,
+                              static_cast<int64_t>(kStaticScratchBytes), tokens, experts, h, i,
+                              top_k, routed_scaling_factor, renormalize, group_size, stream);
 }
 
 int lk_mxfp4_moe_forward(const uint16_t* x, const float* logits, const float* bias,
