@@ -1,46 +1,66 @@
 #!/usr/bin/env python3
-"""MoE-layer decode µs/token and achieved HBM GB/s at W4A16 on one MI355X.
+"""MoE-layer decode µs/token + achieved HBM GB/s (% of peak) at W4A16, one MI355X.
 
-Workload (default, ``moe_decode``): one Kimi-Linear MoE layer decoding one
-token: hidden 2304, 256 routed experts + 1 shared, moe_intermediate 1024,
-sigmoid top-8 router (routed_scaling_factor 2.446) on logits ~N(0, 1), W4A16
-weights drawn from N(0, 0.02) and quantised at group 128 on the GPU. A step is
-router + gate/up + SwiGLU + W2 + weighted combine + shared expert for one
-token. 26 distinct layer banks (24.4 GB) are rotated so every step reads its
-weights from HBM, not from the 256 MB MALL. Steps are captured in a HIP graph
-and replayed; inputs are resident in HBM before the timed region.
+Default run (``--workload all``): one JSON line whose top level is the
+headline, a batch-1 Kimi-Linear MoE layer decode (hidden 2304, 256 routed + 1
+shared experts, moe_intermediate 1024, sigmoid top-8 router with
+routed_scaling_factor 2.446 on logits ~N(0, 1), W4A16 weights ~N(0, 0.02)
+quantised at group 128 on the GPU). A step is router + gate/up + SwiGLU + W2
++ weighted combine + shared expert for one token. 26 distinct layer banks
+(24.4 GB) rotate so every step reads its weights from HBM, not from the
+256 MB MALL; the steps of one rotation are captured in a HIP graph and
+replayed; inputs are resident in HBM before the timed region. At least 104
+steps (four rotations) are timed after at least 10 warm-up steps, whatever
+``--steps`` / ``--warmup`` ask; both the requested and the timed counts are
+printed.
 
-``--workload dense_decode``: x [1, 2304] x W [9216, 2304] at group 128, 40
-rotated weight copies (439 MB).
+The line also carries ``configs``: the other four workload shapes, each timed
+the same way and each with its own ``roofline`` and ``cpu_baseline``:
+config 1 dense GEMV x[1,2304] . W[9216,2304]; config 3 batched decode at
+M = 4, 16, 64 with Zipf(1.1) routing; config 4 the 2048-token MoE prefill and
+the fused QKV projection [2048,2304] x [2304,3 x 4096]; config 5 the MXFP4
+expert banks at M = 64 and 2048 tokens. ``floor`` holds the measured memory
+floors (empty-kernel launch, a streaming read of 11 MB and of one MoE layer's
+33 MB in its 27 matrices) that the decode kernels are also reported against.
 
-``--workload klinear_decode``: the model-slice caller of the same layer
-(``local_kimi_amd.klinear.KLinearMoE``: the router logits ``x Wg^T`` in fp32
-from bf16 router weights, then the MoE block), 26 layers with their own
-router weights, one token per layer step, captured in one HIP graph.
-
-Prints ONE JSON line. ``roofline`` is for the dominant kernel (gate/up +
-SwiGLU, or the dense GEMV), timed with HIP events on the stream it runs on;
-``cpu_baseline`` times the numpy oracle of the same step on the host (one
-thread, a bounded sample of tokens).
+``roofline``: for the decode configs the dominant kernel's algorithmic bytes
+per launch over its average launch time, timed with HIP events on the stream
+it is launched on; for the prefill configs the whole block's (or the QKV
+kernel's) FLOPs over its time. ``cpu_baseline``: a torch restatement of the
+reference path on the host (dequantise to bf16, F.linear with fp32
+accumulation, the bf16 SwiGLU, the fp32 weighted combine, the bf16 add of the
+shared expert), all host threads the process may use, median of 10 runs after
+3 warm-ups, on a bounded sample stated per config.
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
+import math
 import os
+import platform
 import sys
 import time
 
 import numpy as np
 import torch
+import torch.nn.functional as F
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
 H, E_ROUTED, INTER, TOP_K, G, SCALING = 2304, 256, 1024, 8, 128, 2.446
-DENSE_N = 9216
+DENSE_N, QKV_N, PREFILL_TOKENS = 9216, 4096, 2048
+LAYERS, DENSE_COPIES = 26, 40
+MIN_TIMED_STEPS, MIN_WARMUP_STEPS = 104, 10
+
+HBM_PEAK_GBPS = 8000.0        # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0     # dense bf16 MFMA
+FP4_PEAK_TFLOPS = 10100.0     # dense fp4 MFMA
+
+METRIC = "MoE-layer decode us/token + achieved HBM GB/s (% of peak) at W4A16"
 
 
 def log(msg: str) -> None:
@@ -51,24 +71,71 @@ def w4a16_bytes(n: int, k: int, g: int = G) -> int:
     return n * k // 2 + n * (k // g) * 2
 
 
-EXPERT_BYTES = 2 * w4a16_bytes(INTER, H) + w4a16_bytes(H, INTER)       # 3,649,536
-GATEUP_EXPERT_BYTES = 2 * w4a16_bytes(INTER, H)                         # 2,433,024
-TOKEN_IO_BYTES = H * 2 + E_ROUTED * 4 + H * 2                           # x + logits + y
+def mxfp4_bytes(n: int, k: int) -> int:
+    return n * k // 2 + n * (k // 32)
 
 
-def measured_traffic(kernel: str) -> tuple[int | None, str | None]:
-    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/traffic.json)."""
-    import json as _json
-
-    path = os.path.join(ROOT, "profiles", "traffic.json")
-    try:
-        data = _json.load(open(path))
-        return int(data["kernels"][kernel]["traffic_bytes"]), "profiles/traffic.json"
-    except (OSError, KeyError, ValueError):
-        return None, None
+EXPERT_BYTES = 2 * w4a16_bytes(INTER, H) + w4a16_bytes(H, INTER)          # 3,649,536
+GATEUP_EXPERT_BYTES = 2 * w4a16_bytes(INTER, H)                            # 2,433,024
+MX_EXPERT_BYTES = 2 * mxfp4_bytes(INTER, H) + mxfp4_bytes(H, INTER)        # 3,760,128
+TOKEN_IO_BYTES = H * 2 + E_ROUTED * 4 + H * 2                              # x + logits + y
+EXPERT_FLOPS = 2 * 3 * INTER * H                                           # per routed row
 
 
-def make_bank(rows: int, cols: int, experts: int, gen: torch.Generator, dev):
+# ---------------------------------------------------------------------------
+# GPU timing
+
+
+class Plan:
+    """Warm-up and timed step counts: at least MIN_WARMUP_STEPS / MIN_TIMED_STEPS,
+    rounded up to whole replays of a graph of `per_graph` steps."""
+
+    def __init__(self, steps: int, warmup: int):
+        self.steps_requested, self.warmup_requested = steps, warmup
+
+    def replays(self, per_graph: int) -> tuple[int, int]:
+        warm = math.ceil(max(self.warmup_requested, MIN_WARMUP_STEPS) / per_graph)
+        timed = math.ceil(max(self.steps_requested, MIN_TIMED_STEPS) / per_graph)
+        return warm, timed
+
+
+def capture(fn, stream: torch.cuda.Stream) -> torch.cuda.CUDAGraph:
+    with torch.cuda.stream(stream):
+        fn()  # outside the graph first: allocations, library load, kernel attributes
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_graph(graph, stream, per_graph: int, plan: Plan) -> dict:
+    """Replay warm-ups, then time whole replays with HIP events recorded on the
+    replay stream; returns µs per step and the step counts."""
+    warm, timed = plan.replays(per_graph)
+    with torch.cuda.stream(stream):
+        for _ in range(warm):
+            graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(timed):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    steps = timed * per_graph
+    return {"us": ms * 1000.0 / steps, "steps": steps, "warmup": warm * per_graph,
+            "ms_total": ms}
+
+
+# ---------------------------------------------------------------------------
+# synthetic weights (quantised on the GPU)
+
+
+def make_w4a16_bank(rows, cols, experts, gen, dev):
     from local_kimi_amd.quant import quantise
 
     packed = torch.empty((experts, rows, cols // 2), dtype=torch.uint8, device=dev)
@@ -81,219 +148,209 @@ def make_bank(rows: int, cols: int, experts: int, gen: torch.Generator, dev):
     return packed, scales
 
 
-def time_graph(graph: torch.cuda.CUDAGraph, replays: int, stream: torch.cuda.Stream) -> float:
-    """Milliseconds for `replays` graph replays, HIP events on the replay stream."""
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        start.record(stream)
-        for _ in range(replays):
-            graph.replay()
-        end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end)
+def make_mxfp4_bank(rows, cols, experts, gen, dev):
+    from local_kimi_amd.quant import quantize_mxfp4
+
+    packed = torch.empty((experts, rows, cols // 2), dtype=torch.uint8, device=dev)
+    scale = torch.empty((experts, rows, cols // 32), dtype=torch.uint8, device=dev)
+    for e in range(experts):
+        w = (torch.randn((rows, cols), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        p, s = quantize_mxfp4(w)
+        packed[e].copy_(p)
+        scale[e].copy_(s)
+    return packed, scale
 
 
-def capture(fn, stream: torch.cuda.Stream) -> torch.cuda.CUDAGraph:
-    with torch.cuda.stream(stream):
-        fn()  # warm-up outside the graph (allocations, library load)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
+def layer_banks(weights: str, gen, dev, layers: int = LAYERS):
+    mk = make_mxfp4_bank if weights == "mxfp4" else make_w4a16_bank
+    master = (*mk(INTER, H, E_ROUTED + 1, gen, dev), *mk(INTER, H, E_ROUTED + 1, gen, dev),
+              *mk(H, INTER, E_ROUTED + 1, gen, dev))
+    return [master] + [tuple(t.clone() for t in master) for _ in range(layers - 1)]
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: a torch restatement of the reference path on the host
+
+
+def cpu_threads() -> int:
+    limit = os.environ.get("OMP_NUM_THREADS")
+    n = os.cpu_count() or 1
+    threads = min(n, int(limit)) if limit and limit.isdigit() and int(limit) > 0 else n
+    torch.set_num_threads(threads)
+    return threads
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_median(fn, runs: int = 10, warm: int = 3) -> float:
+    for _ in range(warm):
         fn()
-    torch.cuda.synchronize()
-    return graph
-
-
-def cpu_baseline_moe(banks_l0, xs, logits, sample: int) -> dict:
-    """Oracle decode of `sample` tokens on one host thread (layer-0 weights)."""
-    from threadpoolctl import threadpool_limits
-
-    from oracle import moe as OM
-
-    host = [t.cpu().numpy() if t.dtype == torch.uint8 else
-            t.cpu().view(torch.int16).numpy().view(np.uint16) for t in banks_l0]
     times = []
-    with threadpool_limits(1):
-        for i in range(sample):
-            x = xs[i].cpu().view(torch.int16).numpy().view(np.uint16)
-            lg = logits[i].cpu().numpy()
-            t0 = time.perf_counter()
-            OM.moe_block(x, lg, None, *host, top_k=TOP_K, routed_scaling_factor=SCALING, group_size=G)
-            times.append(time.perf_counter() - t0)
-    us = float(np.median(times)) * 1e6
-    return {"value": round(us, 1), "unit": "us/token", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle of the full MoE decode step (router, dequantise 9 experts, "
-                      f"gate/up, SwiGLU, W2, combine) for {sample} tokens on one host thread, median"}
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times))
 
 
-def cpu_baseline_dense(packed, scales, x, sample: int) -> dict:
-    from threadpoolctl import threadpool_limits
-
-    from oracle import w4a16 as OW
-
-    p = packed.cpu().numpy()
-    s = scales.cpu().view(torch.int16).numpy().view(np.uint16)
-    xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
-    times = []
-    with threadpool_limits(1):
-        for _ in range(sample):
-            t0 = time.perf_counter()
-            OW.dense(xb, p, s, G)
-            times.append(time.perf_counter() - t0)
-    us = float(np.median(times)) * 1e6
-    return {"value": round(us, 1), "unit": "us/token", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle dense GEMV (dequantise + matmul) x{sample}, one host thread, median"}
+def cpu_dequant_w4a16(packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """bf16(q * s) (engine/quant/w4a16.py:108-129) on the host."""
+    n = packed.shape[0]
+    codes = torch.stack(((packed & 0xF), (packed >> 4)), dim=-1).reshape(n, -1).to(torch.int16)
+    codes = torch.where(codes >= 8, codes - 16, codes).float()
+    g = codes.shape[1] // scales.shape[1]
+    return (codes.reshape(n, -1, g) * scales.float()[..., None]).reshape(n, -1).to(torch.bfloat16)
 
 
-def run_moe(args, dev) -> dict:
+_E2M1 = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+                      -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0])
+
+
+def cpu_dequant_mxfp4(packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """e2m1 * 2^(e8m0 - 127) cast to bf16 (engine/k3ref/dequant.py:43-73)."""
+    n = packed.shape[0]
+    codes = torch.stack(((packed & 0xF), (packed >> 4)), dim=-1).reshape(n, -1).long()
+    vals = _E2M1[codes].reshape(n, -1, 32)
+    exps = torch.ldexp(torch.ones(()), scale.to(torch.int32) - 127)
+    return (vals * exps[..., None]).reshape(n, -1).to(torch.bfloat16)
+
+
+def cpu_linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    return F.linear(x.float(), w.float()).to(torch.bfloat16)
+
+
+def cpu_router(logits: torch.Tensor, top_k: int | None = None):
+    """klinear/router.py:52-85 (no bias, one group)."""
+    s = torch.sigmoid(logits)
+    idx = torch.topk(s, TOP_K if top_k is None else top_k, dim=1).indices
+    w = s.gather(1, idx)
+    return idx, w / (w.sum(dim=1, keepdim=True) + 1e-20) * SCALING
+
+
+class CpuMoe:
+    """The block on the host for one layer's banks (W4A16 or MXFP4)."""
+
+    def __init__(self, banks, weights: str):
+        self.host = [t.cpu() for t in banks]
+        self.deq = cpu_dequant_mxfp4 if weights == "mxfp4" else cpu_dequant_w4a16
+
+    def expert(self, e: int, rows: torch.Tensor) -> torch.Tensor:
+        """SwiGLU expert e on bf16 rows: kernels/__init__.py:182-197 then W2."""
+        w1p, w1s, w3p, w3s, w2p, w2s = self.host
+        gate = cpu_linear(rows, self.deq(w1p[e], w1s[e]))
+        up = cpu_linear(rows, self.deq(w3p[e], w3s[e]))
+        act = F.silu(gate) * up  # bf16 silu, bf16 multiply
+        return cpu_linear(act, self.deq(w2p[e], w2s[e]))
+
+    def routed(self, x, idx, experts, eo):
+        for e in experts:
+            tok, slot = torch.nonzero(idx == e, as_tuple=True)
+            eo[tok, slot] = self.expert(int(e), x[tok])
+
+    def step(self, x, logits, experts=None):
+        """Router, the routed experts (all, or `experts` only), shared expert, combine."""
+        idx, w = cpu_router(logits)
+        eo = torch.zeros((x.shape[0], TOP_K + 1, H), dtype=torch.bfloat16)
+        self.routed(x, idx, torch.unique(idx) if experts is None else experts, eo)
+        eo[:, TOP_K] = self.expert(E_ROUTED, x)
+        routed = eo[:, :TOP_K].float().mul(w.unsqueeze(-1)).sum(dim=1).to(torch.bfloat16)
+        return routed + eo[:, TOP_K]
+
+
+def cpu_baseline_block(banks, x, logits, weights: str, unit: str, per_step: float = 1.0,
+                       max_experts: int = 16) -> dict:
+    """The block of one step on the host. With more routed experts than
+    `max_experts` in the step, a stride sample of them is timed with the router,
+    shared expert and combine, and the routed part is scaled by the expert count."""
+    threads = cpu_threads()
+    cpu = CpuMoe(banks, weights)
+    xh, lh = x.cpu(), logits.cpu()
+    union = torch.unique(cpu_router(lh)[0])
+    u = int(union.numel())
+    if u <= max_experts:
+        t = cpu_median(lambda: cpu.step(xh, lh))
+        sample = f"the whole step ({xh.shape[0]} tokens, {u} routed experts + shared)"
+    else:
+        subset = union[:: math.ceil(u / max_experts)]
+        idx = cpu_router(lh)[0]
+        eo = torch.zeros((xh.shape[0], TOP_K + 1, H), dtype=torch.bfloat16)
+        t_sample = cpu_median(lambda: cpu.step(xh, lh, subset))
+        t_subset = cpu_median(lambda: cpu.routed(xh, idx, subset, eo))
+        t = t_sample + t_subset * (u / subset.numel() - 1.0)
+        sample = (f"{xh.shape[0]} tokens: router, shared expert, combine and {subset.numel()} of "
+                  f"the {u} routed experts (every {math.ceil(u / max_experts)}th, their real rows) "
+                  f"timed; the routed part scaled by {u}/{subset.numel()}")
+    return {"value": round(t * 1e6 / per_step, 1), "unit": unit, "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": f"torch restatement on the host ({weights}: dequantise to bf16, F.linear "
+                      f"fp32, bf16 SwiGLU, W2, fp32 combine + shared); {sample}; median of 10 "
+                      "after 3 warm-ups"}
+
+
+# ---------------------------------------------------------------------------
+# configs
+
+
+def run_moe_decode(plan: Plan, dev, banks, cpu: bool) -> dict:
+    """Config 2: batch-1 decode, the headline."""
     from local_kimi_amd.kernels import w4a16_moe_block, w4a16_moe_gateup
 
-    layers = args.layers
     gen = torch.Generator(device=dev).manual_seed(20260729)
-    t0 = time.time()
-    master = (*make_bank(INTER, H, E_ROUTED + 1, gen, dev), *make_bank(INTER, H, E_ROUTED + 1, gen, dev),
-              *make_bank(H, INTER, E_ROUTED + 1, gen, dev))
-    banks = [master] + [tuple(t.clone() for t in master) for _ in range(layers - 1)]
-    xs = [(torch.randn((1, H), device=dev, generator=gen)).to(torch.bfloat16) for _ in range(layers)]
-    logits = [torch.randn((1, E_ROUTED), device=dev, generator=gen) for _ in range(layers)]
-    torch.cuda.synchronize()
-    log(f"[bench] {layers} layer banks ready in {time.time() - t0:.1f}s "
-        f"({layers * (E_ROUTED + 1) * EXPERT_BYTES / 1e9:.1f} GB)")
-
+    xs = [torch.randn((1, H), device=dev, generator=gen).to(torch.bfloat16) for _ in range(LAYERS)]
+    logits = [torch.randn((1, E_ROUTED), device=dev, generator=gen) for _ in range(LAYERS)]
     stream = torch.cuda.Stream(device=dev)
 
     def block_all():
-        for l in range(layers):
+        for l in range(LAYERS):
             w4a16_moe_block(xs[l], logits[l], None, *banks[l], TOP_K, SCALING)
 
     def gateup_all():
-        for l in range(layers):
-            w1p, w1s, w3p, w3s = banks[l][:4]
-            w4a16_moe_gateup(xs[l], logits[l], None, w1p, w1s, w3p, w3s, TOP_K, SCALING)
+        for l in range(LAYERS):
+            w4a16_moe_gateup(xs[l], logits[l], None, *banks[l][:4], TOP_K, SCALING)
 
-    g_block = capture(block_all, stream)
-    g_gateup = capture(gateup_all, stream)
-
-    steps = max(layers, (args.steps + layers - 1) // layers * layers)
-    warm = max(1, (args.warmup + layers - 1) // layers)
-    for _ in range(warm):
-        g_block.replay()
-        g_gateup.replay()
-    torch.cuda.synchronize()
-    log(f"[bench] warm-up done ({warm * layers} steps); timing {steps} steps")
-    block_ms = time_graph(g_block, steps // layers, stream)
-    gateup_ms = time_graph(g_gateup, steps // layers, stream)
-    us_per_token = block_ms * 1000.0 / steps
-    gateup_us = gateup_ms * 1000.0 / steps
-    block_bytes = (TOP_K + 1) * EXPERT_BYTES + TOKEN_IO_BYTES
-    gateup_bytes = (TOP_K + 1) * GATEUP_EXPERT_BYTES + H * 2 + E_ROUTED * 4 + (TOP_K + 1) * INTER * 2
-    log(f"[bench] block {us_per_token:.2f} us/token, gate/up kernel {gateup_us:.2f} us/launch")
-
-    result = {
-        "metric": "MoE-layer decode us/token + achieved HBM GB/s (% of peak) at W4A16",
-        "value": round(us_per_token, 3),
-        "unit": "us/token",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": warm * layers,
-        "ms_per_step": round(block_ms / steps, 6),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x and logits",
-        "config": {"workload": "moe_decode_batch1", "hidden": H, "routed_experts": E_ROUTED,
-                   "shared_experts": 1, "moe_intermediate": INTER, "top_k": TOP_K, "group_size": G,
-                   "tokens_per_step": 1, "layer_banks_rotated": layers, "launches_per_step": 2},
-        "achieved_gbps": round(block_bytes / (us_per_token * 1e3), 1),
-        "pct_hbm_peak": round(100.0 * block_bytes / (us_per_token * 1e3) / HBM_PEAK_GBPS, 2),
-        "algorithmic_bytes_per_step": block_bytes,
-        "roofline": {"kernel": "moe_gateup_ksplit_kernel (router + gate/up + SwiGLU, 9 routes)",
-                     "bound": "hbm",
-                     "achieved": round(gateup_bytes / (gateup_us * 1e3), 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s",
-                     "frac": round(gateup_bytes / (gateup_us * 1e3) / HBM_PEAK_GBPS, 4),
-                     "traffic": measured_traffic("moe_gateup_ksplit_kernel")[0],
-                     "traffic_source": measured_traffic("moe_gateup_ksplit_kernel")[1],
-                     "bytes_per_launch": gateup_bytes,
-                     "avg_launch_us": round(gateup_us, 3)},
-    }
-    if args.cpu_sample > 0:
-        log(f"[bench] timing the CPU oracle on {args.cpu_sample} tokens")
-        result["cpu_baseline"] = cpu_baseline_moe(banks[0], xs, logits, args.cpu_sample)
-    return result
-
-
-def run_klinear_decode(args, dev) -> dict:
-    from local_kimi_amd.checkpoint import MoeBanks
-    from local_kimi_amd.klinear import KLinearMoE
-
-    layers = args.layers
-    gen = torch.Generator(device=dev).manual_seed(20260729)
-    t0 = time.time()
-    master = (*make_bank(INTER, H, E_ROUTED + 1, gen, dev), *make_bank(INTER, H, E_ROUTED + 1, gen, dev),
-              *make_bank(H, INTER, E_ROUTED + 1, gen, dev))
-    mods = []
-    for l in range(layers):
-        b = master if l == 0 else tuple(t.clone() for t in master)
-        gate = (torch.randn((E_ROUTED, H), device=dev, generator=gen) * (1.0 / H ** 0.5)).to(torch.bfloat16)
-        bias = torch.randn((E_ROUTED,), device=dev, generator=gen) * 0.01
-        mods.append(KLinearMoE(gate, bias, MoeBanks(*b), top_k=TOP_K, routed_scaling_factor=SCALING))
-    xs = [(torch.randn((1, H), device=dev, generator=gen)).to(torch.bfloat16) for _ in range(layers)]
-    torch.cuda.synchronize()
-    log(f"[bench] {layers} KLinearMoE layers ready in {time.time() - t0:.1f}s")
-    stream = torch.cuda.Stream(device=dev)
-
-    def all_layers():
-        for l in range(layers):
-            mods[l](xs[l])
-
-    graph = capture(all_layers, stream)
-    steps = max(layers, (args.steps + layers - 1) // layers * layers)
-    warm = max(1, (args.warmup + layers - 1) // layers)
-    for _ in range(warm):
-        graph.replay()
-    torch.cuda.synchronize()
-    ms = time_graph(graph, steps // layers, stream)
-    us = ms * 1000.0 / steps
-    router_bytes = E_ROUTED * H * 2
-    step_bytes = (TOP_K + 1) * EXPERT_BYTES + TOKEN_IO_BYTES + router_bytes
-    log(f"[bench] KLinearMoE decode {us:.2f} us/token")
-    return {
-        "metric": "MoE-layer decode us/token + achieved HBM GB/s (% of peak) at W4A16",
-        "value": round(us, 3),
-        "unit": "us/token",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": warm * layers,
-        "ms_per_step": round(ms / steps, 6),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x, "
-                "N(0,1/H) bf16 router weights",
-        "config": {"workload": "klinear_moe_decode_batch1", "hidden": H, "routed_experts": E_ROUTED,
-                   "shared_experts": 1, "moe_intermediate": INTER, "top_k": TOP_K, "group_size": G,
-                   "tokens_per_step": 1, "layer_banks_rotated": layers,
-                   "router": "lk_router_logits (bf16 x, bf16 Wg [256, 2304], fp32 sums), then the MoE block"},
-        "achieved_gbps": round(step_bytes / (us * 1e3), 1),
-        "pct_hbm_peak": round(100.0 * step_bytes / (us * 1e3) / HBM_PEAK_GBPS, 2),
+    blk = time_graph(capture(block_all, stream), stream, LAYERS, plan)
+    gu = time_graph(capture(gateup_all, stream), stream, LAYERS, plan)
+    step_bytes = (TOP_K + 1) * EXPERT_BYTES + TOKEN_IO_BYTES
+    gu_bytes = (TOP_K + 1) * GATEUP_EXPERT_BYTES + H * 2 + E_ROUTED * 4 + (TOP_K + 1) * INTER * 2
+    traffic = measured_traffic("moe_gateup_ksplit_kernel")
+    log(f"[bench] config 2: block {blk['us']:.2f} us/token, gate/up kernel {gu['us']:.2f} us")
+    res = {
+        "value": round(blk["us"], 3), "unit": "us/token", "steps": blk["steps"],
+        "warmup": blk["warmup"], "ms_per_step": round(blk["us"] / 1000.0, 6),
+        "achieved_gbps": round(step_bytes / (blk["us"] * 1e3), 1),
+        "pct_hbm_peak": round(100.0 * step_bytes / (blk["us"] * 1e3) / HBM_PEAK_GBPS, 2),
         "algorithmic_bytes_per_step": step_bytes,
+        "roofline": {"kernel": "moe_gateup_ksplit_kernel (router + gate/up + SwiGLU, 9 routes)",
+                     "bound": "hbm", "achieved": round(gu_bytes / (gu["us"] * 1e3), 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gu_bytes / (gu["us"] * 1e3) / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic, "bytes_per_launch": gu_bytes,
+                     "avg_launch_us": round(gu["us"], 3)},
     }
+    if cpu:
+        log("[bench] config 2: CPU baseline")
+        res["cpu_baseline"] = cpu_baseline_block(banks[0], xs[0], logits[0], "w4a16", "us/token")
+    return res
 
 
-def run_dense(args, dev) -> dict:
+def run_dense(plan: Plan, dev, cpu: bool) -> dict:
+    """Config 1: dense GEMV x[1,2304] . W[9216,2304], 40 rotated copies (439 MB)."""
     from local_kimi_amd.kernels import w4a16_dense
     from local_kimi_amd.quant import quantise
 
-    copies = args.copies
-    gen = torch.Generator(device=dev).manual_seed(20260729)
-    w = (torch.randn((DENSE_N, H), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
-    enc = quantise(w, group_size=G)
-    weights = [(enc.packed.clone(), enc.scales.clone()) for _ in range(copies)]
+    gen = torch.Generator(device=dev).manual_seed(20260730)
+    enc = quantise((torch.randn((DENSE_N, H), device=dev, generator=gen) * 0.02)
+                   .to(torch.bfloat16), group_size=G)
+    weights = [(enc.packed.clone(), enc.scales.clone()) for _ in range(DENSE_COPIES)]
     x = torch.randn((1, H), device=dev, generator=gen).to(torch.bfloat16)
     stream = torch.cuda.Stream(device=dev)
 
@@ -301,287 +358,230 @@ def run_dense(args, dev) -> dict:
         for p, s in weights:
             w4a16_dense(x, p, s)
 
-    graph = capture(all_copies, stream)
-    steps = max(copies, (args.steps + copies - 1) // copies * copies)
-    warm = max(1, (args.warmup + copies - 1) // copies)
-    for _ in range(warm):
-        graph.replay()
-    ms = time_graph(graph, steps // copies, stream)
-    us = ms * 1000.0 / steps
+    t = time_graph(capture(all_copies, stream), stream, DENSE_COPIES, plan)
     nbytes = w4a16_bytes(DENSE_N, H) + H * 2 + DENSE_N * 2
-    result = {
-        "metric": "Dense W4A16 GEMV decode us/token + achieved HBM GB/s (% of peak)",
-        "value": round(us, 3), "unit": "us/token", "n_gpus": 1, "steps": steps,
-        "warmup": warm * copies, "ms_per_step": round(ms / steps, 6), "higher_is_better": False,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x",
-        "config": {"workload": "dense_gemv_decode", "m": 1, "n": DENSE_N, "k": H, "group_size": G,
-                   "weight_copies_rotated": copies},
-        "achieved_gbps": round(nbytes / (us * 1e3), 1),
-        "pct_hbm_peak": round(100.0 * nbytes / (us * 1e3) / HBM_PEAK_GBPS, 2),
+    log(f"[bench] config 1: dense GEMV {t['us']:.2f} us")
+    res = {
+        "metric": "Dense W4A16 GEMV decode us/call + HBM GB/s", "value": round(t["us"], 3),
+        "unit": "us/call", "steps": t["steps"], "warmup": t["warmup"],
+        "config": {"workload": "dense_gemv_decode", "m": 1, "n": DENSE_N, "k": H,
+                   "group_size": G, "weight_copies_rotated": DENSE_COPIES},
         "roofline": {"kernel": "dense_ksplit_kernel", "bound": "hbm",
-                     "achieved": round(nbytes / (us * 1e3), 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(nbytes / (us * 1e3) / HBM_PEAK_GBPS, 4),
-                     "traffic": measured_traffic("dense_ksplit_kernel")[0],
-                     "traffic_source": measured_traffic("dense_ksplit_kernel")[1],
-                     "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3)},
+                     "achieved": round(nbytes / (t["us"] * 1e3), 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(nbytes / (t["us"] * 1e3) / HBM_PEAK_GBPS, 4),
+                     "traffic": measured_traffic("dense_ksplit_kernel"),
+                     "bytes_per_launch": nbytes, "avg_launch_us": round(t["us"], 3)},
     }
-    if args.cpu_sample > 0:
-        result["cpu_baseline"] = cpu_baseline_dense(weights[0][0], weights[0][1], x, args.cpu_sample)
-    return result
+    if cpu:
+        threads = cpu_threads()
+        p, s, xh = enc.packed.cpu(), enc.scales.cpu(), x.cpu()
+        sec = cpu_median(lambda: cpu_linear(xh, cpu_dequant_w4a16(p, s)))
+        res["cpu_baseline"] = {
+            "value": round(sec * 1e6, 1), "unit": "us/call", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": "torch restatement: dequantise W [9216, 2304] to bf16 + F.linear fp32, "
+                      "the whole call, median of 10 after 3 warm-ups"}
+    return res
 
 
-def make_mx_bank(rows: int, cols: int, experts: int, gen: torch.Generator, dev):
-    from local_kimi_amd.quant import quantize_mxfp4
-
-    packed = torch.empty((experts, rows, cols // 2), dtype=torch.uint8, device=dev)
-    scale = torch.empty((experts, rows, cols // 32), dtype=torch.uint8, device=dev)
-    for e in range(experts):
-        w = (torch.randn((rows, cols), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
-        p, sc = quantize_mxfp4(w)
-        packed[e].copy_(p)
-        scale[e].copy_(sc)
-    return packed, scale
-
-
-MX_EXPERT_BYTES = 3 * (INTER * H // 2 + INTER * (H // 32))   # 3,760,128
-
-
-def _layer_banks(layers: int, gen: torch.Generator, dev, weights: str = "w4a16"):
-    mk = make_mx_bank if weights == "mxfp4" else make_bank
-    master = (*mk(INTER, H, E_ROUTED + 1, gen, dev), *mk(INTER, H, E_ROUTED + 1, gen, dev),
-              *mk(H, INTER, E_ROUTED + 1, gen, dev))
-    return [master] + [tuple(t.clone() for t in master) for _ in range(layers - 1)]
-
-
-def _block_fn(weights: str, path: str = "expert"):
-    from local_kimi_amd.kernels import mxfp4_moe_block, w4a16_moe_decode, w4a16_moe_forward
-
-    if weights == "mxfp4":
-        return mxfp4_moe_block
-    return w4a16_moe_forward if path == "expert" else w4a16_moe_decode
-
-
-def cpu_baseline_block(banks_l0, xs, logits, tokens: int, weights: str) -> dict:
-    """Oracle block for `tokens` tokens of the step on one host thread."""
-    from threadpoolctl import threadpool_limits
-
-    from oracle import moe as OM
-    from oracle import mxfp4 as OX
-
-    host = [t.cpu().numpy() if t.dtype == torch.uint8 else
-            t.cpu().view(torch.int16).numpy().view(np.uint16) for t in banks_l0]
-    x = xs[:tokens].cpu().view(torch.int16).numpy().view(np.uint16)
-    lg = logits[:tokens].cpu().numpy()
-    with threadpool_limits(1):
-        t0 = time.perf_counter()
-        if weights == "mxfp4":
-            OX.moe_block(x, lg, None, *host, top_k=TOP_K, routed_scaling_factor=SCALING)
-        else:
-            OM.moe_block(x, lg, None, *host, top_k=TOP_K, routed_scaling_factor=SCALING, group_size=G)
-        dt = time.perf_counter() - t0
-    return {"value": round(dt * 1e6 / tokens, 1), "unit": "us/token", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle of the MoE block ({weights}: router, dequantise the routed "
-                      f"experts, gate/up, SwiGLU, W2, combine) for {tokens} tokens of the step "
-                      "on one host thread"}
-
-
-MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
-EXPERT_FLOPS = 2 * 3 * INTER * H  # gate, up and down projections per routed row
-
-
-def run_moe_batched(args, dev) -> dict:
-    """Batched decode: M tokens per step, Zipf(1.1)-skewed routing (the block's path by default)."""
+def zipf_logits(rng, m: int):
     from local_kimi_amd.workloads import zipf_router_logits
-    from oracle import moe as OM
 
-    from local_kimi_amd.kernels.moe import MOE_EXPERT_MAJOR_MIN_TOKENS
+    return zipf_router_logits(rng, m, E_ROUTED)
 
-    m, layers = args.tokens, args.layers
-    path = args.moe_path
-    if path == "auto":  # the block's own choice
-        path = "expert" if m >= MOE_EXPERT_MAJOR_MIN_TOKENS or args.weights == "mxfp4" else "token"
-    gen = torch.Generator(device=dev).manual_seed(20260729)
-    rng = np.random.default_rng(20260729)
-    t0 = time.time()
-    banks = _layer_banks(layers, gen, dev, args.weights)
-    block = _block_fn(args.weights, path)
-    xs = [(torch.randn((m, H), device=dev, generator=gen)).to(torch.bfloat16) for _ in range(layers)]
-    host_logits = [zipf_router_logits(rng, m, E_ROUTED) for _ in range(layers)]
-    logits = [torch.from_numpy(lg).to(dev) for lg in host_logits]
-    unions = [len(np.unique(OM.route(lg, None, TOP_K)[0])) for lg in host_logits]
-    torch.cuda.synchronize()
-    log(f"[bench] {layers} layer banks ready in {time.time() - t0:.1f}s; distinct routed "
-        f"experts per layer: mean {np.mean(unions):.1f} (min {min(unions)}, max {max(unions)})")
+
+def run_moe_batched(plan: Plan, dev, banks, m: int, weights: str, cpu: bool) -> dict:
+    """Configs 3 and 5 (M = 64): M tokens per step, Zipf(1.1)-skewed routing."""
+    from local_kimi_amd.kernels import mxfp4_moe_block, w4a16_moe_block
+
+    block = mxfp4_moe_block if weights == "mxfp4" else w4a16_moe_block
+    gen = torch.Generator(device=dev).manual_seed(20260731 + m)
+    rng = np.random.default_rng(20260731 + m)
+    xs = [torch.randn((m, H), device=dev, generator=gen).to(torch.bfloat16) for _ in range(LAYERS)]
+    logits = [torch.from_numpy(zipf_logits(rng, m)).to(dev) for _ in range(LAYERS)]
+    unions = [int(torch.unique(cpu_router(lg.cpu())[0]).numel()) for lg in logits]
     stream = torch.cuda.Stream(device=dev)
 
     def all_layers():
+        for l in range(LAYERS):
+            block(xs[l], logits[l], None, *banks[l], TOP_K, SCALING)
+
+    t = time_graph(capture(all_layers, stream), stream, LAYERS, plan)
+    ebytes = MX_EXPERT_BYTES if weights == "mxfp4" else EXPERT_BYTES
+    step_bytes = float(np.mean([(u + 1) * ebytes for u in unions])) + m * TOKEN_IO_BYTES
+    gbps = step_bytes / (t["us"] * 1e3)
+    log(f"[bench] batched {weights} M={m}: {t['us']:.2f} us/step ({gbps:.0f} GB/s)")
+    res = {
+        "metric": f"Batched MoE decode us/step + HBM GB/s at {weights.upper()}",
+        "value": round(t["us"], 3), "unit": "us/step", "steps": t["steps"],
+        "warmup": t["warmup"], "us_per_token": round(t["us"] / m, 3),
+        "config": {"workload": f"moe_batched_decode_m{m}", "weights": weights,
+                   "tokens_per_step": m, "routing": "Zipf(1.1): log p + Gumbel",
+                   "mean_distinct_routed_experts": round(float(np.mean(unions)), 2)},
+        "roofline": {"kernel": "whole block (router, schedule, expert GEMMs, combine)",
+                     "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_step": int(step_bytes)},
+    }
+    if cpu:
+        log(f"[bench] batched {weights} M={m}: CPU baseline")
+        res["cpu_baseline"] = cpu_baseline_block(banks[0], xs[0], logits[0], weights, "us/step")
+    return res
+
+
+def run_moe_prefill(plan: Plan, dev, banks, weights: str, cpu: bool) -> dict:
+    """Configs 4 and 5: 2048 tokens x top-8 (+ shared) through one layer, N(0,1) logits."""
+    from local_kimi_amd.kernels import mxfp4_moe_block, w4a16_moe_block
+
+    block = mxfp4_moe_block if weights == "mxfp4" else w4a16_moe_block
+    m = PREFILL_TOKENS
+    layers = 4  # 4 x 0.94 GB of weights rotated: each step reads its layer from HBM
+    gen = torch.Generator(device=dev).manual_seed(20260733)
+    xs = [torch.randn((m, H), device=dev, generator=gen).to(torch.bfloat16) for _ in range(layers)]
+    logits = [torch.randn((m, E_ROUTED), device=dev, generator=gen) for _ in range(layers)]
+    stream = torch.cuda.Stream(device=dev)
+
+    def some_layers():
         for l in range(layers):
             block(xs[l], logits[l], None, *banks[l], TOP_K, SCALING)
 
-    graph = capture(all_layers, stream)
-    reps = max(1, args.steps // layers)
-    warm = max(1, args.warmup // layers)
-    for _ in range(warm):
-        graph.replay()
-    ms = time_graph(graph, reps, stream)
-    steps = reps * layers
-    us_step = ms * 1000.0 / steps
-    ebytes = MX_EXPERT_BYTES if args.weights == "mxfp4" else EXPERT_BYTES
-    step_bytes = float(np.mean([(u + 1) * ebytes for u in unions])) + m * TOKEN_IO_BYTES
-    step_flops = m * (TOP_K + 1) * EXPERT_FLOPS
-    gbps = step_bytes / (us_step * 1e3)
-    result = {
-        "metric": f"Batched MoE decode us/step + achieved HBM GB/s (% of peak) at {args.weights.upper()}",
-        "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": steps,
-        "warmup": warm * layers, "ms_per_step": round(ms / steps, 6), "higher_is_better": False,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": f"synthetic: N(0,0.02) weights quantised {_weights_desc(args.weights)} on the GPU, "
-                "N(0,1) x, Zipf(1.1) router logits (log p + Gumbel)",
-        "config": {"workload": f"moe_batched_decode_m{m}", "weights": args.weights,
-                   "path": f"{path}-major", "tokens_per_step": m, "hidden": H,
-                   "routed_experts": E_ROUTED, "shared_experts": 1, "moe_intermediate": INTER,
-                   "top_k": TOP_K, "layer_banks_rotated": layers,
-                   "mean_distinct_routed_experts": round(float(np.mean(unions)), 2)},
-        "us_per_token": round(us_step / m, 3),
-        "achieved_gbps": round(gbps, 1),
-        "pct_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
-        "algorithmic_bytes_per_step": int(step_bytes),
-        "roofline": {"kernel": (("whole block (router + schedule, gate/up GEMM, W2 + combine GEMV)"
-                                 if args.weights == "w4a16" and m <= 4 else
-                                 "whole block (router, schedule, gate/up GEMM, down GEMM, combine)")
-                                if path == "expert" else
-                                "whole block (router + gate/up GEMV, W2 + combine GEMV)"),
-                     "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "mfma_tflops": round(step_flops / (us_step * 1e6), 2)},
-    }
-    if args.cpu_sample > 0:
-        log(f"[bench] timing the CPU oracle on {min(args.cpu_sample, m)} tokens")
-        result["cpu_baseline"] = cpu_baseline_block(banks[0], xs[0], logits[0], min(args.cpu_sample, m),
-                                                    args.weights)
-    return result
-
-
-def _weights_desc(weights: str) -> str:
-    return "OCP MXFP4 (E2M1, E8M0 per 32)" if weights == "mxfp4" else "W4A16 g128"
-
-
-def run_moe_prefill(args, dev) -> dict:
-    """Prefill: 2048 tokens x top-8 (+ shared) through one layer, N(0,1) logits."""
-    m = args.prefill_tokens
-    gen = torch.Generator(device=dev).manual_seed(20260729)
-    banks = _layer_banks(2, gen, dev, args.weights)
-    block = _block_fn(args.weights)
-    xs = [(torch.randn((m, H), device=dev, generator=gen)).to(torch.bfloat16) for _ in range(2)]
-    logits = [torch.randn((m, E_ROUTED), device=dev, generator=gen) for _ in range(2)]
-    stream = torch.cuda.Stream(device=dev)
-
-    def both():
-        for l in range(2):
-            block(xs[l], logits[l], None, *banks[l], TOP_K, SCALING)
-
-    graph = capture(both, stream)
-    reps = max(1, args.prefill_steps // 2)
-    for _ in range(3):
-        graph.replay()
-    ms = time_graph(graph, reps, stream)
-    steps = 2 * reps
-    us = ms * 1000.0 / steps
-    ebytes = MX_EXPERT_BYTES if args.weights == "mxfp4" else EXPERT_BYTES
+    t = time_graph(capture(some_layers, stream), stream, layers, plan)
+    ebytes = MX_EXPERT_BYTES if weights == "mxfp4" else EXPERT_BYTES
     nbytes = (E_ROUTED + 1) * ebytes + m * TOKEN_IO_BYTES
     flops = m * (TOP_K + 1) * EXPERT_FLOPS
-    tflops = flops / (us * 1e6)
-    gbps = nbytes / (us * 1e3)
-    result = {
-        "metric": f"MoE prefill us/layer + MFMA TFLOP/s and HBM GB/s at {args.weights.upper()}",
-        "value": round(us, 2), "unit": "us/layer", "n_gpus": 1, "steps": steps, "warmup": 6,
-        "ms_per_step": round(ms / steps, 6), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16",
-        "data": f"synthetic: N(0,0.02) weights quantised {_weights_desc(args.weights)} on the GPU, "
-                "N(0,1) x and logits",
-        "config": {"workload": f"moe_prefill_{m}", "weights": args.weights, "tokens": m, "hidden": H,
-                   "routed_experts": E_ROUTED, "shared_experts": 1, "moe_intermediate": INTER,
-                   "top_k": TOP_K},
-        "tokens_per_s": round(m / (us * 1e-6), 1),
-        "achieved_gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
-        "achieved_tflops": round(tflops, 1),
-        "pct_mfma_peak": round(100 * tflops / MFMA_BF16_PEAK_TFLOPS, 2),
-        "algorithmic_bytes_per_step": nbytes, "flops_per_step": flops,
+    tflops = flops / (t["us"] * 1e6)
+    peak = FP4_PEAK_TFLOPS if weights == "mxfp4" else BF16_PEAK_TFLOPS
+    log(f"[bench] prefill {weights}: {t['us']:.1f} us/layer ({tflops:.0f} TFLOP/s)")
+    res = {
+        "metric": f"MoE prefill us/layer + MFMA TFLOP/s at {weights.upper()}",
+        "value": round(t["us"], 2), "unit": "us/layer", "steps": t["steps"],
+        "warmup": t["warmup"], "tokens_per_s": round(m / (t["us"] * 1e-6), 1),
+        "config": {"workload": f"moe_prefill_{m}", "weights": weights, "tokens": m,
+                   "routing": "N(0,1) logits"},
+        "achieved_gbps": round(nbytes / (t["us"] * 1e3), 1),
+        "pct_hbm_peak": round(100 * nbytes / (t["us"] * 1e3) / HBM_PEAK_GBPS, 2),
         "roofline": {"kernel": "whole block (router, schedule, gate/up GEMM, down GEMM, combine)",
-                     "bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "traffic": None, "hbm_gbps": round(gbps, 1)},
+                     "bound": "mfma", "achieved": round(tflops, 1), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(tflops / peak, 4), "traffic": None,
+                     "flops_per_step": flops,
+                     "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)},
     }
-    if args.cpu_sample > 0:
-        n = min(args.cpu_sample, m)
-        log(f"[bench] timing the CPU oracle on {n} tokens")
-        result["cpu_baseline"] = cpu_baseline_block(banks[0], xs[0], logits[0], n, args.weights)
-    return result
+    if cpu:
+        log(f"[bench] prefill {weights}: CPU baseline")
+        res["cpu_baseline"] = cpu_baseline_block(banks[0], xs[0], logits[0], weights, "us/layer")
+    return res
 
 
-def run_qkv_prefill(args, dev) -> dict:
-    """Fused QKV projection of 2048 tokens: [2048, 2304] x [2304, 3 x 4096] at W4A16."""
+def run_qkv_prefill(plan: Plan, dev, cpu: bool) -> dict:
+    """Config 4: fused QKV [2048, 2304] x [2304, 3 x 4096] at W4A16, one launch."""
     from local_kimi_amd.kernels import fused_qkv_w4a16
     from local_kimi_amd.quant import quantise
 
-    m, n = args.prefill_tokens, 4096
-    gen = torch.Generator(device=dev).manual_seed(20260729)
+    m, n = PREFILL_TOKENS, QKV_N
+    copies = 4
+    gen = torch.Generator(device=dev).manual_seed(20260734)
     mats = []
     for _ in range(3):
         enc = quantise((torch.randn((n, H), device=dev, generator=gen) * 0.02).to(torch.bfloat16),
                        group_size=G)
         mats += [enc.packed, enc.scales]
+    sets = [mats] + [[t.clone() for t in mats] for _ in range(copies - 1)]
     x = torch.randn((m, H), device=dev, generator=gen).to(torch.bfloat16)
     stream = torch.cuda.Stream(device=dev)
-    graph = capture(lambda: fused_qkv_w4a16(x, *mats), stream)
-    reps = max(1, args.prefill_steps)
-    for _ in range(3):
-        graph.replay()
-    ms = time_graph(graph, reps, stream)
-    us = ms * 1000.0 / reps
-    nbytes = 3 * w4a16_bytes(n, H) + m * H * 2 + 3 * m * n * 2
+
+    def all_sets():
+        for s in sets:
+            fused_qkv_w4a16(x, *s)
+
+    t = time_graph(capture(all_sets, stream), stream, copies, plan)
     flops = 2 * m * H * 3 * n
-    tflops = flops / (us * 1e6)
-    result = {
-        "metric": "Fused QKV prefill GEMM us + MFMA TFLOP/s at W4A16",
-        "value": round(us, 2), "unit": "us/call", "n_gpus": 1, "steps": reps, "warmup": 3,
-        "ms_per_step": round(ms / reps, 6), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x",
+    tflops = flops / (t["us"] * 1e6)
+    log(f"[bench] fused QKV: {t['us']:.1f} us ({tflops:.0f} TFLOP/s)")
+    res = {
+        "metric": "Fused QKV prefill GEMM us/call + MFMA TFLOP/s at W4A16",
+        "value": round(t["us"], 2), "unit": "us/call", "steps": t["steps"], "warmup": t["warmup"],
         "config": {"workload": f"qkv_prefill_{m}", "m": m, "n_per_projection": n, "k": H,
                    "group_size": G},
-        "achieved_tflops": round(tflops, 1),
-        "pct_mfma_peak": round(100 * tflops / MFMA_BF16_PEAK_TFLOPS, 2),
-        "achieved_gbps": round(nbytes / (us * 1e3), 1),
-        "algorithmic_bytes_per_step": nbytes, "flops_per_step": flops,
-        "roofline": {"kernel": "dense W4A16 GEMM (3 outputs, one launch)", "bound": "mfma",
-                     "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None},
+        "roofline": {"kernel": "w4a16_stream_kernel (dense, three outputs in one launch)",
+                     "bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None, "flops_per_launch": flops, "avg_launch_us": round(t["us"], 2)},
     }
-    if args.cpu_sample > 0:
-        from threadpoolctl import threadpool_limits
+    if cpu:
+        threads = cpu_threads()
+        host = [a.cpu() for a in mats]
+        rows = 256
+        xh = x[:rows].cpu()
+        deq = lambda: [cpu_dequant_w4a16(host[2 * j], host[2 * j + 1]) for j in range(3)]
+        ws = deq()
+        t_all = cpu_median(lambda: [cpu_linear(xh, w) for w in deq()])
+        t_gemm = cpu_median(lambda: [cpu_linear(xh, w) for w in ws])
+        sec = t_all + t_gemm * (m / rows - 1.0)
+        res["cpu_baseline"] = {
+            "value": round(sec * 1e6, 1), "unit": "us/call", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": f"torch restatement: dequantise the three [4096, 2304] matrices + F.linear "
+                      f"fp32 for {rows} of the {m} rows, timed; the F.linear part scaled by "
+                      f"{m}/{rows}; median of 10 after 3 warm-ups"}
+    return res
 
-        from oracle import w4a16 as OW
 
-        rows = min(args.cpu_sample, m)
-        host = [t.cpu().numpy() if t.dtype == torch.uint8 else
-                t.cpu().view(torch.int16).numpy().view(np.uint16) for t in mats]
-        xb = x[:rows].cpu().view(torch.int16).numpy().view(np.uint16)
-        with threadpool_limits(1):
-            t0 = time.perf_counter()
-            OW.fused_qkv(xb, *host, G)
-            dt = time.perf_counter() - t0
-        result["cpu_baseline"] = {
-            "value": round(dt * 1e6 / rows, 1), "unit": "us/token", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle fused QKV (dequantise 3 x [4096, 2304] + matmul) for {rows} "
-                      "rows on one host thread"}
-    return result
+def run_floor(plan: Plan, dev, banks) -> dict:
+    """Memory floors: empty-kernel launches, a streaming read of one dense
+    weight (11 MB) and of one batch-1 MoE layer's 27 matrices (33 MB)."""
+    from local_kimi_amd import _lib
+
+    lib = _lib.load()
+    stream = torch.cuda.Stream(device=dev)
+    sink = torch.zeros(256, dtype=torch.int32, device=dev)
+    s_ptr = stream.cuda_stream
+
+    def probe(regions):
+        ptrs = (ctypes.c_void_p * len(regions))(*[r.data_ptr() for r in regions])
+        sizes = (ctypes.c_int64 * len(regions))(*[r.numel() * r.element_size() for r in regions])
+        _lib.call("lk_probe_stream_read", ptrs, sizes, len(regions), sink.data_ptr(), s_ptr)
+
+    empty = time_graph(capture(lambda: [lib.lk_probe_empty(s_ptr) for _ in range(100)], stream),
+                       stream, 100, plan)
+    # one MoE layer's matrices: 9 experts x (gate, up, down) packed weights + scales, per layer
+    rng = np.random.default_rng(5)
+    layer_sets = []
+    for l in range(LAYERS):
+        experts = list(rng.choice(E_ROUTED, TOP_K, replace=False)) + [E_ROUTED]
+        regions = []
+        for e in experts:
+            for j in (0, 2, 4):
+                regions.append(banks[l][j][e])
+        layer_sets.append(regions)  # 27 packed matrices (scales are 3 % more)
+    layer_bytes = sum(r.numel() for r in layer_sets[0])
+    moe = time_graph(capture(lambda: [probe(r) for r in layer_sets], stream), stream, LAYERS, plan)
+    dense = [torch.empty(w4a16_bytes(DENSE_N, H), dtype=torch.uint8, device=dev).fill_(3)
+             for _ in range(DENSE_COPIES)]
+    den = time_graph(capture(lambda: [probe([d]) for d in dense], stream), stream,
+                     DENSE_COPIES, plan)
+    d_bytes = dense[0].numel()
+    log(f"[bench] floor: empty {empty['us']:.2f} us, 11 MB {den['us']:.2f} us, "
+        f"{layer_bytes / 1e6:.1f} MB in 27 regions {moe['us']:.2f} us")
+    return {"empty_kernel_us": round(empty["us"], 3),
+            "read_11MB_us": round(den["us"], 3), "read_11MB_bytes": d_bytes,
+            "read_11MB_gbps": round(d_bytes / (den["us"] * 1e3), 1),
+            "read_moe_layer_us": round(moe["us"], 3), "read_moe_layer_bytes": layer_bytes,
+            "read_moe_layer_gbps": round(layer_bytes / (moe["us"] * 1e3), 1),
+            "kernel": "stream_read_kernel (16-byte non-temporal loads, one launch per step)"}
 
 
-def run_copy(args, dev) -> dict:
+def measured_traffic(kernel: str):
+    """HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (profiles/traffic.json)."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            return int(json.load(f)["kernels"][kernel]["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def run_copy(dev) -> dict:
     """Plain device copy of a known size: calibrates the HBM byte counters."""
-    nbytes = args.copy_mb << 20
+    nbytes = 256 << 20
     src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -589,35 +589,49 @@ def run_copy(args, dev) -> dict:
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
-    reps = 10
-    for _ in range(reps):
+    for _ in range(10):
         dst.copy_(src)
     end.record()
     torch.cuda.synchronize()
-    us = start.elapsed_time(end) * 1000.0 / reps
-    return {"metric": "device copy (counter calibration)", "value": round(us, 2), "unit": "us/copy",
-            "bytes_read": nbytes, "bytes_written": nbytes, "gbps": round(2 * nbytes / (us * 1e3), 1)}
+    us = start.elapsed_time(end) * 100.0
+    return {"metric": "device copy (counter calibration)", "value": round(us, 2),
+            "unit": "us/copy", "bytes_read": nbytes, "bytes_written": nbytes}
+
+
+# ---------------------------------------------------------------------------
+
+
+def headline(plan: Plan, res: dict) -> dict:
+    out = {
+        "metric": METRIC, "value": res["value"], "unit": "us/token", "n_gpus": 1,
+        "steps": res["steps"], "warmup": res["warmup"], "steps_requested": plan.steps_requested,
+        "warmup_requested": plan.warmup_requested, "ms_per_step": res["ms_per_step"],
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x and logits",
+        "config": {"workload": "moe_decode_batch1", "hidden": H, "routed_experts": E_ROUTED,
+                   "shared_experts": 1, "moe_intermediate": INTER, "top_k": TOP_K,
+                   "group_size": G, "tokens_per_step": 1, "layer_banks_rotated": LAYERS,
+                   "launches_per_step": 2},
+    }
+    for key in ("achieved_gbps", "pct_hbm_peak", "algorithmic_bytes_per_step", "roofline",
+                "cpu_baseline"):
+        if key in res:
+            out[key] = res[key]
+    return out
 
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2600)
-    ap.add_argument("--warmup", type=int, default=260)
-    ap.add_argument("--workload", default="moe_decode",
-                    choices=["moe_decode", "dense_decode", "moe_batched", "moe_prefill",
-                             "qkv_prefill", "klinear_decode", "copy"])
+    ap.add_argument("--steps", type=int, default=520)
+    ap.add_argument("--warmup", type=int, default=52)
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "moe_decode", "dense_decode", "moe_batched", "moe_prefill",
+                             "qkv_prefill", "stream_floor", "klinear_decode", "copy"])
     ap.add_argument("--tokens", type=int, default=64, help="moe_batched tokens per step")
-    ap.add_argument("--moe-path", choices=["auto", "expert", "token"], default="auto",
-                    help="moe_batched: the block's choice, expert-major GEMMs or token-major GEMVs")
     ap.add_argument("--weights", choices=["w4a16", "mxfp4"], default="w4a16",
                     help="moe_batched / moe_prefill expert weight format")
-    ap.add_argument("--prefill-tokens", type=int, default=2048)
-    ap.add_argument("--prefill-steps", type=int, default=40)
-    ap.add_argument("--copy-mb", type=int, default=256, help="copy workload size (MiB)")
-    ap.add_argument("--layers", type=int, default=26, help="MoE layer banks rotated")
-    ap.add_argument("--copies", type=int, default=40, help="dense weight copies rotated")
-    ap.add_argument("--cpu-sample", type=int, default=4, help="tokens for the CPU oracle baseline (0: skip)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
@@ -630,13 +644,87 @@ def main() -> int:
 
     _lib.load()
     dev = torch.device("cuda:0")
-    log(f"[bench] device {torch.cuda.get_device_name(0)}, workload {args.workload}")
-    runners = {"moe_decode": run_moe, "dense_decode": run_dense, "moe_batched": run_moe_batched,
-               "moe_prefill": run_moe_prefill, "qkv_prefill": run_qkv_prefill,
-               "klinear_decode": run_klinear_decode, "copy": run_copy}
-    result = runners[args.workload](args, dev)
-    print(json.dumps(result), flush=True)
+    plan = Plan(args.steps, args.warmup)
+    cpu = not args.no_cpu
+    log(f"[bench] device {torch.cuda.get_device_name(0)}, workload {args.workload}, "
+        f"steps requested {args.steps}, warm-up requested {args.warmup}")
+    t0 = time.time()
+    w4 = None
+    needs_w4a16 = args.workload in ("all", "moe_decode", "stream_floor", "klinear_decode") or (
+        args.workload in ("moe_batched", "moe_prefill") and args.weights == "w4a16")
+    if needs_w4a16:
+        w4 = layer_banks("w4a16", torch.Generator(device=dev).manual_seed(20260729), dev)
+        torch.cuda.synchronize()
+        log(f"[bench] {LAYERS} W4A16 layer banks ready in {time.time() - t0:.1f}s")
+
+    if args.workload == "all":
+        res = headline(plan, run_moe_decode(plan, dev, w4, cpu))
+        configs = {"1_dense_gemv": run_dense(plan, dev, cpu)}
+        for m in (4, 16, 64):
+            configs[f"3_batched_m{m}"] = run_moe_batched(plan, dev, w4, m, "w4a16", cpu)
+        configs["4_moe_prefill"] = run_moe_prefill(plan, dev, w4, "w4a16", cpu)
+        configs["4_qkv_prefill"] = run_qkv_prefill(plan, dev, cpu)
+        res["floor"] = run_floor(plan, dev, w4)
+        del w4
+        torch.cuda.empty_cache()
+        mx = layer_banks("mxfp4", torch.Generator(device=dev).manual_seed(20260735), dev)
+        configs["5_mxfp4_batched_m64"] = run_moe_batched(plan, dev, mx, 64, "mxfp4", cpu)
+        configs["5_mxfp4_prefill"] = run_moe_prefill(plan, dev, mx, "mxfp4", cpu)
+        res["configs"] = configs
+        floor = res["floor"]
+        res["roofline"]["frac_of_measured_floor"] = round(
+            floor["read_moe_layer_us"] / res["value"], 4)
+        configs["1_dense_gemv"]["roofline"]["frac_of_measured_floor"] = round(
+            floor["read_11MB_us"] / configs["1_dense_gemv"]["value"], 4)
+    elif args.workload == "moe_decode":
+        res = headline(plan, run_moe_decode(plan, dev, w4, cpu))
+    elif args.workload == "dense_decode":
+        res = run_dense(plan, dev, cpu)
+    elif args.workload == "moe_batched":
+        banks = w4 if args.weights == "w4a16" else layer_banks(
+            "mxfp4", torch.Generator(device=dev).manual_seed(20260735), dev)
+        res = run_moe_batched(plan, dev, banks, args.tokens, args.weights, cpu)
+    elif args.workload == "moe_prefill":
+        banks = w4 if args.weights == "w4a16" else layer_banks(
+            "mxfp4", torch.Generator(device=dev).manual_seed(20260735), dev, layers=4)
+        res = run_moe_prefill(plan, dev, banks, args.weights, cpu)
+    elif args.workload == "qkv_prefill":
+        res = run_qkv_prefill(plan, dev, cpu)
+    elif args.workload == "stream_floor":
+        res = run_floor(plan, dev, w4)
+    elif args.workload == "klinear_decode":
+        res = run_klinear_decode(plan, dev, w4)
+    else:
+        res = run_copy(dev)
+    res["bench_seconds"] = round(time.time() - t0, 1)
+    print(json.dumps(res), flush=True)
     return 0
+
+
+def run_klinear_decode(plan: Plan, dev, banks) -> dict:
+    """The model-slice caller: KLinearMoE (router logits x Wg^T, then the block)."""
+    from local_kimi_amd.checkpoint import MoeBanks
+    from local_kimi_amd.klinear import KLinearMoE
+
+    gen = torch.Generator(device=dev).manual_seed(20260736)
+    mods = []
+    for l in range(LAYERS):
+        gate = (torch.randn((E_ROUTED, H), device=dev, generator=gen) * H ** -0.5).to(torch.bfloat16)
+        bias = torch.randn((E_ROUTED,), device=dev, generator=gen) * 0.01
+        mods.append(KLinearMoE(gate, bias, MoeBanks(*banks[l]), top_k=TOP_K,
+                               routed_scaling_factor=SCALING))
+    xs = [torch.randn((1, H), device=dev, generator=gen).to(torch.bfloat16) for _ in range(LAYERS)]
+    stream = torch.cuda.Stream(device=dev)
+
+    def all_layers():
+        for l in range(LAYERS):
+            mods[l](xs[l])
+
+    t = time_graph(capture(all_layers, stream), stream, LAYERS, plan)
+    step_bytes = (TOP_K + 1) * EXPERT_BYTES + TOKEN_IO_BYTES + E_ROUTED * H * 2
+    return {"metric": "KLinearMoE decode us/token (router logits + MoE block)",
+            "value": round(t["us"], 3), "unit": "us/token", "steps": t["steps"],
+            "warmup": t["warmup"], "achieved_gbps": round(step_bytes / (t["us"] * 1e3), 1)}
 
 
 if __name__ == "__main__":
