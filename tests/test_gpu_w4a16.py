@@ -309,6 +309,63 @@ def test_router_selection_is_bit_exact(rng, e, k):
         np.testing.assert_allclose(w.cpu().numpy(), ew, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("experts,top_k", [(256, 8), (256, 1), (200, 6), (64, 8), (9, 8),
+                                           (8, 8), (256, 3)])
+def test_router_many_tokens_bit_exact(rng, experts, top_k):
+    """Up to 256 experts and top_k <= 8 select by merging sorted lists across
+    the wave; a token whose boundary is closer than the merge keys resolve
+    takes the exact rounds. 4096 tokens, with and without a bias, against the
+    oracle: selections bit-exact, weights within 2e-6."""
+    from local_kimi_amd.kernels import moe_router
+
+    logits = rng.normal(0, 1, (4096, experts)).astype(np.float32)
+    bias = rng.normal(0, 0.05, experts).astype(np.float32)
+    for b in (None, bias):
+        idx, w = moe_router(torch.from_numpy(logits).to(DEV),
+                            None if b is None else torch.from_numpy(b).to(DEV), top_k,
+                            routed_scaling_factor=2.446)
+        eidx, ew = OM.route(logits, b, top_k, routed_scaling_factor=2.446)
+        assert np.array_equal(idx.cpu().numpy(), eidx)
+        np.testing.assert_allclose(w.cpu().numpy(), ew, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("step_ulps", [1, 3, 256, 512])
+def test_router_boundary_near_ties(rng, step_ulps):
+    """Candidates with logit 0 (sigmoid exactly 0.5 on every side) whose bias
+    puts their choice scores a multiple of `step_ulps` ulps apart, others far
+    below: at 1 and 3 ulps the candidates agree in the merge keys' high 24 bits
+    and the exact rounds decide (including exact ties, to the lower id); at 256
+    and 512 ulps the merge selection is exact by itself."""
+    from local_kimi_amd.kernels import moe_router
+
+    tokens, experts = 96, 256
+    ulp = np.float32(2.0 ** -24)  # spacing of floats in [0.5, 1)
+    bias = ((np.arange(experts) % 12) * step_ulps * ulp).astype(np.float32)
+    tied = np.arange(0, experts - 1, 5)
+    bias[tied] = bias[tied + 1]  # exact ties too
+    logits = np.full((tokens, experts), -6.0, dtype=np.float32)
+    for t in range(tokens):
+        logits[t, rng.choice(experts, size=12, replace=False)] = 0.0
+    idx, w = moe_router(torch.from_numpy(logits).to(DEV), torch.from_numpy(bias).to(DEV), 8,
+                        routed_scaling_factor=2.446)
+    eidx, ew = OM.route(logits, bias, 8, routed_scaling_factor=2.446)
+    assert np.array_equal(idx.cpu().numpy(), eidx)
+    np.testing.assert_allclose(w.cpu().numpy(), ew, rtol=2e-6, atol=1e-7)
+
+
+def test_router_saturated_scores_tie_to_the_lower_id(rng):
+    """Logits >= 40: every sigmoid is exactly 1.0, so the top 8 are the lowest
+    ids among them."""
+    from local_kimi_amd.kernels import moe_router
+
+    logits = rng.normal(0, 1, (32, 256)).astype(np.float32)
+    for t in range(32):
+        logits[t, rng.choice(256, size=11, replace=False)] = 40.0 + t
+    idx, _ = moe_router(torch.from_numpy(logits).to(DEV), None, 8)
+    eidx, _ = OM.route(logits, None, 8)
+    assert np.array_equal(idx.cpu().numpy(), eidx)
+
+
 def test_router_kat_and_ties():
     from local_kimi_amd.kernels import moe_router
 
