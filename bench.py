@@ -450,7 +450,10 @@ def run_moe_prefill(plan: Plan, dev, banks, weights: str, cpu: bool) -> dict:
     nbytes = (E_ROUTED + 1) * ebytes + m * TOKEN_IO_BYTES
     flops = m * (TOP_K + 1) * EXPERT_FLOPS
     tflops = flops / (t["us"] * 1e6)
-    peak = FP4_PEAK_TFLOPS if weights == "mxfp4" else BF16_PEAK_TFLOPS
+    # the default forms of both formats multiply on bf16 MFMA (MXFP4 weights
+    # decoded by the scaled convert), so the bf16 peak is the bound; the fp4
+    # one is also reported
+    peak = BF16_PEAK_TFLOPS
     log(f"[bench] prefill {weights}: {t['us']:.1f} us/layer ({tflops:.0f} TFLOP/s)")
     res = {
         "metric": f"MoE prefill us/layer + MFMA TFLOP/s at {weights.upper()}",
@@ -464,7 +467,7 @@ def run_moe_prefill(plan: Plan, dev, banks, weights: str, cpu: bool) -> dict:
                      "bound": "mfma", "achieved": round(tflops, 1), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(tflops / peak, 4), "traffic": None,
                      "flops_per_step": flops,
-                     "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)},
+                     "frac_of_fp4_peak": round(tflops / FP4_PEAK_TFLOPS, 4)},
     }
     if cpu:
         log(f"[bench] prefill {weights}: CPU baseline")
@@ -632,6 +635,9 @@ def main() -> int:
     ap.add_argument("--weights", choices=["w4a16", "mxfp4"], default="w4a16",
                     help="moe_batched / moe_prefill expert weight format")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--path", action="append", default=[], metavar="KNOB=CHOICE",
+                    help="force one of the library's kernel forms (lk_set_path), e.g. "
+                         "mxfp4_mfma=bf16; repeatable")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
@@ -643,6 +649,15 @@ def main() -> int:
     from local_kimi_amd import _lib
 
     _lib.load()
+    forced = {}
+    for item in args.path:
+        knob, sep, choice = item.partition("=")
+        if not sep or knob not in _lib.PATH_KNOBS or choice not in _lib.PATH_KNOBS[knob]:
+            print(f"--path takes KNOB=CHOICE with a knob and choice of {_lib.PATH_KNOBS}; "
+                  f"got {item!r}", file=sys.stderr)
+            return 2
+        _lib.set_path(knob, choice)
+        forced[knob] = choice
     dev = torch.device("cuda:0")
     plan = Plan(args.steps, args.warmup)
     cpu = not args.no_cpu
@@ -696,6 +711,8 @@ def main() -> int:
         res = run_klinear_decode(plan, dev, w4)
     else:
         res = run_copy(dev)
+    if forced:
+        res["forced_paths"] = forced
     res["bench_seconds"] = round(time.time() - t0, 1)
     print(json.dumps(res), flush=True)
     return 0

@@ -2236,18 +2236,14 @@ int stream_fmt(bool mx, const GemmArgs& g, Mode mode, int64_t tiles, int mt, hip
 // LDS-staged kernel instead, moe_gemm=stream16|stream64 forces a tile height.
 constexpr int64_t kStreamSmallEntries = 2048;
 
-// Which MFMA form the MXFP4 expert GEMMs take. The scaled fp4 MFMA (raw fp4
-// weights, activations split into fp8 hi + lo) wins on 64-row prefill tiles
-// (782 vs 831 us for a 2048-token Kimi-Linear layer); on 16-row decode tiles
-// the GEMMs are weight-bandwidth bound and bf16 MFMA on decoded weights is
-// faster (175 vs 198 us at 64 tokens: no split launches, fewer registers).
-// The path knob mxfp4_mfma=fp4 or =bf16 forces one form for every tile height.
-bool mxfp4_scaled_mfma(int mt) {
-  const int c = path_choice(kKnobMxfp4Mfma);
-  if (c == 2) return false;
-  if (c == 1) return true;
-  return mt == 4;
-}
+// Which MFMA form the MXFP4 expert GEMMs take: bf16 MFMA on weights decoded
+// by the scaled convert unless the path knob mxfp4_mfma=fp4 asks for the
+// scaled fp4 MFMA (raw fp4 weights, activations split into fp8 hi + lo). The
+// split keeps bf16 precision but takes two scaled MFMAs per 128-wide k-step,
+// the same MFMA time as four bf16 ones, plus two split launches: a 2048-token
+// Kimi-Linear layer measured 581 us in the bf16 form against 620 us, and 64
+// tokens 145 against 196 us.
+bool mxfp4_scaled_mfma() { return path_choice(kKnobMxfp4Mfma) == 1; }
 
 // 16-row tiles -> 1, 64-row tiles -> 4, the LDS-staged kernel -> 0.
 int stream_tile_mt(int64_t entries) {
@@ -2628,7 +2624,7 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   }
 
   // MXFP4 on the scaled fp4 MFMA: x and the activations go in as fp8 hi + lo
-  const bool f8 = mx && mt != 0 && h % 128 == 0 && i % 128 == 0 && mxfp4_scaled_mfma(mt);
+  const bool f8 = mx && mt != 0 && h % 128 == 0 && i % 128 == 0 && mxfp4_scaled_mfma();
   SplitBufs xs{}, as{};
   if (f8) {
     xs = split_bufs(ws + l.x_split, tokens * h);

@@ -9,11 +9,11 @@ matrix cores with fp32 accumulation.
 
 Grouped banks stack experts on a leading axis; the MoE block is the
 Kimi-Linear SwiGLU block of :mod:`.moe` with MXFP4 banks (shared expert
-last). At prefill sizes its expert GEMMs run on the gfx950 scaled fp4 MFMA:
-raw E2M1 weights with their E8M0 exponents, activations split into fp8 hi +
-lo (:func:`split_activations_fp8`) so the product keeps bf16 activation
-precision; decode sizes (bandwidth bound) use bf16 MFMA on decoded weights
-(the path knob ``mxfp4_mfma=fp4|bf16`` forces one form).
+last). Its expert GEMMs run bf16 MFMA on weights decoded by the scaled
+convert; the path knob ``mxfp4_mfma=fp4`` selects the gfx950 scaled fp4 MFMA
+instead (raw E2M1 weights with their E8M0 exponents, activations split into
+fp8 hi + lo by :func:`split_activations_fp8` so the product keeps bf16
+activation precision), which measured slower at every batch size.
 ``mxfp4_expert_mlp`` is the K3 packed expert with SiTU
 (engine/kernels/moe_grouped.py:163-194).
 """

@@ -361,7 +361,7 @@ def test_prefill_every_token_matches_oracle(designed_mx_prefill, form):
     from local_kimi_amd.kernels import mxfp4_moe_block
 
     x, logits, banks, counts, ey, eidx = designed_mx_prefill
-    with forced_path("mxfp4_mfma", "bf16" if form == "bf16" else "auto"):
+    with forced_path("mxfp4_mfma", "bf16" if form == "bf16" else "fp4"):
         y, idx, _ = mxfp4_moe_block(_dev(x), _dev(logits), None, *banks, 8, 2.446)
     assert np.array_equal(idx.cpu().numpy(), eidx)
     assert np.array_equal(np.bincount(idx.cpu().numpy().reshape(-1), minlength=counts.size),
