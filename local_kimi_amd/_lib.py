@@ -62,6 +62,11 @@ SIGNATURES: dict[str, list] = {
                              _I64, _I64, _I64, _I64, _I64, _F, _I, _P],
     "lk_mxfp4_expert_mlp": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _P],
     "lk_mxfp4_split_activations": [_P, _P, _P, _P, _I64, _I64, _P],
+    "lk_kda_decode_step": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _P],
+    "lk_kda_short_conv_triple": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
+                                 _I, _I, _P],
+    "lk_kda_gates": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _I, _I,
+                     _I, _P],
     "lk_probe_stream_read": [_P, _P, _I, _P, _P],
     "lk_probe_empty": [_P],
 }

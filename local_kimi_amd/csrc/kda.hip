@@ -1,0 +1,332 @@
+// Kimi Delta Attention decode kernels for gfx950: the recurrent-state step
+// (engine/kernels/kda_step.py) and its launch-fused preparation, the three
+// width-4 short convolutions and the gates (engine/kernels/kda_prepare.py).
+//
+// All three are small and memory- or latency-bound at decode: the step reads
+// and writes each head's d_k x d_v fp32 state once (2 MB each way for 32
+// heads of 128 x 128), the preparation touches a few KB per token.
+
+#include "lk_common.hpp"
+#include "lk_kda.h"
+
+namespace lk {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Recurrence step. Block = (batch * head, tile of 32 value columns), 256
+// threads: thread t owns columns c0 + 4 * (t & 7) .. + 3 (one 16-byte load per
+// row, eight threads per 128-byte row segment) and key rows
+// (t >> 3) + 32 p, p < P. The state tile is loaded once into registers,
+// decayed, its prediction S^T k reduced over the 32 row groups (three xor
+// shuffles inside a wave, then the four waves through LDS in wave order),
+// updated with the delta, reduced again for the output, and stored once.
+constexpr int kStepThreads = 256;
+constexpr int kStepCols = 32;
+constexpr int kStepRowGroups = kStepThreads / (kStepCols / 4);  // 32
+
+// Sums of v[0..3] over the 32 row groups of the block for this thread's
+// column group; every thread of the column group gets the same values (fixed
+// order: three xor shuffles, then waves 0..3).
+__device__ inline void row_group_sum4(float (&v)[4], float (*red)[kStepCols]) {
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int cg = threadIdx.x & 7;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {  // lanes 8 apart hold the same columns
+    v[c] += __shfl_xor(v[c], 8);
+    v[c] += __shfl_xor(v[c], 16);
+    v[c] += __shfl_xor(v[c], 32);
+  }
+  __syncthreads();  // the previous use of red is over
+  if (lane < 8) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) red[wave][cg * 4 + c] = v[c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    v[c] = ((red[0][cg * 4 + c] + red[1][cg * 4 + c]) + red[2][cg * 4 + c]) + red[3][cg * 4 + c];
+}
+
+template <int P>
+__global__ void __launch_bounds__(kStepThreads)
+kda_step_kernel(float* __restrict__ state, const float* __restrict__ q,
+                const float* __restrict__ k, const float* __restrict__ v,
+                const float* __restrict__ decay, const float* __restrict__ beta,
+                float* __restrict__ out, int dk, int dv, float scale) {
+  __shared__ float red[kStepThreads / kWave][kStepCols];
+  const int64_t bh = blockIdx.y;
+  const int cg = threadIdx.x & 7;
+  const int rg = threadIdx.x >> 3;
+  const int c0 = blockIdx.x * kStepCols + cg * 4;
+  float* const s_head = state + bh * dk * dv;
+  const float* const kh = k + bh * dk;
+  const float* const qh = q + bh * dk;
+  const float* const dh = decay + bh * dk;
+  bool col_ok[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) col_ok[c] = c0 + c < dv;
+  const bool vec = (dv & 3) == 0 && c0 + 3 < dv;
+
+  // the state rows of this thread, decayed; the key and query rows
+  float s[P][4], kr[P], qr[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int i = rg + kStepRowGroups * p;
+    const bool row_ok = i < dk;
+    const int ic = row_ok ? i : 0;
+    const float* row = s_head + static_cast<int64_t>(ic) * dv;
+    if (vec) {
+      const float4 x = *reinterpret_cast<const float4*>(row + c0);
+      s[p][0] = x.x;
+      s[p][1] = x.y;
+      s[p][2] = x.z;
+      s[p][3] = x.w;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) s[p][c] = col_ok[c] ? row[c0 + c] : 0.f;
+    }
+    const float g = row_ok ? expf(dh[ic]) : 0.f;
+    kr[p] = row_ok ? kh[ic] : 0.f;
+    qr[p] = row_ok ? qh[ic] * scale : 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s[p][c] *= g;
+  }
+  const float b = beta[bh];
+  float vc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) vc[c] = col_ok[c] ? v[bh * dv + c0 + c] : 0.f;
+
+  // prediction S^T k for the four columns, then the delta
+  float delta[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float part = 0.f;
+#pragma unroll
+    for (int p = 0; p < P; ++p) part = fmaf(s[p][c], kr[p], part);
+    delta[c] = part;
+  }
+  row_group_sum4(delta, red);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) delta[c] = vc[c] - delta[c];
+  // S += beta * k * delta^T; output S^T (q * scale)
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const float bk = b * kr[p];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s[p][c] = fmaf(bk, delta[c], s[p][c]);
+  }
+  float o[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float part = 0.f;
+#pragma unroll
+    for (int p = 0; p < P; ++p) part = fmaf(s[p][c], qr[p], part);
+    o[c] = part;
+  }
+  row_group_sum4(o, red);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int i = rg + kStepRowGroups * p;
+    if (i >= dk) continue;
+    float* row = s_head + static_cast<int64_t>(i) * dv;
+    if (vec) {
+      *reinterpret_cast<float4*>(row + c0) = make_float4(s[p][0], s[p][1], s[p][2], s[p][3]);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (col_ok[c]) row[c0 + c] = s[p][c];
+    }
+  }
+  if (rg == 0) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (col_ok[c]) out[bh * dv + c0 + c] = o[c];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// storage dtypes of the preparation kernels
+
+__device__ inline float load_value(const void* p, int64_t i, int dtype) {
+  if (dtype == LK_DTYPE_F32) return static_cast<const float*>(p)[i];
+  const uint16_t b = static_cast<const uint16_t*>(p)[i];
+  if (dtype == LK_DTYPE_BF16) return bf16_to_f32(b);
+  return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+
+__device__ inline void store_value(void* p, int64_t i, float x, int dtype) {
+  if (dtype == LK_DTYPE_F32) {
+    static_cast<float*>(p)[i] = x;
+  } else if (dtype == LK_DTYPE_BF16) {
+    static_cast<uint16_t*>(p)[i] = f32_to_bf16(x);
+  } else {
+    static_cast<uint16_t*>(p)[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Short convolutions: one thread per (convolution, batch row, channel); grid
+// (channel blocks, batch, 3). The window's products are accumulated in window
+// order, as the reference kernel sums them; the state values are stored back
+// from their exact fp32 images, so the shifted state is bit-identical to the
+// inputs.
+constexpr int kConvThreads = 256;
+
+struct ConvArgs {
+  const void* in[3];
+  void* state[3];
+  const void* weight[3];
+  void* out[3];
+};
+
+__global__ void __launch_bounds__(kConvThreads)
+short_conv_kernel(const ConvArgs a, int64_t channels, int vdt, int wdt) {
+  const int conv = blockIdx.z;
+  const int64_t b = blockIdx.y;
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * kConvThreads + threadIdx.x;
+  if (ch >= channels) return;
+  const int64_t si = (b * channels + ch) * 4;
+  const float s1 = load_value(a.state[conv], si + 1, vdt);
+  const float s2 = load_value(a.state[conv], si + 2, vdt);
+  const float s3 = load_value(a.state[conv], si + 3, vdt);
+  const float token = load_value(a.in[conv], b * channels + ch, vdt);
+  const float w0 = load_value(a.weight[conv], ch * 4 + 0, wdt);
+  const float w1 = load_value(a.weight[conv], ch * 4 + 1, wdt);
+  const float w2 = load_value(a.weight[conv], ch * 4 + 2, wdt);
+  const float w3 = load_value(a.weight[conv], ch * 4 + 3, wdt);
+  float acc = s1 * w0;
+  acc += s2 * w1;
+  acc += s3 * w2;
+  acc += token * w3;
+  store_value(a.out[conv], b * channels + ch, acc / (1.0f + expf(-acc)), vdt);
+  store_value(a.state[conv], si + 0, s1, vdt);
+  store_value(a.state[conv], si + 1, s2, vdt);
+  store_value(a.state[conv], si + 2, s3, vdt);
+  store_value(a.state[conv], si + 3, token, vdt);
+}
+
+// ---------------------------------------------------------------------------
+// Gates: one wave per (row, head). Lane l takes elements l, l + 64, ...; the
+// squared norms are summed per lane in element order, then across the wave
+// by a fixed butterfly.
+constexpr int kGateWaves = 4;
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+__device__ inline float softplus_f32(float x) {
+  // x above the threshold passes through (torch's and the reference kernel's
+  // 20); below it the stable form max(x, 0) + log1p(exp(-|x|))
+  return x > 20.0f ? x : fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+}
+
+__global__ void __launch_bounds__(kGateWaves * kWave)
+kda_gates_kernel(const void* __restrict__ raw_decay, const float* __restrict__ dt_bias,
+                 const float* __restrict__ a_log, const void* __restrict__ raw_beta,
+                 const void* __restrict__ q, const void* __restrict__ k,
+                 float* __restrict__ decay, float* __restrict__ beta,
+                 float* __restrict__ q_out, float* __restrict__ k_out, int64_t programs,
+                 int heads, int dim, float eps, int ddt, int bdt, int qdt) {
+  const int64_t prog = static_cast<int64_t>(blockIdx.x) * kGateWaves + threadIdx.x / kWave;
+  if (prog >= programs) return;  // wave-uniform
+  const int lane = threadIdx.x & (kWave - 1);
+  const int h = static_cast<int>(prog % heads);
+  const int64_t base = prog * dim;
+  const float rate = expf(a_log[h]);
+  float qs = 0.f, ks = 0.f;
+  for (int d = lane; d < dim; d += kWave) {
+    const float biased = load_value(raw_decay, base + d, ddt) + dt_bias[h * dim + d];
+    decay[base + d] = -rate * softplus_f32(biased);
+    const float qv = load_value(q, base + d, qdt);
+    const float kv = load_value(k, base + d, qdt);
+    qs = fmaf(qv, qv, qs);
+    ks = fmaf(kv, kv, ks);
+  }
+  const float qn = 1.0f / sqrtf(wave_sum(qs) + eps);
+  const float kn = 1.0f / sqrtf(wave_sum(ks) + eps);
+  for (int d = lane; d < dim; d += kWave) {
+    q_out[base + d] = load_value(q, base + d, qdt) * qn;
+    k_out[base + d] = load_value(k, base + d, qdt) * kn;
+  }
+  if (lane == 0) beta[prog] = 1.0f / (1.0f + expf(-load_value(raw_beta, prog, bdt)));
+}
+
+bool valid_dtype(int d) { return d == LK_DTYPE_F32 || d == LK_DTYPE_F16 || d == LK_DTYPE_BF16; }
+
+}  // namespace
+}  // namespace lk
+
+using namespace lk;
+
+extern "C" {
+
+int lk_kda_decode_step(float* state, const float* q, const float* k, const float* v,
+                       const float* decay, const float* beta, float* out, int64_t batch,
+                       int64_t heads, int64_t d_k, int64_t d_v, float scale, void* stream) {
+  LK_REQUIRE(batch > 0 && heads > 0 && d_k > 0 && d_v > 0, "KDA decode dimensions must be nonzero");
+  LK_REQUIRE(d_k <= 256, "KDA decode step supports d_k up to 256, got %lld", (long long)d_k);
+  LK_REQUIRE(batch * heads <= 65535, "at most 65535 batch x heads per call");
+  LK_REQUIRE(d_v <= (int64_t{1} << 20), "d_v too large");
+  LK_REQUIRE(state && q && k && v && decay && beta && out, "null pointer argument");
+  LK_REQUIRE(reinterpret_cast<uintptr_t>(state) % 16 == 0, "state must be 16-byte aligned");
+  dim3 grid(static_cast<unsigned>((d_v + kStepCols - 1) / kStepCols),
+            static_cast<unsigned>(batch * heads));
+  hipStream_t s = as_stream(stream);
+  const int dk = static_cast<int>(d_k), dv = static_cast<int>(d_v);
+  if (d_k <= 128)
+    kda_step_kernel<4><<<grid, kStepThreads, 0, s>>>(state, q, k, v, decay, beta, out, dk, dv,
+                                                      scale);
+  else
+    kda_step_kernel<8><<<grid, kStepThreads, 0, s>>>(state, q, k, v, decay, beta, out, dk, dv,
+                                                      scale);
+  return check_launch("lk_kda_decode_step");
+}
+
+int lk_kda_short_conv_triple(const void* q_in, const void* k_in, const void* v_in,
+                             void* q_state, void* k_state, void* v_state, const void* q_weight,
+                             const void* k_weight, const void* v_weight, void* q_out,
+                             void* k_out, void* v_out, int64_t batch, int64_t channels,
+                             int value_dtype, int weight_dtype, void* stream) {
+  LK_REQUIRE(batch > 0 && channels > 0, "fused short convolution requires nonempty input");
+  LK_REQUIRE(batch <= 65535, "at most 65535 batch rows per call");
+  LK_REQUIRE(valid_dtype(value_dtype) && valid_dtype(weight_dtype), "unknown dtype code");
+  LK_REQUIRE(q_in && k_in && v_in && q_state && k_state && v_state && q_weight && k_weight &&
+                 v_weight && q_out && k_out && v_out,
+             "null pointer argument");
+  ConvArgs a{{q_in, k_in, v_in}, {q_state, k_state, v_state}, {q_weight, k_weight, v_weight},
+             {q_out, k_out, v_out}};
+  dim3 grid(static_cast<unsigned>((channels + kConvThreads - 1) / kConvThreads),
+            static_cast<unsigned>(batch), 3);
+  short_conv_kernel<<<grid, kConvThreads, 0, as_stream(stream)>>>(a, channels, value_dtype,
+                                                                  weight_dtype);
+  return check_launch("lk_kda_short_conv_triple");
+}
+
+int lk_kda_gates(const void* raw_decay, const float* dt_bias, const float* a_log,
+                 const void* raw_beta, const void* q, const void* k, float* decay, float* beta,
+                 float* q_out, float* k_out, int64_t rows, int64_t heads, int64_t head_dim,
+                 float eps, int decay_dtype, int beta_dtype, int qk_dtype, void* stream) {
+  LK_REQUIRE(heads > 0 && head_dim > 0 && head_dim <= 1024,
+             "num_heads and head_dim must be positive, with head_dim at most 1024");
+  LK_REQUIRE(eps > 0, "eps must be positive");
+  LK_REQUIRE(rows > 0, "KDA gate inputs must have nonempty batch and sequence dimensions");
+  LK_REQUIRE(valid_dtype(decay_dtype) && valid_dtype(beta_dtype) && valid_dtype(qk_dtype),
+             "unknown dtype code");
+  LK_REQUIRE(raw_decay && dt_bias && a_log && raw_beta && q && k && decay && beta && q_out &&
+                 k_out,
+             "null pointer argument");
+  const int64_t programs = rows * heads;
+  const int64_t blocks = (programs + kGateWaves - 1) / kGateWaves;
+  LK_REQUIRE(blocks < (int64_t{1} << 31), "too many rows");
+  kda_gates_kernel<<<static_cast<unsigned>(blocks), kGateWaves * kWave, 0, as_stream(stream)>>>(
+      raw_decay, dt_bias, a_log, raw_beta, q, k, decay, beta, q_out, k_out, programs,
+      static_cast<int>(heads), static_cast<int>(head_dim), eps, decay_dtype, beta_dtype,
+      qk_dtype);
+  return check_launch("lk_kda_gates");
+}
+
+}  // extern "C"

@@ -67,3 +67,52 @@ def test_codec_validation():
     with pytest.raises(ValueError, match="scale shape"):
         W4A16Tensor(torch.zeros((2, 64), dtype=torch.uint8), torch.zeros((2, 3), dtype=torch.bfloat16),
                     (2, 128), group_size=32)
+
+
+def test_kda_ops_validate_like_the_reference_before_any_launch():
+    """engine/kernels/kda_step.py:140-170 and kda_prepare.py:378-431, 541-587:
+    the same exception types and messages, raised on CPU tensors before any
+    kernel runs."""
+    from local_kimi_amd.kernels import fused_kda_gates, fused_short_conv_triple, kda_decode_step
+
+    st = torch.zeros((1, 2, 4, 4))
+    z3 = torch.zeros((1, 2, 4))
+    b = torch.zeros((1, 2))
+    with pytest.raises(ValueError, match=r"state must have shape"):
+        kda_decode_step(st[0], z3, z3, z3, z3, b, scale=1.0)
+    with pytest.raises(TypeError, match="float32"):
+        kda_decode_step(st.double(), z3, z3, z3, z3, b, scale=1.0)
+    with pytest.raises(ValueError, match=r"beta must have shape"):
+        kda_decode_step(st, z3, z3, z3, z3, z3, scale=1.0)
+    with pytest.raises(ValueError, match="requires CUDA"):
+        kda_decode_step(st, z3, z3, z3, z3, b, scale=1.0)
+
+    x = torch.zeros((2, 1, 8))
+    s4 = torch.zeros((2, 8, 4))
+    w = torch.zeros((8, 1, 4))
+    with pytest.raises(ValueError, match="sequence length one"):
+        fused_short_conv_triple(*(torch.zeros((2, 2, 8)),) * 3, s4, s4, s4, w, w, w)
+    with pytest.raises(ValueError, match=r"state must have shape \[batch, channels, 4\]"):
+        fused_short_conv_triple(x, x, x, s4[:, :, :3], s4, s4, w, w, w)
+    with pytest.raises(TypeError, match="share a dtype"):
+        fused_short_conv_triple(x, x, x, s4.half(), s4, s4, w, w, w)
+    with pytest.raises(ValueError, match="requires CUDA"):
+        fused_short_conv_triple(x, x, x, s4, s4, s4, w, w, w)
+
+    rd = torch.zeros((1, 1, 2, 4))
+    with pytest.raises(ValueError, match="head_dim at most 1024"):
+        fused_kda_gates(rd, torch.zeros(8), torch.zeros((1, 1, 2, 1)), torch.zeros((1, 1, 2)),
+                        torch.zeros((1, 1, 8)), torch.zeros((1, 1, 8)), num_heads=2,
+                        head_dim=2048, eps=1e-6)
+    with pytest.raises(ValueError, match="eps must be positive"):
+        fused_kda_gates(rd, torch.zeros(8), torch.zeros((1, 1, 2, 1)), torch.zeros((1, 1, 2)),
+                        torch.zeros((1, 1, 8)), torch.zeros((1, 1, 8)), num_heads=2,
+                        head_dim=4, eps=0.0)
+    with pytest.raises(ValueError, match="contiguous without transposition"):
+        q = torch.zeros((1, 1, 16))[..., ::2]
+        fused_kda_gates(rd, torch.zeros(8), torch.zeros((1, 1, 2, 1)), torch.zeros((1, 1, 2)),
+                        q, q, num_heads=2, head_dim=4, eps=1e-6)
+    with pytest.raises(ValueError, match="require CUDA"):
+        fused_kda_gates(rd, torch.zeros(8), torch.zeros((1, 1, 2, 1)), torch.zeros((1, 1, 2)),
+                        torch.zeros((1, 1, 8)), torch.zeros((1, 1, 8)), num_heads=2,
+                        head_dim=4, eps=1e-6)
