@@ -630,7 +630,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=52)
     ap.add_argument("--workload", default="all",
                     choices=["all", "moe_decode", "dense_decode", "moe_batched", "moe_prefill",
-                             "qkv_prefill", "stream_floor", "klinear_decode", "copy"])
+                             "qkv_prefill", "stream_floor", "klinear_decode", "kda_decode",
+                             "copy"])
     ap.add_argument("--tokens", type=int, default=64, help="moe_batched tokens per step")
     ap.add_argument("--weights", choices=["w4a16", "mxfp4"], default="w4a16",
                     help="moe_batched / moe_prefill expert weight format")
@@ -679,6 +680,8 @@ def main() -> int:
             configs[f"3_batched_m{m}"] = run_moe_batched(plan, dev, w4, m, "w4a16", cpu)
         configs["4_moe_prefill"] = run_moe_prefill(plan, dev, w4, "w4a16", cpu)
         configs["4_qkv_prefill"] = run_qkv_prefill(plan, dev, cpu)
+        configs["next1_klinear_decode"] = run_klinear_decode(plan, dev, w4)
+        configs["next4_kda_decode"] = run_kda_decode(plan, dev, cpu)
         res["floor"] = run_floor(plan, dev, w4)
         del w4
         torch.cuda.empty_cache()
@@ -709,6 +712,8 @@ def main() -> int:
         res = run_floor(plan, dev, w4)
     elif args.workload == "klinear_decode":
         res = run_klinear_decode(plan, dev, w4)
+    elif args.workload == "kda_decode":
+        res = run_kda_decode(plan, dev, cpu)
     else:
         res = run_copy(dev)
     if forced:
@@ -742,6 +747,119 @@ def run_klinear_decode(plan: Plan, dev, banks) -> dict:
     return {"metric": "KLinearMoE decode us/token (router logits + MoE block)",
             "value": round(t["us"], 3), "unit": "us/token", "steps": t["steps"],
             "warmup": t["warmup"], "achieved_gbps": round(step_bytes / (t["us"] * 1e3), 1)}
+
+
+KDA_HEADS, KDA_DIM, KDA_LAYERS = 32, 128, 160
+
+
+def run_kda_decode(plan: Plan, dev, cpu: bool) -> dict:
+    """KDA decode, batch 1 (next 4): per layer the three short convolutions,
+    the gates and the recurrence step on a 32 x 128 x 128 fp32 state; 160
+    layers' states (320 MB) rotate so each step reads and writes HBM."""
+    from local_kimi_amd.kernels import fused_kda_gates, fused_short_conv_triple, kda_decode_step
+
+    gen = torch.Generator(device=dev).manual_seed(20260740)
+    h, d, c = KDA_HEADS, KDA_DIM, KDA_HEADS * KDA_DIM
+    bf = torch.bfloat16
+
+    def rnd(shape, std=1.0, dtype=bf):
+        return (torch.randn(shape, device=dev, generator=gen) * std).to(dtype)
+
+    ins = [rnd((1, 1, c)) for _ in range(3)]
+    conv_w = [rnd((c, 1, 4), 0.3) for _ in range(3)]
+    raw_decay, raw_beta = rnd((1, 1, h, d)), rnd((1, 1, h))
+    dt_bias = rnd((c,), 1.0, torch.float32)
+    a_log = torch.log(torch.rand((1, 1, h, 1), device=dev, generator=gen) * 15 + 1)
+    conv_states = [[torch.zeros((1, c, 4), dtype=bf, device=dev) for _ in range(3)]
+                   for _ in range(KDA_LAYERS)]
+    rec = [rnd((1, h, d, d), 0.05, torch.float32) for _ in range(KDA_LAYERS)]
+    stream = torch.cuda.Stream(device=dev)
+    scale = d ** -0.5
+
+    def layer(l):
+        q, k, v = fused_short_conv_triple(*ins, *conv_states[l], *conv_w)
+        decay, beta, qn, kn = fused_kda_gates(raw_decay, dt_bias, a_log, raw_beta, q, k,
+                                              num_heads=h, head_dim=d, eps=1e-6)
+        return kda_decode_step(rec[l], qn[:, 0], kn[:, 0], v.view(1, h, d).float(), decay[:, 0],
+                               beta[:, 0], scale=scale)
+
+    def all_layers():
+        for l in range(KDA_LAYERS):
+            layer(l)
+
+    qn = torch.randn((1, h, d), device=dev, generator=gen)
+    qn = qn / qn.norm(dim=-1, keepdim=True)
+    vv = torch.randn((1, h, d), device=dev, generator=gen) * 0.2
+    dd = -(0.005 + 0.075 * torch.rand((1, h, d), device=dev, generator=gen))
+    bb = torch.sigmoid(torch.randn((1, h), device=dev, generator=gen))
+
+    def steps_only():
+        for l in range(KDA_LAYERS):
+            kda_decode_step(rec[l], qn, qn, vv, dd, bb, scale=scale)
+
+    t = time_graph(capture(all_layers, stream), stream, KDA_LAYERS, plan)
+    st = time_graph(capture(steps_only, stream), stream, KDA_LAYERS, plan)
+    state_bytes = h * d * d * 4
+    step_bytes = 2 * state_bytes + h * (3 * d + d + 1) * 4 + h * d * 4  # state in + out, q k v decay beta, out
+    log(f"[bench] KDA decode: {t['us']:.2f} us/layer, step kernel {st['us']:.2f} us")
+    res = {
+        "metric": "KDA decode us/layer (short convs + gates + recurrence step, batch 1)",
+        "value": round(t["us"], 3), "unit": "us/layer", "steps": t["steps"],
+        "warmup": t["warmup"], "higher_is_better": False, "dtype": "f32 state, bf16 projections",
+        "config": {"workload": "kda_decode_batch1", "heads": h, "head_dim": d,
+                   "layers_rotated": KDA_LAYERS, "launches_per_layer": 3},
+        "roofline": {"kernel": "kda_step_kernel (recurrence step)", "bound": "hbm",
+                     "achieved": round(step_bytes / (st["us"] * 1e3), 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(step_bytes / (st["us"] * 1e3) / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "bytes_per_launch": step_bytes,
+                     "avg_launch_us": round(st["us"], 3)},
+    }
+    if cpu:
+        log("[bench] KDA decode: CPU baseline")
+        res["cpu_baseline"] = cpu_kda_layer(ins, conv_states[0], conv_w, raw_decay, dt_bias,
+                                            a_log, raw_beta, rec[0], scale)
+    return res
+
+
+def cpu_kda_layer(ins, conv_states, conv_w, raw_decay, dt_bias, a_log, raw_beta, rec, scale):
+    """The reference's eager decode path for one KDA layer on the host
+    (engine/klinear/attention.py:219-276 through the kda_prepare / kda_step
+    reference functions), in torch on all host threads."""
+    threads = cpu_threads()
+    c_ins = [t.cpu() for t in ins]
+    c_states = [t.cpu().clone() for t in conv_states]
+    c_w = [t.cpu()[:, 0, :].float() for t in conv_w]
+    c_rd, c_rb = raw_decay.cpu(), raw_beta.cpu()
+    c_bias, c_alog = dt_bias.cpu(), a_log.cpu()
+    c_rec = rec.cpu().clone()
+    h, d = KDA_HEADS, KDA_DIM
+
+    def layer():
+        outs = []
+        for x, st, w in zip(c_ins, c_states, c_w):
+            shifted = torch.cat((st[:, :, 1:], x[:, 0].unsqueeze(-1)), dim=-1)
+            conv = (shifted.float() * w.unsqueeze(0)).sum(dim=-1)
+            outs.append(F.silu(conv).to(x.dtype))
+            st.copy_(shifted)
+        q, k, v = (o.view(1, h, d).float() for o in outs)
+        decay = -c_alog.float().view(1, h, 1).exp() * F.softplus(
+            c_rd.float().view(1, h, d) + c_bias.view(h, d))
+        beta = torch.sigmoid(c_rb.float().view(1, h))
+        q = q * torch.rsqrt(q.square().sum(-1, keepdim=True) + 1e-6)
+        k = k * torch.rsqrt(k.square().sum(-1, keepdim=True) + 1e-6)
+        cand = c_rec * torch.exp(decay).unsqueeze(-1)
+        pred = (cand * k.unsqueeze(-1)).sum(dim=-2)
+        cand = cand + beta.unsqueeze(-1).unsqueeze(-1) * k.unsqueeze(-1) * (v - pred).unsqueeze(-2)
+        out = (cand * (q * scale).unsqueeze(-1)).sum(dim=-2)
+        c_rec.copy_(cand)
+        return out
+
+    sec = cpu_median(layer)
+    return {"value": round(sec * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": "one KDA layer, batch 1: the three short convolutions, gates and the "
+                      "recurrence step in eager torch on the host (the reference's eager path); "
+                      "median of 10 after 3 warm-ups"}
 
 
 if __name__ == "__main__":
