@@ -64,6 +64,25 @@ LK_API int lk_kda_gates(const void* raw_decay, const float* dt_bias, const float
                         int64_t head_dim, float eps, int decay_dtype, int beta_dtype,
                         int qk_dtype, void* stream);
 
+/* ---- a whole KDA decode layer in one launch. No reference counterpart: it
+ * runs, for one token per batch row, what engine/klinear/attention.py:193-271
+ * runs through fused_short_conv_triple, fused_kda_gates and kda_decode_step
+ * (three launches there, plus the bf16 -> fp32 view of v), with one block
+ * per (batch row, head). Inputs as lk_kda_short_conv_triple (C = heads *
+ * head_dim) and lk_kda_gates (rows = batch, sequence one); state fp32
+ * [B, H, D, D] and out fp32 [B, H, D] as lk_kda_decode_step with
+ * d_k = d_v = D. Conv states and state are updated in place. q, k, v, decay
+ * and beta are bit-identical to the three-launch chain's; the step sums its
+ * row groups in another order. head_dim a multiple of 4, at most 128. */
+LK_API int lk_kda_decode_layer(const void* q_in, const void* k_in, const void* v_in,
+                               void* q_state, void* k_state, void* v_state,
+                               const void* q_weight, const void* k_weight,
+                               const void* v_weight, const void* raw_decay,
+                               const float* dt_bias, const float* a_log, const void* raw_beta,
+                               float* state, float* out, int64_t batch, int64_t heads,
+                               int64_t head_dim, float eps, float scale, int value_dtype,
+                               int weight_dtype, int decay_dtype, int beta_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

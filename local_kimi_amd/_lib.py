@@ -67,6 +67,8 @@ SIGNATURES: dict[str, list] = {
                                  _I, _I, _P],
     "lk_kda_gates": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _I, _I,
                      _I, _P],
+    "lk_kda_decode_layer": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                            _I64, _I64, _I64, _F, _F, _I, _I, _I, _I, _P],
     "lk_probe_stream_read": [_P, _P, _I, _P, _P],
     "lk_probe_empty": [_P],
 }

@@ -255,6 +255,180 @@ kda_gates_kernel(const void* __restrict__ raw_decay, const float* __restrict__ d
   if (lane == 0) beta[prog] = 1.0f / (1.0f + expf(-load_value(raw_beta, prog, bdt)));
 }
 
+// ---------------------------------------------------------------------------
+// A whole decode layer in one launch: one block of 1024 threads per (batch,
+// head) owns the head's 3 x D convolution channels (so its in-place state
+// updates cannot race with another block), computes the convolutions and the
+// gates into LDS, and runs the recurrence step on the head's D x D state,
+// whose loads are issued first so their latency overlaps the preparation.
+// The preparation repeats the separate kernels' arithmetic exactly (the same
+// per-channel sums and the same per-lane norm order), so q, k, v, decay and
+// beta are bit-identical to fused_short_conv_triple + fused_kda_gates; the
+// step reduces its 32 row groups in another order than kda_step_kernel.
+constexpr int kLayerThreads = 1024;
+constexpr int kLayerMaxDim = 128;
+constexpr int kLayerRowGroups = kLayerThreads / (kLayerMaxDim / 4);  // 32
+constexpr int kLayerWaves = kLayerThreads / kWave;                    // 16
+
+struct LayerArgs {
+  const void* in[3];
+  void* conv_state[3];
+  const void* conv_weight[3];
+  const void* raw_decay;
+  const float* dt_bias;
+  const float* a_log;
+  const void* raw_beta;
+  float* state;
+  float* out;
+};
+
+__global__ void __launch_bounds__(kLayerThreads)
+kda_layer_kernel(const LayerArgs a, int heads, int dim, float eps, float scale, int vdt,
+                 int wdt, int ddt, int bdt) {
+  __shared__ float qkv[3][kLayerMaxDim];
+  __shared__ float gain[kLayerMaxDim];  // exp(decay)
+  __shared__ float norm[2];
+  __shared__ float beta_s;
+  __shared__ float red[kLayerWaves][kLayerMaxDim];
+  const int t = threadIdx.x;
+  const int64_t bh = blockIdx.x;  // batch * heads + head
+  const int64_t b = bh / heads;
+  const int h = static_cast<int>(bh - b * heads);
+  const int channels = heads * dim;
+  const int cg = t & 31, rg = t >> 5;
+  const int c0 = cg * 4;
+  const bool cols = c0 < dim;  // dim % 4 == 0 (host-checked)
+  float* const s_head = a.state + bh * dim * dim;
+
+  // 1. the state rows of this thread (rows rg + 32 p), before anything else
+  float s[4][4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int i = rg + kLayerRowGroups * p;
+    if (cols && i < dim) {
+      const float4 x = *reinterpret_cast<const float4*>(s_head + static_cast<int64_t>(i) * dim + c0);
+      s[p][0] = x.x;
+      s[p][1] = x.y;
+      s[p][2] = x.z;
+      s[p][3] = x.w;
+    } else {
+      s[p][0] = s[p][1] = s[p][2] = s[p][3] = 0.f;
+    }
+  }
+
+  // 2. the three convolutions of this head's channels (as short_conv_kernel)
+  if (t < 3 * dim) {
+    const int conv = t / dim, j = t - conv * dim;
+    const int64_t ch = static_cast<int64_t>(h) * dim + j;
+    const int64_t si = (b * channels + ch) * 4;
+    const float s1 = load_value(a.conv_state[conv], si + 1, vdt);
+    const float s2 = load_value(a.conv_state[conv], si + 2, vdt);
+    const float s3 = load_value(a.conv_state[conv], si + 3, vdt);
+    const float token = load_value(a.in[conv], b * channels + ch, vdt);
+    const float w0 = load_value(a.conv_weight[conv], ch * 4 + 0, wdt);
+    const float w1 = load_value(a.conv_weight[conv], ch * 4 + 1, wdt);
+    const float w2 = load_value(a.conv_weight[conv], ch * 4 + 2, wdt);
+    const float w3 = load_value(a.conv_weight[conv], ch * 4 + 3, wdt);
+    float acc = s1 * w0;
+    acc += s2 * w1;
+    acc += s3 * w2;
+    acc += token * w3;
+    // the conv output rounded to the value dtype, then widened (as the
+    // reference's gates read their bf16 / fp16 inputs)
+    float y = acc / (1.0f + expf(-acc));
+    if (vdt == LK_DTYPE_BF16) y = round_bf16(y);
+    else if (vdt == LK_DTYPE_F16) y = static_cast<float>(static_cast<_Float16>(y));
+    qkv[conv][j] = y;
+    store_value(a.conv_state[conv], si + 0, s1, vdt);
+    store_value(a.conv_state[conv], si + 1, s2, vdt);
+    store_value(a.conv_state[conv], si + 2, s3, vdt);
+    store_value(a.conv_state[conv], si + 3, token, vdt);
+  }
+  // 3. decay (as kda_gates_kernel), kept as exp(decay) for the step
+  if (t < dim) {
+    const float rate = expf(a.a_log[h]);
+    const float biased = load_value(a.raw_decay, bh * dim + t, ddt) + a.dt_bias[h * dim + t];
+    gain[t] = expf(-rate * softplus_f32(biased));
+  }
+  if (t == 0) beta_s = 1.0f / (1.0f + expf(-load_value(a.raw_beta, bh, bdt)));
+  __syncthreads();
+  // 4. q and k norms: waves 0 and 1, the gates kernel's per-lane order
+  if (t < 2 * kWave) {
+    const int which = t / kWave, lane = t & (kWave - 1);
+    float acc = 0.f;
+    for (int d = lane; d < dim; d += kWave) acc = fmaf(qkv[which][d], qkv[which][d], acc);
+    acc = wave_sum(acc);
+    if (lane == 0) norm[which] = 1.0f / sqrtf(acc + eps);
+  }
+  __syncthreads();
+  const float rq = norm[0], rk = norm[1], beta = beta_s;
+
+  // 5. the recurrence step
+  float kr[4], qr[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int i = rg + kLayerRowGroups * p;
+    const bool row_ok = i < dim;
+    const float g = row_ok ? gain[i] : 0.f;
+    kr[p] = row_ok ? qkv[1][i] * rk : 0.f;
+    qr[p] = row_ok ? (qkv[0][i] * rq) * scale : 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s[p][c] *= g;
+  }
+  auto reduce = [&](float (&v)[4]) {  // over the 32 row groups, fixed order
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] += __shfl_xor(v[c], 32);
+    const int wave = t / kWave, lane = t & (kWave - 1);
+    __syncthreads();
+    if (lane < 32) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) red[wave][c0 + c] = v[c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float acc = 0.f;
+      for (int w = 0; w < kLayerWaves; ++w) acc += red[w][c0 + c];
+      v[c] = acc;
+    }
+  };
+  float delta[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float part = 0.f;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) part = fmaf(s[p][c], kr[p], part);
+    delta[c] = part;
+  }
+  reduce(delta);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) delta[c] = (cols ? qkv[2][c0 + c] : 0.f) - delta[c];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float bk = beta * kr[p];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s[p][c] = fmaf(bk, delta[c], s[p][c]);
+  }
+  float o[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float part = 0.f;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) part = fmaf(s[p][c], qr[p], part);
+    o[c] = part;
+  }
+  reduce(o);
+  if (!cols) return;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int i = rg + kLayerRowGroups * p;
+    if (i < dim)
+      *reinterpret_cast<float4*>(s_head + static_cast<int64_t>(i) * dim + c0) =
+          make_float4(s[p][0], s[p][1], s[p][2], s[p][3]);
+  }
+  if (rg == 0) *reinterpret_cast<float4*>(a.out + bh * dim + c0) = make_float4(o[0], o[1], o[2], o[3]);
+}
+
 bool valid_dtype(int d) { return d == LK_DTYPE_F32 || d == LK_DTYPE_F16 || d == LK_DTYPE_BF16; }
 
 }  // namespace
@@ -327,6 +501,36 @@ int lk_kda_gates(const void* raw_decay, const float* dt_bias, const float* a_log
       static_cast<int>(heads), static_cast<int>(head_dim), eps, decay_dtype, beta_dtype,
       qk_dtype);
   return check_launch("lk_kda_gates");
+}
+
+int lk_kda_decode_layer(const void* q_in, const void* k_in, const void* v_in, void* q_state,
+                        void* k_state, void* v_state, const void* q_weight, const void* k_weight,
+                        const void* v_weight, const void* raw_decay, const float* dt_bias,
+                        const float* a_log, const void* raw_beta, float* state, float* out,
+                        int64_t batch, int64_t heads, int64_t head_dim, float eps, float scale,
+                        int value_dtype, int weight_dtype, int decay_dtype, int beta_dtype,
+                        void* stream) {
+  LK_REQUIRE(batch > 0 && heads > 0, "KDA decode dimensions must be nonzero");
+  LK_REQUIRE(head_dim > 0 && head_dim <= kLayerMaxDim && head_dim % 4 == 0,
+             "one-launch KDA layer takes head_dim a multiple of 4 up to %d, got %lld",
+             kLayerMaxDim, (long long)head_dim);
+  LK_REQUIRE(eps > 0, "eps must be positive");
+  LK_REQUIRE(batch * heads < (int64_t{1} << 31), "too many heads");
+  LK_REQUIRE(heads * head_dim < (int64_t{1} << 31), "too many channels");
+  LK_REQUIRE(valid_dtype(value_dtype) && valid_dtype(weight_dtype) && valid_dtype(decay_dtype) &&
+                 valid_dtype(beta_dtype),
+             "unknown dtype code");
+  LK_REQUIRE(q_in && k_in && v_in && q_state && k_state && v_state && q_weight && k_weight &&
+                 v_weight && raw_decay && dt_bias && a_log && raw_beta && state && out,
+             "null pointer argument");
+  LK_REQUIRE(reinterpret_cast<uintptr_t>(state) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
+             "state and out must be 16-byte aligned");
+  LayerArgs a{{q_in, k_in, v_in}, {q_state, k_state, v_state}, {q_weight, k_weight, v_weight},
+              raw_decay, dt_bias, a_log, raw_beta, state, out};
+  kda_layer_kernel<<<static_cast<unsigned>(batch * heads), kLayerThreads, 0, as_stream(stream)>>>(
+      a, static_cast<int>(heads), static_cast<int>(head_dim), eps, scale, value_dtype,
+      weight_dtype, decay_dtype, beta_dtype);
+  return check_launch("lk_kda_decode_layer");
 }
 
 }  // extern "C"

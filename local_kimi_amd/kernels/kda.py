@@ -4,6 +4,8 @@ Same names, signatures, validation and in-place semantics as the reference's
 engine/kernels/kda_step.py:273-293 (``kda_decode_step``) and
 engine/kernels/kda_prepare.py:479-538 (``fused_short_conv_triple``), :630-686
 (``fused_kda_gates``); each runs one launch of ``local_kimi_amd/csrc/kda.hip``.
+``kda_decode_layer`` (no reference counterpart) runs all three for one decode
+token in a single launch.
 
 Beyond the reference's checks: values and states of the short convolutions
 and the q / k / raw inputs of the gates must be float32, float16 or bfloat16
@@ -243,3 +245,69 @@ def fused_kda_gates(raw_decay: torch.Tensor, dt_bias: torch.Tensor, a_log: torch
                   beta.data_ptr(), q_out.data_ptr(), k_out.data_ptr(), batch * sequence,
                   num_heads, head_dim, float(eps), dcode, bcode, qcode, _w._stream(dev))
     return decay, beta, q_out, k_out
+
+
+# ---------------------------------------------------------------------------
+# the whole layer in one launch (no reference counterpart)
+
+KDA_LAYER_MAX_DIM = 128
+
+
+def kda_decode_layer(q_in: torch.Tensor, k_in: torch.Tensor, v_in: torch.Tensor,
+                     q_state: torch.Tensor, k_state: torch.Tensor, v_state: torch.Tensor,
+                     q_weight: torch.Tensor, k_weight: torch.Tensor, v_weight: torch.Tensor,
+                     raw_decay: torch.Tensor, dt_bias: torch.Tensor, a_log: torch.Tensor,
+                     raw_beta: torch.Tensor, state: torch.Tensor, *, num_heads: int,
+                     head_dim: int, eps: float = 1e-6, scale: float | None = None
+                     ) -> torch.Tensor:
+    """One KDA decode token: the short convolutions, the gates and the
+    recurrence step in one launch (what engine/klinear/attention.py:193-271
+    does with fused_short_conv_triple, fused_kda_gates and kda_decode_step).
+
+    Arguments as those three functions take them, with ``state`` the fp32
+    recurrent state [B, H, D, D]; ``scale`` defaults to D ** -0.5. Conv states
+    and ``state`` are updated in place; returns the fp32 output [B, H, D]
+    (``fused_output`` of attention.py:268). head_dim: a multiple of 4 up to 128.
+    """
+    batch, channels = _validate_conv(q_in, k_in, v_in, q_state, k_state, v_state, q_weight,
+                                     k_weight, v_weight)
+    _validate_gates(raw_decay, dt_bias, a_log, raw_beta, q_in, k_in, num_heads=num_heads,
+                    head_dim=head_dim, eps=eps)
+    if raw_decay.shape[:2] != (batch, 1):
+        raise ValueError("raw_decay must hold one token per batch row")
+    if state.dtype != torch.float32:
+        raise TypeError("KDA decode inputs must all use torch.float32")
+    if tuple(state.shape) != (batch, num_heads, head_dim, head_dim):
+        raise ValueError("state must have shape [batch, heads, head_dim, head_dim]")
+    if state.device != q_in.device:
+        raise ValueError("all KDA tensors must share one device")
+    if head_dim > KDA_LAYER_MAX_DIM or head_dim % 4:
+        raise ValueError(f"kda_decode_layer takes head_dim a multiple of 4 up to "
+                         f"{KDA_LAYER_MAX_DIM}, got {head_dim}")
+    vcode = _code(q_in, "short convolution inputs and states")
+    weights = [_weight_view(w) for w in (q_weight, k_weight, v_weight)]
+    if weights[0].dtype not in _DTYPE_CODES or any(w.dtype != weights[0].dtype for w in weights):
+        weights = [w.float() for w in weights]
+    wcode = _DTYPE_CODES[weights[0].dtype]
+    weights = [_w._c(w) for w in weights]
+    ins = [_w._c(t) for t in (q_in, k_in, v_in)]
+    conv_states = [q_state, k_state, v_state]
+    conv_work = [s if s.is_contiguous() else s.contiguous() for s in conv_states]
+    work = _dense(state)
+    bias = dt_bias.float().contiguous()
+    rate = a_log.float().reshape(num_heads).contiguous()
+    out = torch.empty((batch, num_heads, head_dim), dtype=torch.float32, device=state.device)
+    s = head_dim ** -0.5 if scale is None else float(scale)
+    with torch.cuda.device(state.device):
+        _lib.call("lk_kda_decode_layer", *(t.data_ptr() for t in ins),
+                  *(t.data_ptr() for t in conv_work), *(t.data_ptr() for t in weights),
+                  raw_decay.data_ptr(), bias.data_ptr(), rate.data_ptr(), raw_beta.data_ptr(),
+                  work.data_ptr(), out.data_ptr(), batch, num_heads, head_dim, float(eps), s,
+                  vcode, wcode, _code(raw_decay, "raw_decay"), _code(raw_beta, "raw_beta"),
+                  _w._stream(state.device))
+    for st, w in zip(conv_states, conv_work):
+        if w is not st:
+            st.copy_(w)
+    if work is not state:
+        state.copy_(work)
+    return out

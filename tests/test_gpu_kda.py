@@ -271,3 +271,126 @@ def test_prepare_and_step_graph_replays_match_eager(rng):
         for a, b in zip(g_conv, e_conv):
             assert torch.equal(a, b), rep
         _ = (e_rec.sum() * 2).item()  # unrelated eager work between replays
+
+
+# ---------------------------------------------------------------------------
+# the whole layer in one launch
+
+
+def _layer_inputs(rng, b, h, d, name):
+    c = h * d
+    ins = [K.round_to(rng.normal(size=(b, 1, c)), name) for _ in range(3)]
+    conv_states = [K.round_to(rng.normal(size=(b, c, 4)), name) for _ in range(3)]
+    conv_w = [K.round_to(0.3 * rng.normal(size=(c, 1, 4)), name) for _ in range(3)]
+    raw_decay = K.round_to(rng.normal(size=(b, 1, h, d)), name)
+    raw_beta = K.round_to(rng.normal(size=(b, 1, h)), name)
+    dt_bias = rng.normal(size=c).astype(np.float32)
+    a_log = np.log(rng.uniform(1, 16, size=h)).astype(np.float32).reshape(1, 1, h, 1)
+    rec = (0.05 * rng.normal(size=(b, h, d, d))).astype(np.float32)
+    return ins, conv_states, conv_w, raw_decay, raw_beta, dt_bias, a_log, rec
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("b,h,d", [(1, 32, 128), (2, 4, 72), (3, 2, 8)])
+def test_layer_matches_the_oracle_chain(rng, dtype, b, h, d):
+    """Convolutions (states bit-exact), gates and step against the oracle's
+    composition, within the step's single-step bound (3e-5)."""
+    from local_kimi_amd.kernels import kda_decode_layer
+
+    name = _STORAGE[dtype]
+    ins, conv_states, conv_w, raw_decay, raw_beta, dt_bias, a_log, rec = _layer_inputs(
+        rng, b, h, d, name)
+    (qo, ko, vo), states_want = K.short_conv_triple(*ins, *conv_states, *conv_w, name)
+    decay, beta, qn, kn = K.gates(raw_decay, dt_bias, a_log, raw_beta, qo, ko, h, d, 1e-6)
+    want_state, want_out = K.decode_step(rec, qn[:, 0], kn[:, 0], vo.reshape(b, h, d),
+                                         decay[:, 0], beta[:, 0], d ** -0.5)
+    dev_states = [_t(s, dtype) for s in conv_states]
+    st = _t(rec)
+    out = kda_decode_layer(*(_t(x, dtype) for x in ins), *dev_states,
+                           *(_t(w, dtype) for w in conv_w), _t(raw_decay, dtype), _t(dt_bias),
+                           _t(a_log), _t(raw_beta, dtype), st, num_heads=h, head_dim=d)
+    for s, want in zip(dev_states, states_want):
+        assert np.array_equal(_np(s), want)
+    _close(_np(st), want_state, 3e-5, 3e-5, f"layer state {b, h, d}")
+    _close(_np(out), want_out, 3e-5, 3e-5, f"layer output {b, h, d}")
+
+
+def test_layer_agrees_with_the_three_launch_chain(rng):
+    """Same inputs through fused_short_conv_triple + fused_kda_gates +
+    kda_decode_step: conv states bit-identical, state and output within the
+    rounding of two summation orders (1e-6 absolute + 1e-5 relative)."""
+    from local_kimi_amd.kernels import (fused_kda_gates, fused_short_conv_triple,
+                                        kda_decode_layer, kda_decode_step)
+
+    b, h, d = 2, 32, 128
+    bf = torch.bfloat16
+    ins, conv_states, conv_w, raw_decay, raw_beta, dt_bias, a_log, rec = _layer_inputs(
+        rng, b, h, d, "bfloat16")
+    args = [_t(x, bf) for x in ins], [_t(w, bf) for w in conv_w]
+    s1 = [_t(s, bf) for s in conv_states]
+    s2 = [_t(s, bf) for s in conv_states]
+    r1, r2 = _t(rec), _t(rec)
+    out1 = kda_decode_layer(*args[0], *s1, *args[1], _t(raw_decay, bf), _t(dt_bias), _t(a_log),
+                            _t(raw_beta, bf), r1, num_heads=h, head_dim=d)
+    q, k, v = fused_short_conv_triple(*args[0], *s2, *args[1])
+    decay, beta, qn, kn = fused_kda_gates(_t(raw_decay, bf), _t(dt_bias), _t(a_log),
+                                          _t(raw_beta, bf), q, k, num_heads=h, head_dim=d,
+                                          eps=1e-6)
+    out2 = kda_decode_step(r2, qn[:, 0], kn[:, 0], v.view(b, h, d).float(), decay[:, 0],
+                           beta[:, 0], scale=d ** -0.5)
+    for a, c in zip(s1, s2):
+        assert torch.equal(a, c)
+    _close(_np(r1), _np(r2), 1e-6, 1e-5, "layer vs chain state")
+    _close(_np(out1), _np(out2), 1e-6, 1e-5, "layer vs chain output")
+
+
+def test_layer_graph_replays_match_eager(rng):
+    from local_kimi_amd.kernels import kda_decode_layer
+
+    b, h, d = 1, 32, 128
+    bf = torch.bfloat16
+    ins, conv_states, conv_w, raw_decay, raw_beta, dt_bias, a_log, rec = _layer_inputs(
+        rng, b, h, d, "bfloat16")
+    fixed = ([_t(x, bf) for x in ins], [_t(w, bf) for w in conv_w], _t(raw_decay, bf),
+             _t(dt_bias), _t(a_log), _t(raw_beta, bf))
+
+    def run(states, r):
+        return kda_decode_layer(*fixed[0], *states, *fixed[1], fixed[2], fixed[3], fixed[4],
+                                fixed[5], r, num_heads=h, head_dim=d)
+
+    g_states, e_states = [_t(s, bf) for s in conv_states], [_t(s, bf) for s in conv_states]
+    g_rec, e_rec = _t(rec), _t(rec)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        run([_t(s, bf) for s in conv_states], _t(rec))
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        g_out = run(g_states, g_rec)
+    for rep in range(4):
+        with torch.cuda.stream(stream):
+            graph.replay()
+        e_out = run(e_states, e_rec)
+        torch.cuda.synchronize()
+        assert torch.equal(g_out, e_out) and torch.equal(g_rec, e_rec), rep
+        for a, c in zip(g_states, e_states):
+            assert torch.equal(a, c), rep
+
+
+def test_layer_rejects_wide_heads():
+    from local_kimi_amd.kernels import kda_decode_layer
+
+    h, d = 1, 132
+    c = h * d
+    bf = torch.bfloat16
+    x = torch.zeros((1, 1, c), dtype=bf, device=DEV)
+    s = torch.zeros((1, c, 4), dtype=bf, device=DEV)
+    w = torch.zeros((c, 1, 4), dtype=bf, device=DEV)
+    with pytest.raises(ValueError, match="multiple of 4 up to 128"):
+        kda_decode_layer(x, x, x, s, s.clone(), s.clone(), w, w, w,
+                         torch.zeros((1, 1, h, d), dtype=bf, device=DEV),
+                         torch.zeros(c, device=DEV), torch.zeros((1, 1, h, 1), device=DEV),
+                         torch.zeros((1, 1, h), dtype=bf, device=DEV),
+                         torch.zeros((1, h, d, d), device=DEV), num_heads=h, head_dim=d)
