@@ -81,3 +81,37 @@ def designed_router_logits(rng: np.random.Generator, counts: np.ndarray, tokens:
         logits[t, order] = rng.uniform(2.0, 4.0, top_k).astype(np.float32)
     assert not left.any()
     return logits
+
+
+def bf16_ulp_distance(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
+    """Distance in bf16 units in the last place: bit patterns mapped to a
+    monotonic integer order (+0 and -0 coincide)."""
+    def order(bits):
+        b = np.asarray(bits, dtype=np.uint16).astype(np.int32)
+        mag = b & 0x7FFF
+        return np.where(b & 0x8000, -mag, mag)
+    return np.abs(order(a_bits) - order(b_bits))
+
+
+def paths_agreement(a_bits: np.ndarray, b_bits: np.ndarray) -> tuple[float, float, float]:
+    """(fraction bit-identical, fraction within one bf16 ulp, largest distance
+    in ulps) of two bf16 outputs. A distance is counted in ulps of the larger
+    magnitude of the pair, floored at 1/16 of the outputs' rms, so values
+    near zero that cancel are compared at the scale of the outputs."""
+    a = bf16_values(a_bits).astype(np.float64)
+    b = bf16_values(b_bits).astype(np.float64)
+    scale = float(np.sqrt((b * b).mean())) if b.size else 1.0
+    mag = np.maximum(np.maximum(np.abs(a), np.abs(b)), scale / 16.0)
+    d = np.abs(a - b) / 2.0 ** (np.floor(np.log2(mag)) - 7)
+    return float((d == 0).mean()), float((d <= 1).mean()), float(d.max(initial=0.0))
+
+
+def assert_paths_agree(actual_bits: np.ndarray, expected_bits: np.ndarray, *, exact: float,
+                       within_one: float, max_ulps: float, what: str = "") -> None:
+    """Two HIP paths that differ only in fp32 accumulation order: at least
+    ``exact`` of the outputs bit-identical, ``within_one`` within one ulp, and
+    none beyond ``max_ulps`` (paths_agreement's measure)."""
+    same, one, worst = paths_agreement(actual_bits, expected_bits)
+    assert same >= exact and one >= within_one and worst <= max_ulps, (
+        f"{what}: {same:.4%} identical (bound {exact:.2%}), {one:.4%} within one ulp "
+        f"(bound {within_one:.2%}), max {worst:.1f} ulps (bound {max_ulps})")

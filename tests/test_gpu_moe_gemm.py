@@ -19,7 +19,7 @@ from oracle import w4a16 as OW
 
 from local_kimi_amd._lib import forced_path
 
-from ._helpers import assert_close_bf16, from_bits, random_bf16_bits, to_bits
+from ._helpers import assert_close_bf16, assert_paths_agree, from_bits, random_bf16_bits, to_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -280,6 +280,13 @@ def test_moe_forward_full_size(rng, kimi_banks, tokens, zipf):
     yd, idxd, _ = w4a16_moe_decode(*args)
     assert torch.equal(idx, idxd)
     assert_close_bf16(to_bits(y), to_bits(yd), what="expert-major vs token-major")
+    # the two paths differ only in fp32 accumulation order. Measured at 1 to
+    # 2048 tokens: 96-97 % of the outputs bit-identical, 98.5-99.2 % within
+    # one ulp, at most 32 ulps (a bf16 rounding of a route output that moved
+    # across a tie, seen through a combine that cancels). A dropped or extra
+    # rounding point in one path would break the first two.
+    assert_paths_agree(to_bits(y), to_bits(yd), exact=0.94, within_one=0.98, max_ulps=64,
+                       what=f"expert-major vs token-major, T={tokens}")
     sel = np.unique(rng.choice(tokens, size=min(tokens, 6), replace=False))
     ey, eidx = _oracle_tokens(x, logits, kimi_banks, sel)
     assert np.array_equal(idx.cpu().numpy()[sel], eidx)

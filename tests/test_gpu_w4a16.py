@@ -16,7 +16,8 @@ from oracle import moe as OM
 from oracle import w4a16 as OW
 from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
 
-from ._helpers import ATOL, RTOL, assert_close_bf16, from_bits, random_bf16_bits, to_bits
+from ._helpers import (ATOL, RTOL, assert_close_bf16, bf16_ulp_distance, from_bits,
+                       random_bf16_bits, to_bits)
 
 pytestmark = pytest.mark.gpu
 
@@ -214,6 +215,29 @@ def test_swiglu_matches_oracle(rng, g):
     with registry.using("w4a16_grouped", "reference"):
         ref = registry.reference_of("w4a16_swiglu").fn(*args)
     assert np.abs(to_bits(ref).astype(np.int32) - expected.astype(np.int32)).max() <= 1
+
+
+def test_silu_mul_follows_the_rounding_contract_bit_for_bit(rng):
+    """``silu_mul`` against torch's own bf16 ``F.silu(gate) * up`` on the GPU
+    (the reference's two ops): bit-identical on 1M random pairs plus edge
+    values; against the oracle (numpy's fp32 exp, which may differ from the
+    device's in the last fp32 bit) within one bf16 ulp, and equal on at least
+    99.9 %."""
+    import torch.nn.functional as F
+
+    from local_kimi_amd.kernels import silu_mul
+
+    gate = random_bf16_bits(rng, (1 << 20,), 3.0)
+    up = random_bf16_bits(rng, (1 << 20,), 1.0)
+    edges = np.array([0.0, -0.0, 1e-30, -1e-30, 88.0, -88.0, 100.0, -100.0, 3e38, -3e38],
+                     np.float32)
+    gate[:edges.size] = f32_to_bf16_bits(edges)
+    g, u = _dev_bf16(gate), _dev_bf16(up)
+    out = silu_mul(g, u)
+    assert torch.equal(out, F.silu(g) * u)
+    want = OW.mul_bf16(OW.silu_bf16(gate), up)
+    d = bf16_ulp_distance(to_bits(out), want)
+    assert d.max() <= 1 and (d == 0).mean() >= 0.999
 
 
 # ---------------------------------------------------------------------------
