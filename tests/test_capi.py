@@ -74,6 +74,29 @@ def test_expert_major_sizes_and_argument_errors(lib):
         _lib.call("lk_w4a16_dense_gemm", 1, 1, 1, 1, 16, 8, 100, 32, None)
 
 
+def test_workspace_sizes_are_checked_before_any_launch(lib):
+    """Every entry point that writes a caller-owned workspace refuses one
+    smaller than its size query, before touching device memory (the pointers
+    here are never dereferenced)."""
+    need = _lib.query("lk_w4a16_moe_forward_workspace", 64, 257, 2304, 1024, 8)
+    # 13 device pointers, then workspace_bytes one short of the query
+    args = [1] * 13 + [need - 1, 64, 257, 2304, 1024, 8, 1.0, 1, 128, None]
+    with pytest.raises(RuntimeError, match="MoE workspace too small"):
+        _lib.call("lk_w4a16_moe_forward", *args)
+    gneed = _lib.query("lk_w4a16_grouped_gemm_workspace", 64, 9, 257)
+    assert gneed > 0
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        _lib.call("lk_w4a16_grouped_gemm", 1, 1, 1, 1, 1, 64, 9, 257, 2304, 1024, 128, 1,
+                  gneed - 1, None)
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        _lib.call("lk_w4a16_swiglu_gemm", 1, 1, 1, 1, 1, 1, 1, 64, 9, 257, 1024, 2304, 128, 1,
+                  gneed - 1, None)
+    mxneed = _lib.query("lk_mxfp4_moe_forward_workspace", 64, 257, 2304, 1024, 8)
+    margs = [1] * 13 + [mxneed - 1, 64, 257, 2304, 1024, 8, 1.0, 1, None]
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        _lib.call("lk_mxfp4_moe_forward", *margs)
+
+
 def test_path_knobs_select_and_reject(lib):
     for knob, choices in _lib.PATH_KNOBS.items():
         assert _lib.get_path(knob) == "auto"
