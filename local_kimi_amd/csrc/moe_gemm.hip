@@ -296,6 +296,14 @@ struct GemmArgs {
   const uint8_t* a_hi;       // kFmtMxF8: fp8 hi codes, rows of k bytes
   const uint8_t* a_lo;       // kFmtMxF8: fp8 lo codes
   const uint16_t* a_sc;      // kFmtMxF8: per-32 exponents, byte 0 hi, byte 1 lo
+  // 64-row expert-major launches with 128-wide k-steps (gate/up gather, down
+  // scatter; W4A16 G = 128 or MXFP4 on bf16 MFMA) load activations into LDS
+  // with direct loads: W4A16 from a_pair (rows of a with every 8-value chunk
+  // in the weight decode's k order) and a_neg (-136 * sum(x) per row and
+  // 128-wide group), MXFP4 from a. a_rows bounds both buffers.
+  const uint16_t* a_pair;
+  const float* a_neg;
+  int64_t a_rows;
   const int32_t* perm;       // sorted position -> entry (gather / scatter modes)
   const int32_t* tiles;      // [*, 4] tile list (schedule modes)
   const int32_t* tile_count;
@@ -377,6 +385,62 @@ __device__ inline float sum_x8_dot(const uint4 v) {
   s = dot2_bf16(v.y, kOnesBf16x2, s);
   s = dot2_bf16(v.z, kOnesBf16x2, s);
   return dot2_bf16(v.w, kOnesBf16x2, s);
+}
+
+// ---- direct global -> LDS loads (buffer_load ... lds)
+// One wave-wide load: lane L's 16 (or 4) bytes at voff + soff of the buffer
+// land in LDS at lds + 16 L (4 L); lds and soff are wave-uniform. Issued from
+// inline asm so that the compiler does not order LDS reads behind it: the
+// caller waits for it (s_waitcnt vmcnt) before the barrier that publishes
+// the LDS buffer, and the "memory" clobber keeps the loads issued after it
+// in program order (which that vmcnt count relies on).
+__device__ inline uint32_t lds_offset(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p)));
+}
+// raw buffer descriptor of `bytes` bytes at `base` (stride 0; loads at or
+// past `bytes` return zeros)
+__device__ inline u32x4_t buffer_rsrc(const void* base, int64_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t n = bytes < 0xFFFFFFFFll ? static_cast<uint32_t>(bytes) : 0xFFFFFFFFu;
+  return u32x4_t{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xFFFFu, n,
+                 0x00020000u};
+}
+__device__ inline void lds_direct16(u32x4_t rs, const void* lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               ::"s"(__builtin_amdgcn_readfirstlane(lds_offset(lds))), "v"(voff), "s"(rs),
+                 "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "memory");
+}
+__device__ inline void lds_direct4(u32x4_t rs, const void* lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               ::"s"(__builtin_amdgcn_readfirstlane(lds_offset(lds))), "v"(voff), "s"(rs),
+                 "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "memory");
+}
+
+// Rows of bf16 activations for the direct-load W4A16 GEMM: each 8-value chunk
+// in the weight decode's k order (x0 x4, x1 x5, x2 x6, x3 x7, as the
+// streaming kernel stages it) and -136 * sum(x) per 128-wide group, summed
+// in the staging's order: one 16-lane DPP row per (row, group), lane c on
+// chunk c, so the sums are bit-identical to the in-kernel staging's.
+__global__ void __launch_bounds__(256)
+pair_rows_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xp,
+                 float* __restrict__ neg, uint32_t units) {
+  // unit = row * (k / 128) + group, so its chunk sits at 128 unit + 8 c
+  const uint32_t unit = (blockIdx.x * 256u + threadIdx.x) >> 4;
+  const bool live = unit < units;  // uniform over each 16-lane row
+  const uint32_t u = live ? unit : 0u;
+  const int64_t off = static_cast<int64_t>(u) * 128 + (threadIdx.x & 15) * 8;
+  const uint4 v = *reinterpret_cast<const uint4*>(x + off);
+  uint32_t q[4];
+  pair_x8(v, q);
+  float sx = sum8(sum_x8_dot(v));
+  sx += dpp_f32<kRowMirror>(sx);
+  if (live) {
+    *reinterpret_cast<uint4*>(xp + off) = make_uint4(q[0], q[1], q[2], q[3]);
+    if ((threadIdx.x & 15) == 0) neg[u] = -kCodeOffset * sx;
+  }
 }
 
 // Zero line read by ring reloads past the last k-step. Every wave reads the
@@ -777,6 +841,7 @@ constexpr int kStWaves = 8;
 constexpr int kStDepth = 6;                      // k-steps of weights in flight per wave
 constexpr int kStMaxLds = 150 * 1024;            // LDS a streaming block may take
 constexpr int kStPassSteps = 4;                  // k-steps per activation pass (64-row tiles)
+constexpr int64_t kMaxDirectBytes = 0xFFFFFFFFll;  // direct-load sources: 32-bit byte offsets
 
 template <int FMT>
 __device__ inline uint16_t store_value(float v) {
@@ -795,8 +860,20 @@ inline size_t stream_lds_bytes(int64_t k, int mt) {
   return static_cast<size_t>(nbuf * ps * mt) * (4 * kWave * sizeof(uint4) + 4 * 16 * sizeof(float));
 }
 
+// s_waitcnt vmcnt(N) from inline asm (the compiler does not count the
+// direct loads, so it cannot place this wait itself)
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // One tile of <= 16 * MT rows x kBN columns of a streaming block (below).
-template <int FMT, int MATS, int NT, int MT, bool WIDE, bool GATHER, bool SCATTER, bool DENSE>
+// MT = 1: all k-steps of the activations resident; MT = 4 or 5: passes of
+// kStPassSteps (5: 3) k-steps, double buffered. DIRECT: activations come in by
+// direct loads (see GemmArgs::a_pair).
+template <int FMT, int MATS, int NT, int MT, bool WIDE, bool GATHER, bool SCATTER, bool DENSE,
+          bool DIRECT = false>
 __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert, const int row0,
                                             const int rows, const int cb, const int osel) {
   constexpr bool kMx = FMT != kFmtW4A16;
@@ -807,7 +884,13 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
   constexpr int kBN = kStWaves * NT * 16;
   constexpr int kRows = 16 * MT;
   constexpr int kNBuf = MT == 1 ? 1 : 2;
-  constexpr int kPassUnits = MT == 1 ? 1 : (kRows * kStPassSteps * 16 + kThreads - 1) / kThreads;
+  constexpr int kPS = MT == 5 ? 3 : kStPassSteps;  // k-steps per pass (MT > 1)
+  constexpr int kPassUnits = MT == 1 ? 1 : (kRows * kPS * 16 + kThreads - 1) / kThreads;
+  constexpr bool kDirect = DIRECT;
+  static_assert(!kDirect || (WIDE && (FMT == kFmtW4A16 || FMT == kFmtMxBf16) &&
+                             GATHER != SCATTER && !DENSE),
+                "direct loads: 128-wide k-steps of an expert-major gather or scatter");
+  static_assert(MT == 1 || MT == 4 || (MT == 5 && kDirect), "tile heights 16, 64, direct 80");
   extern __shared__ uint4 smem[];
   __shared__ int64_t row_index[kRows];  // activation row of each tile row
   __shared__ int64_t out_row[kRows];    // output row of each tile row
@@ -816,9 +899,12 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
   const int tid = threadIdx.x;
 
   // the tile's sorted-position lookups, issued ahead of the weight loads so
-  // that waiting for them never waits for weights
+  // that waiting for them never waits for weights. Direct loads fill every
+  // tile row: rows past `rows` read the tile's first row (never stored).
+  const int table_rows = kDirect ? kRows : rows;
+  const int src_m = kDirect && tid >= rows ? 0 : tid;
   int32_t pos = 0;
-  if ((GATHER || SCATTER) && tid < rows) pos = g.perm[row0 + tid];
+  if ((GATHER || SCATTER) && tid < table_rows) pos = g.perm[row0 + src_m];
   const int lane = tid & (kWave - 1);
   const int wv = tid / kWave;
   const int jq = lane >> 4;
@@ -826,7 +912,7 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
   const int64_t rowb = K / 2;
   const int64_t spr = K / g.group;
   const int ksteps = static_cast<int>((K + 127) / 128);
-  const int ps = MT == 1 ? ksteps : kStPassSteps;  // k-steps per pass
+  const int ps = MT == 1 ? ksteps : kPS;  // k-steps per pass
   const int cg = static_cast<int>(g.group / 32);
   const int mt_act = (rows + 15) >> 4;
   uint4* const afrag = smem;  // [kNBuf][ps][MT][4][64]
@@ -851,7 +937,7 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
                        expert * g.sstride + cc * spr;
     }
   }
-  constexpr int kRing = MT == 1 ? kStDepth : kStPassSteps;
+  constexpr int kRing = MT == 1 ? kStDepth : kPS;
   const int gshift = __builtin_ctzll(static_cast<unsigned long long>(g.group));
   WeightStep<FMT, MATS, NT, WIDE> w[kRing];
   // every ring slot is refilled unconditionally (steps past the end read a
@@ -867,8 +953,8 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
 
   // 2. the tile's activation and output rows (one lookup per row, shared
   // through LDS; the epilogue then reads no global memory)
-  if (tid < rows) {
-    row_index[tid] = GATHER ? static_cast<int64_t>(pos / g.routes) : row0 + tid;
+  if (tid < table_rows) {
+    row_index[tid] = GATHER ? static_cast<int64_t>(pos / g.routes) : row0 + src_m;
     out_row[tid] = SCATTER ? static_cast<int64_t>(pos) : row0 + tid;
   }
   __syncthreads();
@@ -877,7 +963,7 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
   // units of one (row, step) sit in one 16-lane DPP row; slots m >= rows are
   // skipped (their MFMA rows are never stored)
   constexpr int kRowShift = MT == 1 ? 4 : 6;
-  static_assert(kRows == (1 << kRowShift), "tile rows must be 16 or 64");
+  static_assert(kDirect || kRows == (1 << kRowShift), "staged tiles have 16 or 64 rows");
   auto unit_live = [&](int u) { return ((u >> 4) & (kRows - 1)) < rows; };
   // kFmtMxF8: unit c < 8 is 16 fp8 hi codes (k = 16c..16c+15 of the step),
   // c >= 8 the lo codes of chunk c - 8; units c < 4 also carry the row's
@@ -941,10 +1027,92 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
   };
   auto pass_steps = [&](int p) { return min(ps, ksteps - p * ps); };
 
+  // Direct-load layout: a k-step's activations are [tile row m][slot] of 16
+  // bytes, chunk c (k = 8c..8c+7 of the step) of row m in slot c ^ (m & 15),
+  // so 16 lanes of one load read one row's 256 contiguous bytes and an MFMA
+  // fragment read (16 rows, one chunk each) meets every bank once. One load
+  // fills a block of 4 rows of one k-step (lane L: row 4 blk + L / 16, chunk
+  // (L & 15) ^ (row & 15)). MT > 1: wave wv fills blocks wv, wv + 8, ... of
+  // every k-step of a pass. MT == 1 (one pass over all k-steps): wave wv
+  // fills block wv & 3 of k-steps wv / 4, wv / 4 + 2, ...
+  // W4A16's group sums come in by 4-byte loads of 64 tile rows (lane = row;
+  // lanes past the tile read row 0 into padding) to offs[buffer][ls][row]:
+  // MT > 1: wave n loads step n / kNegLoads, rows 64 (n % kNegLoads) ..;
+  // MT == 1: waves take the steps round robin.
+  // MT > 1: a wave issues its direct loads before its kPS steps of weight
+  // refills (2 MATS NT loads each), so vmcnt(kAfter) at the pass end covers
+  // them; MT == 1 issues them after the ring and waits for everything.
+  constexpr int kBlocks = kRows / 4;                                      // per k-step
+  constexpr int kPw = MT == 1 ? 1 : (kBlocks + kStWaves - 1) / kStWaves;  // blocks per wave
+  constexpr int kNegLoads = (kRows + 63) / 64;                            // per k-step
+  constexpr int kNegStride = kNegLoads * 64;                              // floats per k-step
+  constexpr int kAfter = kPS * 2 * MATS * NT;
+  static_assert(!kDirect || MT == 1 || kPS * kNegLoads <= kStWaves, "one sum load per wave");
+  static_assert(kNegLoads <= 2, "at most 128 tile rows");
+  [[maybe_unused]] uint32_t voff[kPw] = {};
+  [[maybe_unused]] uint32_t voff_neg0 = 0, voff_neg1 = 0;  // rows lane, 64 + lane
+  [[maybe_unused]] u32x4_t rs_a = {0u, 0u, 0u, 0u}, rs_n = {0u, 0u, 0u, 0u};
+  if constexpr (kDirect) {
+    rs_a = buffer_rsrc(FMT == kFmtW4A16 ? g.a_pair : g.a, g.a_rows * K * 2);
+#pragma unroll
+    for (int h = 0; h < kPw; ++h) {
+      const int blk = MT == 1 ? (wv & 3) : min(wv + kStWaves * h, kBlocks - 1);
+      const int m = blk * 4 + jq;
+      voff[h] = static_cast<uint32_t>(row_index[m] * K * 2 + ((lane & 15) ^ (m & 15)) * 16);
+    }
+    if constexpr (FMT == kFmtW4A16) {
+      rs_n = buffer_rsrc(g.a_neg, g.a_rows * (K / 128) * 4);
+      voff_neg0 = static_cast<uint32_t>(row_index[lane < kRows ? lane : 0] * (K / 128) * 4);
+      if constexpr (kNegLoads > 1)
+        voff_neg1 = static_cast<uint32_t>(row_index[64 + lane < kRows ? 64 + lane : 0] * (K / 128) * 4);
+    }
+  }
+  auto direct_pass = [&](int p, int b) {
+    if constexpr (kDirect) {
+      const int steps = pass_steps(p);
+      if constexpr (MT == 1) {
+        for (int ls = wv >> 2; ls < steps; ls += 2)
+          lds_direct16(rs_a, afrag + (ls * kRows + (wv & 3) * 4) * 16, voff[0],
+                       static_cast<uint32_t>(ls) * 256u);
+        if constexpr (FMT == kFmtW4A16) {
+          for (int ls = wv; ls < steps; ls += kStWaves)
+            lds_direct4(rs_n, offs + ls * kNegStride, voff_neg0, static_cast<uint32_t>(ls) * 4u);
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < kPw; ++h) {
+          const int blk = wv + kStWaves * h;
+          if (blk < kBlocks) {
+#pragma unroll
+            for (int ls = 0; ls < kPS; ++ls)
+              if (ls < steps)
+                lds_direct16(rs_a, afrag + ((b * ps + ls) * kRows + blk * 4) * 16, voff[h],
+                             static_cast<uint32_t>(p * ps + ls) * 256u);
+          }
+        }
+        if constexpr (FMT == kFmtW4A16) {
+          const int ls = wv / kNegLoads, hh = wv % kNegLoads;
+          if (ls < steps)
+            lds_direct4(rs_n, offs + (b * ps + ls) * kNegStride + hh * 64,
+                        hh == 0 ? voff_neg0 : voff_neg1,
+                        static_cast<uint32_t>(p * ps + ls) * 4u);
+        }
+      }
+    }
+  };
+
   // 3. stage the first pass. 64-row tiles: all of its units in one batch of
   // loads, then the weight ring, then the stores (the stores wait for the
-  // activation loads alone)
-  if constexpr (MT > 1) {
+  // activation loads alone); direct loads: the pass, then the ring
+  if constexpr (kDirect && MT == 1) {
+    direct_pass(0, 0);  // the ring is already in flight
+    wait_vmcnt<0>();
+  } else if constexpr (kDirect) {
+    direct_pass(0, 0);
+#pragma unroll
+    for (int j = 0; j < kRing; ++j) w[j].load(wrow, srow, j, jq, K, gshift, ksteps, dummy);
+    wait_vmcnt<kAfter>();
+  } else if constexpr (MT > 1) {
     uint4 v0[kPassUnits];
     uint32_t s0[kPassUnits];
     const int units0 = pass_steps(0) * kRows * 16;
@@ -999,6 +1167,13 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
         tot[mi][nt][ms] = zero4;
         acc[mi][nt][ms] = zero4;
       }
+  // LDS slot of this lane's MFMA fragment (subtile ms, sub-step t) of local
+  // k-step ls in buffer b: the swizzled fragment blocks of the staged layout,
+  // or the row-major layout of direct loads
+  auto a_slot = [&](int b, int ls, int ms, int t) -> int {
+    if constexpr (kDirect) return ((b * ps + ls) * kRows + ms * 16 + ln) * 16 + ((4 * jq + t) ^ ln);
+    else return (((b * ps + ls) * MT + ms) * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq));
+  };
   // one k-step: weights wj (a ring slot), activation buffer b, local step ls.
   // Every subtile is computed (no per-MFMA branch): rows past the tile read
   // stale LDS and produce rows that are never stored (MFMA rows are independent).
@@ -1053,7 +1228,7 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
 #pragma unroll
         for (int ms = 0; ms < MT; ++ms)
           af[ms] = __builtin_bit_cast(
-              bf16x8_t, afrag[(frag0 + ms * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
+              bf16x8_t, afrag[a_slot(b, ls, ms, t)]);
 #pragma unroll
         for (int mi = 0; mi < MATS; ++mi)
 #pragma unroll
@@ -1097,14 +1272,16 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
       f32x4_t neg[MT];
 #pragma unroll
       for (int ms = 0; ms < MT; ++ms)
-        neg[ms] = *reinterpret_cast<const f32x4_t*>(&offs[(frag0 + ms * 4) * 16 + jq * 4]);
+        neg[ms] = *reinterpret_cast<const f32x4_t*>(
+            &offs[kDirect ? (b * ps + ls) * kNegStride + ms * 16 + jq * 4
+                          : (frag0 + ms * 4) * 16 + jq * 4]);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         bf16x8_t af[MT];
 #pragma unroll
         for (int ms = 0; ms < MT; ++ms)
           af[ms] = __builtin_bit_cast(
-              bf16x8_t, afrag[(frag0 + ms * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq))]);
+              bf16x8_t, afrag[a_slot(b, ls, ms, t)]);
 #pragma unroll
         for (int mi = 0; mi < MATS; ++mi)
 #pragma unroll
@@ -1172,8 +1349,8 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
       }
     }
   } else {
-    // 64-row tiles: passes of kStPassSteps k-steps; the ring is one pass deep
-    // (its first kStPassSteps slots), so slot j serves local step j
+    // 64- and 80-row tiles: passes of kPS k-steps; the ring is one pass deep
+    // (its first kPS slots), so slot j serves local step j
     // No exit inside a pass (see the 16-row loop): a partial last pass skips
     // the compute of its missing steps only.
     const int passes = (ksteps + ps - 1) / ps;
@@ -1183,7 +1360,10 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
       const int b = p % kNBuf;
       const bool more = p + 1 < passes;
       const int units1 = more ? pass_steps(p + 1) * kRows * 16 : 0;
-      if (more) {
+      if constexpr (kDirect) {
+        // the next pass's buffer was retired by the previous pass's barrier
+        if (more) direct_pass(p + 1, (p + 1) % kNBuf);
+      } else if (more) {
 #pragma unroll
         for (int q = 0; q < kPassUnits; ++q) {
           const int u = q * kThreads + tid;
@@ -1194,18 +1374,22 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
         }
       }
 #pragma unroll
-      for (int j = 0; j < kStPassSteps; ++j) {
+      for (int j = 0; j < kPS; ++j) {
         const int step = p * ps + j;
         if (step < ksteps) compute_step(w[j], step, b, j);
-        w[j].load(wrow, srow, step + kStPassSteps, jq, K, gshift, ksteps, dummy);
+        w[j].load(wrow, srow, step + kPS, jq, K, gshift, ksteps, dummy);
       }
       if (more) {
         // publish the next pass; the barrier also retires this pass's buffer,
         // which the pass after next overwrites
+        if constexpr (kDirect) {
+          wait_vmcnt<kAfter>();  // this wave's direct loads landed
+        } else {
 #pragma unroll
-        for (int q = 0; q < kPassUnits; ++q) {
-          const int u = q * kThreads + tid;
-          if (u < units1 && unit_live(u)) unit_store((p + 1) % kNBuf, u, vnext[q], snext[q]);
+          for (int q = 0; q < kPassUnits; ++q) {
+            const int u = q * kThreads + tid;
+            if (u < units1 && unit_live(u)) unit_store((p + 1) % kNBuf, u, vnext[q], snext[q]);
+          }
         }
         __syncthreads();
       }
@@ -1285,16 +1469,40 @@ w4a16_stream_kernel(const GemmArgs g) {
     }
     return;
   }
+  // 64-row gather / scatter launches with 128-wide k-steps take their
+  // activations by direct loads, in every tile path below
+  constexpr bool kDirect = MT > 1 && WIDE && (FMT == kFmtW4A16 || FMT == kFmtMxBf16) &&
+                           GATHER != SCATTER && !DENSE;
+  if constexpr (kDirect) {
+    // an expert's last tile of <= 16 rows rides with the 64-row tile before
+    // it: that tile's block makes one pass over the expert's weights for up
+    // to 80 rows, and this tile's block has nothing left to do
+    const int4* const td = reinterpret_cast<const int4*>(g.tiles);
+    if (rows <= 16 && tile > 0) {
+      const int4 pv = td[tile - 1];
+      if (pv.x == expert && pv.z == 64 && pv.y + 64 == row0) return;
+    }
+    if (rows == 64 && tile + 1 < *g.tile_count) {
+      const int4 nx = td[tile + 1];
+      if (nx.x == expert && nx.z <= 16 && nx.y == row0 + 64) {
+        stream_tile<FMT, MATS, NT, 5, WIDE, GATHER, SCATTER, DENSE, true>(g, expert, row0,
+                                                                          64 + nx.z, cb, osel);
+        return;
+      }
+    }
+  }
   // a tile of at most 16 rows (an expert's last rows) takes the 16-row path:
   // a quarter of the MFMAs and all of its activations resident (the host
   // sets tail16 when they fit the launch's LDS)
   if constexpr (MT > 1) {
     if (rows <= 16 && g.tail16) {
-      stream_tile<FMT, MATS, NT, 1, WIDE, GATHER, SCATTER, DENSE>(g, expert, row0, rows, cb, osel);
+      stream_tile<FMT, MATS, NT, 1, WIDE, GATHER, SCATTER, DENSE, kDirect>(g, expert, row0, rows,
+                                                                           cb, osel);
       return;
     }
   }
-  stream_tile<FMT, MATS, NT, MT, WIDE, GATHER, SCATTER, DENSE>(g, expert, row0, rows, cb, osel);
+  stream_tile<FMT, MATS, NT, MT, WIDE, GATHER, SCATTER, DENSE, kDirect>(g, expert, row0, rows, cb,
+                                                                        osel);
 }
 
 // ---------------------------------------------------------------------------
@@ -1875,7 +2083,9 @@ size_t split_bytes(int64_t elems) {
 
 struct MoeLayout {
   SchedLayout sched;
-  size_t offsets, perm, tiles, count, act, eo, x_split, act_split, total;
+  size_t offsets, perm, tiles, count, act, eo, x_split, act_split;
+  size_t x_pair, x_neg, act_pair, act_neg;  // paired W4A16 activations (direct loads)
+  size_t total;
 };
 
 // Pointers into one fp8 split region of `elems` values: hi, lo, exponent words.
@@ -1894,7 +2104,7 @@ SplitBufs split_bufs(char* base, int64_t elems) {
 }
 
 MoeLayout moe_layout(int64_t entries, int64_t experts, int64_t act_cols, int64_t out_cols,
-                     int64_t split_x_elems = 0) {
+                     int64_t split_x_elems = 0, int64_t pair_rows = 0) {
   MoeLayout l;
   l.sched = sched_layout(entries, experts);
   size_t at = l.sched.total;
@@ -1916,6 +2126,17 @@ MoeLayout moe_layout(int64_t entries, int64_t experts, int64_t act_cols, int64_t
   at += split_bytes(split_x_elems);
   l.act_split = at;
   if (split_x_elems > 0) at += split_bytes(entries * act_cols);
+  // W4A16 64-row launches: the gathered input (pair_rows rows of out_cols)
+  // and the activations paired for direct loads, with their group sums
+  const bool pairs = pair_rows > 0;
+  l.x_pair = at;
+  if (pairs) at += align_up(static_cast<size_t>(pair_rows) * out_cols * 2);
+  l.x_neg = at;
+  if (pairs) at += align_up(static_cast<size_t>(pair_rows) * (out_cols / 128) * 4);
+  l.act_pair = at;
+  if (pairs) at += align_up(static_cast<size_t>(entries) * act_cols * 2);
+  l.act_neg = at;
+  if (pairs) at += align_up(static_cast<size_t>(entries) * (act_cols / 128) * 4);
   l.total = at;
   return l;
 }
@@ -1970,6 +2191,18 @@ int schedule_launch(const RouteTable& rt, int64_t entries, char* ws, const Sched
   if (sl.chunks > 1)
     schedule_place_kernel<<<sl.chunks, kSchedThreads, 0, s>>>(rt, entries, sl.chunks, sc);
   return check_launch("moe schedule");
+}
+
+// Paired copy + group sums of `rows` bf16 rows of k (k % 128 == 0) for the
+// direct-load W4A16 GEMM.
+int pair_rows_launch(const uint16_t* x, uint16_t* xp, float* neg, int64_t rows, int64_t k,
+                     hipStream_t s) {
+  const int64_t units = rows * (k / 128);
+  if (units == 0) return LK_OK;
+  LK_REQUIRE(k % 128 == 0 && units < (1LL << 27), "pairing: unsupported size");
+  pair_rows_kernel<<<static_cast<unsigned>((units + 15) / 16), 256, 0, s>>>(
+      x, xp, neg, static_cast<uint32_t>(units));
+  return check_launch("moe activation pairing");
 }
 
 enum class Mode { Gather, Scatter, GatherScatter, Dense };
@@ -2169,6 +2402,13 @@ int stream_launch(GemmArgs g, Mode mode, int64_t tiles, int mt, hipStream_t s, c
   // 64-row launches: tiles of <= 16 rows run the 16-row path when all of
   // their activations fit the LDS the launch takes anyway
   g.tail16 = mt > 1 && stream_lds_bytes(g.k, 1) <= lds ? 1 : 0;
+  // 64-row gather / scatter launches load activations directly (byte
+  // offsets of 32 bits; W4A16 from the paired copy)
+  if (mt > 1 && wide && FMT != kFmtMxF8 && (mode == Mode::Gather || mode == Mode::Scatter)) {
+    LK_REQUIRE(g.a_rows > 0 && g.a_rows * g.k * 2 <= static_cast<int64_t>(kMaxDirectBytes),
+               "%s: activations out of range for direct loads", what);
+    LK_REQUIRE(FMT != kFmtW4A16 || (g.a_pair && g.a_neg), "%s: paired activations missing", what);
+  }
   g.col_blocks = static_cast<int>((g.n + kStWaves * NT * 16 - 1) / (kStWaves * NT * 16));
   const int64_t blocks = (tiles + 7) / 8 * 8 * g.col_blocks * g.outputs;
   LK_REQUIRE(blocks > 0 && blocks < (1LL << 31), "%s: too many blocks", what);
@@ -2254,6 +2494,12 @@ int stream_tile_mt(int64_t entries) {
     default: return entries <= kStreamSmallEntries ? 1 : 4;
   }
 }
+
+// Whether an expert-major W4A16 call of `entries` token-routes sizes the
+// paired-activation buffers of its 64-row launches into the workspace (the
+// workspace query and the call agree through this; calls whose group is not
+// 128 leave them unused).
+bool moe_pairs(int64_t entries, bool mx) { return !mx && stream_tile_mt(entries) == 4; }
 
 // W4A16: a power-of-two group (multiple of 32) dividing k; MXFP4: 32.
 int check_format(bool mx, int64_t k, int64_t group) {
@@ -2545,7 +2791,9 @@ int64_t lk_w4a16_moe_forward_workspace(int64_t tokens, int64_t experts, int64_t 
                                        int64_t top_k) {
   if (tokens < 0 || experts < 2 || h <= 0 || i <= 0 || top_k <= 0) return -1;
   if (check_schedule_dims(tokens, top_k + 1, experts)) return -1;
-  return static_cast<int64_t>(moe_layout(tokens * (top_k + 1), experts, i, h).total);
+  const int64_t entries = tokens * (top_k + 1);
+  return static_cast<int64_t>(
+      moe_layout(entries, experts, i, h, 0, moe_pairs(entries, false) ? tokens : 0).total);
 }
 
 int64_t lk_mxfp4_moe_forward_workspace(int64_t tokens, int64_t experts, int64_t h, int64_t i,
@@ -2593,7 +2841,8 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   LK_REQUIRE(x && logits && workspace, "null pointer argument");
   const int64_t routes = top_k + 1;
   const int64_t entries = tokens * routes;
-  const MoeLayout l = moe_layout(entries, experts, i, h, mx ? tokens * h : 0);
+  const MoeLayout l =
+      moe_layout(entries, experts, i, h, mx ? tokens * h : 0, moe_pairs(entries, mx) ? tokens : 0);
   LK_REQUIRE(workspace_bytes >= static_cast<int64_t>(l.total),
              "MoE workspace too small: %lld < %lld bytes", (long long)workspace_bytes,
              (long long)l.total);
@@ -2608,7 +2857,11 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   const int64_t group = mx ? 32 : group_size;
   int mt = stream_tile_mt(entries);
   if (mt && !(stream_fits(h, mt, group, mx) && stream_fits(i, mt, group, mx))) mt = 0;
+  // 64-row tiles load activations directly (32-bit byte offsets)
+  if (mt == 4 && (tokens * h * 2 > kMaxDirectBytes || entries * i * 2 > kMaxDirectBytes)) mt = 0;
   const int tr = mt == 1 ? kSmallTileRows : kTileRows;
+  // W4A16 G = 128 on 64-row tiles: x and the activations go in paired
+  const bool paired = !mx && mt == 4 && group == 128;
   if (route_schedule_fits(tokens, experts - 1, top_k)) {
     if (int rc = route_schedule_launch(logits, bias, expert_indices, weights, tokens, experts - 1,
                                        top_k, routed_scaling_factor, renormalize, offsets, perm,
@@ -2645,6 +2898,14 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.a_hi = xs.hi;
   g.a_lo = xs.lo;
   g.a_sc = xs.sc;
+  g.a_rows = tokens;
+  if (paired) {
+    g.a_pair = reinterpret_cast<uint16_t*>(ws + l.x_pair);
+    g.a_neg = reinterpret_cast<float*>(ws + l.x_neg);
+    if (int rc = pair_rows_launch(x, const_cast<uint16_t*>(g.a_pair), const_cast<float*>(g.a_neg),
+                                  tokens, h, s))
+      return rc;
+  }
   g.wp[0] = w1_packed;
   g.ws[0] = w1_scales;
   g.wp[1] = w3_packed;
@@ -2680,6 +2941,14 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.a_hi = as.hi;
   g.a_lo = as.lo;
   g.a_sc = as.sc;
+  g.a_rows = entries;
+  if (paired) {
+    g.a_pair = reinterpret_cast<uint16_t*>(ws + l.act_pair);
+    g.a_neg = reinterpret_cast<float*>(ws + l.act_neg);
+    if (int rc = pair_rows_launch(act, const_cast<uint16_t*>(g.a_pair),
+                                  const_cast<float*>(g.a_neg), entries, i, s))
+      return rc;
+  }
   g.wp[0] = g.wp[1] = g.wp[2] = w2_packed;
   g.ws[0] = g.ws[1] = g.ws[2] = w2_scales;
   g.out[0] = g.out[1] = g.out[2] = eo;

@@ -51,9 +51,10 @@ def random_bf16_bits(rng: np.random.Generator, shape, std: float = 1.0) -> np.nd
 
 def designed_counts(tokens: int, experts: int, top_k: int) -> np.ndarray:
     """Per-expert route counts for a prefill-sized batch whose expert tiles take
-    every shape: unused, a handful of rows, exactly one 64-row tile, a full
-    tile plus a tail of 1..16 rows (the 16-row path) or 17..63 rows (a partial
-    64-row tile), and several hundred rows with assorted tails."""
+    every shape: unused, a handful of rows (the 16-row path), exactly one 64-row
+    tile, a full tile plus a tail of 1..16 rows (which rides with the tile
+    before it, an 80-row pass) or 17..63 rows (a partial 64-row tile), and
+    several hundred rows with assorted tails."""
     head = [1, 16, 17, 0, 64, 65, 80, 81, 127, 128]
     assert experts > len(head)
     rest = experts - len(head)

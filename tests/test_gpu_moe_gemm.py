@@ -381,8 +381,10 @@ def designed_prefill():
 
 
 def test_prefill_every_token_matches_oracle(designed_prefill):
-    """Expert-major prefill (64-row tiles; tails of 1..16 rows on the 16-row
-    path, 17..63 rows as partial 64-row tiles): every token against the oracle."""
+    """Expert-major prefill (64-row tiles with activations loaded straight into
+    LDS; a tail of 1..16 rows rides with the 64-row tile before it as one
+    80-row pass, an expert of at most 16 rows takes the 16-row path, 17..63
+    rows are a partial 64-row tile): every token against the oracle."""
     from local_kimi_amd.kernels import w4a16_moe_forward
 
     x, logits, banks, counts, ey, eidx = designed_prefill
