@@ -304,6 +304,9 @@ struct GemmArgs {
   const uint16_t* a_pair;
   const float* a_neg;
   int64_t a_rows;
+  // W4A16 gate/up on those launches: write the activations paired (the down
+  // GEMM's a_pair) and their group sums here (its a_neg); null: plain rows
+  float* out_neg;
   const int32_t* perm;       // sorted position -> entry (gather / scatter modes)
   const int32_t* tiles;      // [*, 4] tile list (schedule modes)
   const int32_t* tile_count;
@@ -1396,25 +1399,72 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
     }
   }
 
+  auto out_value = [&](int nt, int ms, int i) -> uint16_t {
+    if constexpr (MATS == 2)
+      return g.act == kActSitu ? situ_bf16(tot[0][nt][ms][i], tot[1][nt][ms][i], g.situ_beta,
+                                           g.situ_linear_beta)
+                               : swiglu_bf16(tot[0][nt][ms][i], tot[1][nt][ms][i]);
+    else
+      return store_value<FMT>(tot[0][nt][ms][i]);
+  };
+  if constexpr (kDirect) {
+    // the tile goes through LDS ([row][column], rows padded by 8 values so
+    // that the 2-byte writes of 4 rows spread over the banks) and out as
+    // 16-byte chunks, a row's block columns contiguous. W4A16 gate/up with
+    // out_neg: each chunk paired and the 128-wide group sums written too, in
+    // the staging's order (the block's kBN = 128 columns are one group; the
+    // 16 chunks of a row sit in one 16-lane DPP row).
+    constexpr int kPitch = kBN + 8;
+    constexpr int kChunks = kBN / 8;
+    static_assert(kChunks % 16 == 0 && kThreads % 16 == 0, "chunks of a row fill DPP rows");
+    uint16_t* const otile = reinterpret_cast<uint16_t*>(smem);
+    __syncthreads();  // every wave has read its last activations
 #pragma unroll
-  for (int ms = 0; ms < MT; ++ms) {
-    if (ms >= mt_act) break;
+    for (int ms = 0; ms < MT; ++ms) {
+      if (ms >= mt_act) break;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = ms * 16 + jq * 4 + i;
-      if (m >= rows) continue;
-      const int64_t orow = out_row[m];
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        if (col[nt] >= N) continue;
-        uint16_t v;
-        if constexpr (MATS == 2)
-          v = g.act == kActSitu ? situ_bf16(tot[0][nt][ms][i], tot[1][nt][ms][i], g.situ_beta,
-                                            g.situ_linear_beta)
-                                : swiglu_bf16(tot[0][nt][ms][i], tot[1][nt][ms][i]);
-        else
-          v = store_value<FMT>(tot[0][nt][ms][i]);
-        out[orow * N + col[nt]] = v;
+        for (int nt = 0; nt < NT; ++nt)
+          otile[(ms * 16 + jq * 4 + i) * kPitch + (wv * NT + nt) * 16 + ln] = out_value(nt, ms, i);
+    }
+    __syncthreads();
+    constexpr bool kPairOut = FMT == kFmtW4A16 && MATS == 2;
+    static_assert(!kPairOut || kBN == 128, "paired output: one group per block");
+    for (int u = tid; u < kRows * kChunks; u += kThreads) {
+      const int m = u / kChunks, c = u - m * kChunks;
+      const uint4 v = *reinterpret_cast<const uint4*>(otile + m * kPitch + c * 8);
+      const int64_t c0 = static_cast<int64_t>(cb) * kBN + c * 8;
+      const bool live = m < rows && c0 < N;
+      if constexpr (kPairOut) {
+        if (g.out_neg) {
+          uint32_t q[4];
+          pair_x8(v, q);
+          float sx = sum8(sum_x8_dot(v));
+          sx += dpp_f32<kRowMirror>(sx);
+          if (live) {
+            *reinterpret_cast<uint4*>(out + out_row[m] * N + c0) = make_uint4(q[0], q[1], q[2], q[3]);
+            if (c == 0) g.out_neg[out_row[m] * (N / 128) + cb] = -kCodeOffset * sx;
+          }
+          continue;
+        }
+      }
+      if (live) *reinterpret_cast<uint4*>(out + out_row[m] * N + c0) = v;
+    }
+  } else {
+#pragma unroll
+    for (int ms = 0; ms < MT; ++ms) {
+      if (ms >= mt_act) break;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = ms * 16 + jq * 4 + i;
+        if (m >= rows) continue;
+        const int64_t orow = out_row[m];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          if (col[nt] >= N) continue;
+          out[orow * N + col[nt]] = out_value(nt, ms, i);
+        }
       }
     }
   }
@@ -2084,7 +2134,7 @@ size_t split_bytes(int64_t elems) {
 struct MoeLayout {
   SchedLayout sched;
   size_t offsets, perm, tiles, count, act, eo, x_split, act_split;
-  size_t x_pair, x_neg, act_pair, act_neg;  // paired W4A16 activations (direct loads)
+  size_t x_pair, x_neg, act_neg;  // paired W4A16 input and group sums (direct loads)
   size_t total;
 };
 
@@ -2127,14 +2177,13 @@ MoeLayout moe_layout(int64_t entries, int64_t experts, int64_t act_cols, int64_t
   l.act_split = at;
   if (split_x_elems > 0) at += split_bytes(entries * act_cols);
   // W4A16 64-row launches: the gathered input (pair_rows rows of out_cols)
-  // and the activations paired for direct loads, with their group sums
+  // paired for direct loads, its group sums and the activations' group sums
+  // (the gate/up GEMM writes the activations paired in place)
   const bool pairs = pair_rows > 0;
   l.x_pair = at;
   if (pairs) at += align_up(static_cast<size_t>(pair_rows) * out_cols * 2);
   l.x_neg = at;
   if (pairs) at += align_up(static_cast<size_t>(pair_rows) * (out_cols / 128) * 4);
-  l.act_pair = at;
-  if (pairs) at += align_up(static_cast<size_t>(entries) * act_cols * 2);
   l.act_neg = at;
   if (pairs) at += align_up(static_cast<size_t>(entries) * (act_cols / 128) * 4);
   l.total = at;
@@ -2408,6 +2457,8 @@ int stream_launch(GemmArgs g, Mode mode, int64_t tiles, int mt, hipStream_t s, c
     LK_REQUIRE(g.a_rows > 0 && g.a_rows * g.k * 2 <= static_cast<int64_t>(kMaxDirectBytes),
                "%s: activations out of range for direct loads", what);
     LK_REQUIRE(FMT != kFmtW4A16 || (g.a_pair && g.a_neg), "%s: paired activations missing", what);
+    LK_REQUIRE(g.n % 8 == 0 && (!g.out_neg || (MATS == 2 && g.n % 128 == 0)),
+               "%s: output width %lld unsupported for direct loads", what, (long long)g.n);
   }
   g.col_blocks = static_cast<int>((g.n + kStWaves * NT * 16 - 1) / (kStWaves * NT * 16));
   const int64_t blocks = (tiles + 7) / 8 * 8 * g.col_blocks * g.outputs;
@@ -2913,6 +2964,7 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.wp[2] = w1_packed;
   g.ws[2] = w1_scales;
   g.out[0] = g.out[1] = g.out[2] = act;
+  if (paired) g.out_neg = reinterpret_cast<float*>(ws + l.act_neg);
   g.n = i;
   g.k = h;
   g.wstride = i * h / 2;
@@ -2942,12 +2994,10 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.a_lo = as.lo;
   g.a_sc = as.sc;
   g.a_rows = entries;
-  if (paired) {
-    g.a_pair = reinterpret_cast<uint16_t*>(ws + l.act_pair);
-    g.a_neg = reinterpret_cast<float*>(ws + l.act_neg);
-    if (int rc = pair_rows_launch(act, const_cast<uint16_t*>(g.a_pair),
-                                  const_cast<float*>(g.a_neg), entries, i, s))
-      return rc;
+  if (paired) {  // written paired by the gate/up GEMM, with their group sums
+    g.a_pair = act;
+    g.a_neg = g.out_neg;
+    g.out_neg = nullptr;
   }
   g.wp[0] = g.wp[1] = g.wp[2] = w2_packed;
   g.ws[0] = g.ws[1] = g.ws[2] = w2_scales;
