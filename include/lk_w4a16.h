@@ -153,6 +153,19 @@ LK_API int lk_moe_router(const float* logits, const float* bias, int64_t* expert
                   float* weights, int64_t tokens, int64_t experts, int64_t top_k,
                   float routed_scaling_factor, int renormalize, void* stream);
 
+/* ---- grouped top-k router: engine/klinear/router.py:62-80 (num_expert_group,
+ *      topk_group; on precomputed fp32 logits)
+ * Group score = sum of the group's two largest choice scores (the largest
+ * alone when a group holds one expert); the topk_group best groups are kept
+ * (ties to the lower group), every other expert's choice becomes 0.0, then
+ * the selection and weights of lk_moe_router. Requires experts <= 1024,
+ * experts % num_expert_group == 0, num_expert_group <= 64,
+ * 1 <= topk_group <= num_expert_group, top_k <= 32. */
+LK_API int lk_moe_router_grouped(const float* logits, const float* bias, int64_t* expert_indices,
+                                 float* weights, int64_t tokens, int64_t experts, int64_t top_k,
+                                 int64_t num_expert_group, int64_t topk_group,
+                                 float routed_scaling_factor, int renormalize, void* stream);
+
 /* ---- first stage of the MoE block: router + gate/up + SwiGLU in one launch
  *      (engine/klinear/router.py:47-85, engine/kernels/__init__.py:182-197)
  * Writes expert_indices int64 [T,top_k], weights fp32 [T,top_k] and

@@ -34,6 +34,7 @@ SIGNATURES: dict[str, list] = {
     "lk_route_combine": [_P, _P, _P, _I64, _I64, _I64, _P],
     "lk_w4a16_w2_combine": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
     "lk_moe_router": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _I, _P],
+    "lk_moe_router_grouped": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _P],
     "lk_router_logits": [_P, _P, _P, _I64, _I64, _I64, _P],
     "lk_w4a16_moe_gateup": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                             _I64, _I64, _I64, _I64, _I64, _F, _I, _I64, _P],

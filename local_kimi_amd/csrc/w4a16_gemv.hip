@@ -544,6 +544,105 @@ router_kernel(const float* __restrict__ logits, const float* __restrict__ bias,
 }
 
 // ---------------------------------------------------------------------------
+// Grouped top-k router (engine/klinear/router.py:62-80), one wave per token:
+// the experts split into `groups` equal groups; a group's score is the sum of
+// its two largest choice scores (sigmoid + bias; the largest alone for
+// one-expert groups); the topk_group best groups are kept (ties to the lower
+// group) and every expert of the other groups gets choice 0.0 (a masked fill,
+// not -inf: such an expert still outranks a kept one whose choice is
+// negative). The top_k selection then runs on the masked choices exactly as
+// the ungrouped router does (descending, ties to the lower id), and the
+// weights are the unbiased sigmoid scores, summed in selection order for the
+// renormalisation.
+constexpr int kGroupedMaxExperts = 1024;
+constexpr int kGroupedEpl = kGroupedMaxExperts / kWave;
+
+__global__ void __launch_bounds__(kWave)
+router_grouped_kernel(const float* __restrict__ logits, const float* __restrict__ bias,
+                      int64_t* __restrict__ idx, float* __restrict__ w, int experts, int top_k,
+                      int groups, int topk_group, float scaling, int renorm) {
+  __shared__ float choice[kGroupedMaxExperts];
+  __shared__ float score[kGroupedMaxExperts];
+  const int lane = threadIdx.x;
+  const int64_t t = blockIdx.x;
+  const float* lg = logits + t * experts;
+  for (int e = lane; e < experts; e += kWave) {
+    const float sc = 1.0f / (1.0f + expf(-lg[e]));
+    score[e] = sc;
+    choice[e] = sc + (bias != nullptr ? bias[e] : 0.f);
+  }
+  __syncthreads();
+  const int per = experts / groups;
+  // one lane per group: the sum of the group's two largest choices
+  uint32_t gkey = 0u;
+  if (lane < groups) {
+    float t1 = -INFINITY, t2 = -INFINITY;
+    for (int j = 0; j < per; ++j) {
+      const float v = choice[lane * per + j];
+      if (v > t1) {
+        t2 = t1;
+        t1 = v;
+      } else if (v > t2) {
+        t2 = v;
+      }
+    }
+    gkey = max(orderable(per >= 2 ? t1 + t2 : t1), 1u);  // live groups rank above lanes past them
+  }
+  uint64_t kept = 0;
+  for (int rr = 0; rr < topk_group; ++rr) {
+    const uint32_t kmax = wave_max_u32(gkey);
+    const uint64_t holders = __builtin_amdgcn_ballot_w64(gkey == kmax);
+    const int owner = static_cast<int>(__builtin_ctzll(holders | (1ull << 63)));
+    kept |= 1ull << owner;
+    if (lane == owner) gkey = 0u;
+  }
+  // lane l holds experts l * epl .. l * epl + epl - 1 (contiguous, so among
+  // lanes holding equal keys the lowest lane holds the lowest id)
+  const int epl = (experts + kWave - 1) / kWave;
+  uint32_t key[kGroupedEpl];
+#pragma unroll
+  for (int j = 0; j < kGroupedEpl; ++j) {
+    const int e = lane * epl + j;
+    const bool live = j < epl && e < experts;
+    const float c = live ? choice[e] : 0.f;
+    key[j] = live ? max(orderable(((kept >> (e / per)) & 1ull) ? c : 0.0f), 1u) : 0u;
+  }
+  float ssum = 0.f, my_score = 0.f;
+  int64_t mine = -1;
+  for (int rr = 0; rr < top_k; ++rr) {
+    uint32_t best = 0u;
+    int bj = 0;
+#pragma unroll
+    for (int j = 0; j < kGroupedEpl; ++j) {
+      if (key[j] > best) {  // strict: equal keys keep the lower id
+        best = key[j];
+        bj = j;
+      }
+    }
+    const uint32_t kmax = wave_max_u32(best);
+    const uint64_t holders = __builtin_amdgcn_ballot_w64(best == kmax);
+    const int owner = static_cast<int>(__builtin_ctzll(holders | (1ull << 63)));
+    const int j_own = __builtin_amdgcn_readlane(bj, owner);
+    const int sel = min(owner * epl + j_own, experts - 1);  // top_k <= experts: always live
+    const float sc = score[sel];
+    if (lane == owner) {
+#pragma unroll
+      for (int j = 0; j < kGroupedEpl; ++j) key[j] = j == bj ? 0u : key[j];
+    }
+    ssum += sc;
+    if (lane == rr) {
+      mine = sel;
+      my_score = sc;
+    }
+  }
+  if (lane < top_k) {
+    const float denom = ssum + 1e-20f;
+    idx[t * top_k + lane] = mine;
+    w[t * top_k + lane] = (renorm && top_k > 1) ? (my_score / denom) * scaling : my_score * scaling;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // decode: router + gate/up + SwiGLU for route r of token t in one kernel.
 // blockIdx.y = t * (top_k + 1) + r; route top_k is the shared expert (bank
 // entry experts - 1). Each wave recomputes the token's routing (a few hundred
@@ -1266,6 +1365,31 @@ int lk_moe_router(const float* logits, const float* bias, int64_t* expert_indice
     router_kernel<16><<<static_cast<unsigned>(tokens), 64, 0, s>>>(
         logits, bias, expert_indices, weights, experts, k, routed_scaling_factor, renormalize);
   return check_launch("lk_moe_router");
+}
+
+int lk_moe_router_grouped(const float* logits, const float* bias, int64_t* expert_indices,
+                          float* weights, int64_t tokens, int64_t experts, int64_t top_k,
+                          int64_t num_expert_group, int64_t topk_group,
+                          float routed_scaling_factor, int renormalize, void* stream) {
+  LK_REQUIRE(experts > 0 && experts <= kGroupedMaxExperts,
+             "router supports 1..%d experts, got %lld", kGroupedMaxExperts, (long long)experts);
+  LK_REQUIRE(top_k > 0 && top_k <= 32 && top_k <= experts, "invalid top_k %lld",
+             (long long)top_k);
+  LK_REQUIRE(num_expert_group >= 1 && num_expert_group <= kWave,
+             "num_expert_group must be 1..%d, got %lld", kWave, (long long)num_expert_group);
+  LK_REQUIRE(experts % num_expert_group == 0,
+             "num_experts must be divisible by num_expert_group");
+  LK_REQUIRE(topk_group >= 1 && topk_group <= num_expert_group,
+             "topk_group must be 1..num_expert_group, got %lld", (long long)topk_group);
+  LK_REQUIRE(tokens >= 0, "negative token count");
+  if (tokens == 0) return LK_OK;
+  LK_REQUIRE(logits && expert_indices && weights, "null pointer argument");
+  LK_REQUIRE(tokens <= 2147483647LL, "too many tokens");
+  router_grouped_kernel<<<static_cast<unsigned>(tokens), kWave, 0, as_stream(stream)>>>(
+      logits, bias, expert_indices, weights, static_cast<int>(experts), static_cast<int>(top_k),
+      static_cast<int>(num_expert_group), static_cast<int>(topk_group), routed_scaling_factor,
+      renormalize);
+  return check_launch("lk_moe_router_grouped");
 }
 
 static int moe_gateup_launch(const uint16_t* x, const float* logits, const float* bias,

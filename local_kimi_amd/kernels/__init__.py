@@ -20,7 +20,7 @@ from . import registry
 from .kda import fused_kda_gates, fused_short_conv_triple, kda_decode_layer, kda_decode_step
 from .moe import (moe_router, moe_schedule, router_logits, shape_stable_expert_indices, w4a16_moe_block,
                   w4a16_moe_block_reference, w4a16_moe_decode, w4a16_moe_forward,
-                  w4a16_moe_gateup)
+                  w4a16_moe_gateup, w4a16_moe_routed)
 from .mxfp4 import (grouped_mxfp4_gemm, grouped_mxfp4_reference, grouped_mxfp4_swiglu_gemm,
                     mxfp4_expert_mlp, mxfp4_gemm, mxfp4_gemm_reference, mxfp4_linear,
                     mxfp4_moe_block, mxfp4_moe_block_reference, split_activations_fp8)
@@ -147,6 +147,7 @@ __all__ = [
     "W4A16_W2_COMBINE", "W4A16_MOE_BLOCK", "moe_router", "router_logits",
     "shape_stable_expert_indices",
     "w4a16_moe_block", "w4a16_moe_decode", "w4a16_moe_forward", "w4a16_moe_gateup",
+    "w4a16_moe_routed",
     "moe_schedule", "w4a16_dense", "w4a16_dense_gemm", "grouped_w4a16_gemv",
     "grouped_w4a16_gemm", "grouped_w4a16_swiglu_gemv", "grouped_w4a16_swiglu_gemm",
     "fused_w2_combine", "fused_qkv_w4a16", "route_combine", "silu_mul",

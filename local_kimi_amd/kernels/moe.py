@@ -92,15 +92,24 @@ def _validate_router(logits: torch.Tensor, bias: torch.Tensor | None, top_k: int
 
 
 def moe_router(logits: torch.Tensor, bias: torch.Tensor | None, top_k: int, *,
-               routed_scaling_factor: float = 1.0,
-               renormalize: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+               routed_scaling_factor: float = 1.0, renormalize: bool = True,
+               num_expert_group: int = 1,
+               topk_group: int = 1) -> tuple[torch.Tensor, torch.Tensor]:
     """Sigmoid top-k routing: ``(idx int64 [T, k], weights float32 [T, k])``.
 
     Selections are ordered by descending ``sigmoid(logit) + bias``, ties to the
     lower expert id; weights are the un-biased sigmoid scores, renormalised by
     ``sum + 1e-20`` (when ``top_k > 1`` and ``renormalize``) and scaled.
+    ``num_expert_group > 1`` is the grouped top-k of router.py:62-80: groups
+    ranked by the sum of their two largest choice scores, the best
+    ``topk_group`` kept, every other expert's choice masked to 0.0.
     """
     tokens, experts = _validate_router(logits, bias, top_k)
+    num_expert_group, topk_group = int(num_expert_group), int(topk_group)
+    if num_expert_group < 1 or experts % num_expert_group:
+        raise ValueError("num_experts must be divisible by num_expert_group")
+    if num_expert_group > 1 and not 1 <= topk_group <= num_expert_group:
+        raise ValueError("topk_group must lie in 1..num_expert_group")
     idx = torch.empty((tokens, top_k), dtype=torch.long, device=logits.device)
     w = torch.empty((tokens, top_k), dtype=torch.float32, device=logits.device)
     if tokens == 0:
@@ -108,9 +117,17 @@ def moe_router(logits: torch.Tensor, bias: torch.Tensor | None, top_k: int, *,
     lg = _w._c(logits)
     b = _w._c(bias) if bias is not None else None
     with torch.cuda.device(logits.device):
-        _lib.call("lk_moe_router", lg.data_ptr(), b.data_ptr() if b is not None else None,
-                  idx.data_ptr(), w.data_ptr(), tokens, experts, top_k,
-                  float(routed_scaling_factor), int(bool(renormalize)), _w._stream(logits.device))
+        if num_expert_group > 1:
+            _lib.call("lk_moe_router_grouped", lg.data_ptr(),
+                      b.data_ptr() if b is not None else None, idx.data_ptr(), w.data_ptr(),
+                      tokens, experts, top_k, num_expert_group, topk_group,
+                      float(routed_scaling_factor), int(bool(renormalize)),
+                      _w._stream(logits.device))
+        else:
+            _lib.call("lk_moe_router", lg.data_ptr(), b.data_ptr() if b is not None else None,
+                      idx.data_ptr(), w.data_ptr(), tokens, experts, top_k,
+                      float(routed_scaling_factor), int(bool(renormalize)),
+                      _w._stream(logits.device))
     return idx, w
 
 
@@ -185,14 +202,26 @@ def _validate_block(hidden, logits, bias, w1_packed, w1_scales, w3_packed, w3_sc
 
 def w4a16_moe_block(hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor | None,
                     w1_packed, w1_scales, w3_packed, w3_scales, w2_packed, w2_scales, top_k: int,
-                    routed_scaling_factor: float = 1.0, renormalize: bool = True):
+                    routed_scaling_factor: float = 1.0, renormalize: bool = True, *,
+                    num_expert_group: int = 1, topk_group: int = 1):
     """Router + SwiGLU experts + W2 + combine + shared expert on HIP.
 
     Fewer than ``MOE_EXPERT_MAJOR_MIN_TOKENS`` tokens: two launches per call
     (token-major decode). More tokens: the expert-major path
-    (:func:`w4a16_moe_forward`).
+    (:func:`w4a16_moe_forward`). Grouped top-k routing (``num_expert_group >
+    1``) routes with :func:`moe_router` first, then runs
+    :func:`w4a16_moe_routed` on those routes.
     Returns ``(y bf16 [T, H], expert_indices int64 [T, k], weights float32 [T, k])``.
     """
+    if num_expert_group != 1:
+        _validate_block(hidden, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
+                        w2_packed, w2_scales, top_k)
+        idx, w = moe_router(logits, bias, top_k, routed_scaling_factor=routed_scaling_factor,
+                            renormalize=renormalize, num_expert_group=num_expert_group,
+                            topk_group=topk_group)
+        y = w4a16_moe_routed(hidden, idx, w, w1_packed, w1_scales, w3_packed, w3_scales,
+                             w2_packed, w2_scales)
+        return y, idx, w
     expert_major_fits = hidden.ndim == 2 and w1_packed.ndim == 3 and \
         w1_packed.shape[0] <= MOE_EXPERT_MAJOR_MAX_EXPERTS
     if expert_major_fits and (hidden.shape[0] >= MOE_EXPERT_MAJOR_MIN_TOKENS or
@@ -201,6 +230,42 @@ def w4a16_moe_block(hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Tens
                                  w2_packed, w2_scales, top_k, routed_scaling_factor, renormalize)
     return w4a16_moe_decode(hidden, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
                             w2_packed, w2_scales, top_k, routed_scaling_factor, renormalize)
+
+
+def w4a16_moe_routed(hidden: torch.Tensor, expert_indices: torch.Tensor,
+                     combine_weights: torch.Tensor, w1_packed, w1_scales, w3_packed, w3_scales,
+                     w2_packed, w2_scales) -> torch.Tensor:
+    """The block on routes chosen elsewhere (klinear/moe.py:278-334's sequence).
+
+    ``expert_indices`` int64 ``[T, k]`` into the routed experts and
+    ``combine_weights`` float32 ``[T, k]``; the shared expert (bank entry
+    ``E - 1``) is appended as a last route of weight 1. Gate/up + SwiGLU on the
+    ``[T, k + 1]`` routes (GEMV or expert-major GEMM by size), then W2 with the
+    weighted combine in one launch for small batches, or the grouped W2 over
+    ``[T (k + 1), I]`` single-route rows and the route combine.
+    Returns ``y`` bf16 ``[T, H]``.
+    """
+    e_total = w1_packed.shape[0]
+    if expert_indices.ndim != 2 or expert_indices.dtype != torch.long:
+        raise TypeError("expert_indices must be an int64 [tokens, top_k] matrix")
+    if combine_weights.dtype != torch.float32 or combine_weights.shape != expert_indices.shape:
+        raise TypeError("combine_weights must be a float32 matrix shaped like expert_indices")
+    tokens, top_k = expert_indices.shape
+    if hidden.ndim != 2 or hidden.shape[0] != tokens:
+        raise ValueError("hidden states must be [tokens, hidden] with one row per route row")
+    stable = shape_stable_expert_indices(expert_indices, e_total - 1)
+    act = _w.grouped_w4a16_swiglu_gemv(hidden, stable, w1_packed, w1_scales, w3_packed,
+                                       w3_scales)
+    cw = torch.cat((combine_weights,
+                    torch.ones((tokens, 1), dtype=torch.float32, device=combine_weights.device)),
+                   dim=1)
+    inter = act.shape[-1]
+    if tokens < MOE_EXPERT_MAJOR_MIN_TOKENS and decode_supported(w1_packed, top_k):
+        return _w.fused_w2_combine(act.reshape(tokens, top_k + 1, inter), stable, cw, w2_packed,
+                                   w2_scales)
+    eo = _w.grouped_w4a16_gemv(act.reshape(tokens * (top_k + 1), inter),
+                               stable.reshape(tokens * (top_k + 1), 1), w2_packed, w2_scales)
+    return _w.route_combine(eo.reshape(tokens, top_k + 1, -1), cw)
 
 
 def decode_supported(w1_packed: torch.Tensor, top_k: int) -> bool:
@@ -306,12 +371,14 @@ def w4a16_moe_gateup(hidden: torch.Tensor, logits: torch.Tensor, bias: torch.Ten
 
 def w4a16_moe_block_reference(hidden, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
                               w2_packed, w2_scales, top_k: int, routed_scaling_factor: float = 1.0,
-                              renormalize: bool = True):
+                              renormalize: bool = True, *, num_expert_group: int = 1,
+                              topk_group: int = 1):
     """The same block composed from the reference-rounding ops (moe.py:278-334)."""
     tokens, e_total, h, inter, _ = _validate_block(hidden, logits, bias, w1_packed, w1_scales,
                                                    w3_packed, w3_scales, w2_packed, w2_scales, top_k)
     idx, w = moe_router(logits, bias, top_k, routed_scaling_factor=routed_scaling_factor,
-                        renormalize=renormalize)
+                        renormalize=renormalize, num_expert_group=num_expert_group,
+                        topk_group=topk_group)
     stable = shape_stable_expert_indices(idx, e_total - 1)
     gate = _w.grouped_w4a16_reference(hidden, stable, w1_packed, w1_scales)
     up = _w.grouped_w4a16_reference(hidden, stable, w3_packed, w3_scales)

@@ -66,7 +66,8 @@ class KLinearMoE(nn.Module):
     def __init__(self, gate_weight: torch.Tensor, e_score_correction_bias: torch.Tensor | None,
                  banks: MoeBanks, *, top_k: int = TOP_K,
                  routed_scaling_factor: float = ROUTED_SCALING_FACTOR,
-                 renormalize: bool = True) -> None:
+                 renormalize: bool = True, num_expert_group: int = 1,
+                 topk_group: int = 1) -> None:
         super().__init__()
         experts, hidden = gate_weight.shape
         if banks.w1_packed.shape[0] != experts + 1:
@@ -78,6 +79,11 @@ class KLinearMoE(nn.Module):
         self.top_k = top_k
         self.routed_scaling_factor = routed_scaling_factor
         self.renormalize = renormalize
+        # grouped top-k (router.py:62-80); Kimi-Linear uses one group
+        if num_expert_group < 1 or experts % num_expert_group:
+            raise ValueError("num_experts must be divisible by num_expert_group")
+        self.num_expert_group = num_expert_group
+        self.topk_group = topk_group
         # the router computes in fp32 (router.py:51) from the weight as stored
         # (bf16 in the checkpoint layout, exact in fp32)
         self.register_buffer("gate_weight", gate_weight.contiguous(), persistent=False)
@@ -110,9 +116,11 @@ class KLinearMoE(nn.Module):
         flat = hidden_states.reshape(-1, self.hidden_size)
         if self._block is None:
             self._block = registry.resolve(W4A16_MOE_BLOCK)
+        grouping = {} if self.num_expert_group == 1 else {
+            "num_expert_group": self.num_expert_group, "topk_group": self.topk_group}
         y, _, _ = self._block(flat, self.router_logits(flat), self.e_score_correction_bias,
                               *self.banks.as_tuple(), self.top_k, self.routed_scaling_factor,
-                              self.renormalize)
+                              self.renormalize, **grouping)
         return y.reshape(original_shape)
 
 

@@ -111,7 +111,8 @@ def w2_combine(activated_bits, expert_indices, combine_weights, w2_packed, w2_sc
 
 def moe_block(x_bits, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
               w2_packed, w2_scales, *, top_k: int, routed_scaling_factor: float,
-              group_size: int, renormalize: bool = True):
+              group_size: int, renormalize: bool = True, num_expert_group: int = 1,
+              topk_group: int = 1):
     """The grouped W4A16 MoE block with its router.
 
     Follows KLinearMoE.forward's grouped branch (klinear/moe.py:375-398,
@@ -121,7 +122,8 @@ def moe_block(x_bits, logits, bias, w1_packed, w1_scales, w3_packed, w3_scales,
     """
     num_routed = w1_packed.shape[0] - 1
     idx, w = route(logits, bias, top_k, routed_scaling_factor=routed_scaling_factor,
-                   renormalize=renormalize)
+                   renormalize=renormalize, num_expert_group=num_expert_group,
+                   topk_group=topk_group)
     stable = shape_stable_expert_indices(idx, num_routed)
     act = swiglu(x_bits, stable, w1_packed, w1_scales, w3_packed, w3_scales, group_size)
     t_count = act.shape[0]

@@ -56,6 +56,23 @@ def test_argument_errors_are_reported_without_touching_the_gpu(lib):
         _lib.call("lk_moe_router", 1, None, 1, 1, 1, 4, 9, 1.0, 1, None)
 
 
+def test_grouped_router_argument_errors(lib):
+    # (logits, bias, idx, w, tokens, experts, top_k, groups, topk_group, scale, renorm, stream)
+    with pytest.raises(RuntimeError, match="divisible"):
+        _lib.call("lk_moe_router_grouped", 1, None, 1, 1, 1, 10, 2, 4, 1, 1.0, 1, None)
+    with pytest.raises(RuntimeError, match="topk_group"):
+        _lib.call("lk_moe_router_grouped", 1, None, 1, 1, 1, 16, 2, 4, 5, 1.0, 1, None)
+    with pytest.raises(RuntimeError, match="num_expert_group"):
+        _lib.call("lk_moe_router_grouped", 1, None, 1, 1, 1, 256, 2, 128, 1, 1.0, 1, None)
+    with pytest.raises(RuntimeError, match="experts"):
+        _lib.call("lk_moe_router_grouped", 1, None, 1, 1, 1, 2048, 2, 8, 1, 1.0, 1, None)
+    with pytest.raises(RuntimeError, match="top_k"):
+        _lib.call("lk_moe_router_grouped", 1, None, 1, 1, 1, 16, 40, 4, 1, 1.0, 1, None)
+    # no tokens: nothing to launch, no pointers needed
+    assert lib.lk_moe_router_grouped(None, None, None, None, 0, 16, 2, 4, 2,
+                                     ctypes.c_float(1.0), 1, None) == 0
+
+
 def test_expert_major_sizes_and_argument_errors(lib):
     max_tiles, ws = _lib.schedule_sizes(2048, 9, 257)
     # prefill bound for the smaller (16-row) tiles: min(E + 1, n) + n / 16 + 1

@@ -86,6 +86,37 @@ def test_router_grouped_topk_masks_unselected_groups(rng):
         assert set(idx[t].tolist()) <= allowed
 
 
+def test_router_grouped_kat_changes_the_selection():
+    # 4 groups of 2 experts, logits 0 (score 0.5), the bias sets each choice:
+    # choices 0.9 0.5 | 0.8 0.8 | 0.95 0.0 | 0.7 0.75 -> group scores 1.4, 1.6,
+    # 0.95, 1.45: groups 1 and 3 kept; top-2 of (0.8, 0.8, 0.7, 0.75) is
+    # experts 2 and 3 (tie to the lower id), where ungrouped routing takes 4, 0
+    logits = np.zeros((1, 8), dtype=np.float32)
+    bias = np.array([0.4, 0.0, 0.3, 0.3, 0.45, -0.5, 0.2, 0.25], dtype=np.float32)
+    idx, w = M.route(logits, bias, 2, num_expert_group=4, topk_group=2)
+    assert idx[0].tolist() == [2, 3]
+    assert w[0].tolist() == [0.5, 0.5]
+    assert M.route(logits, bias, 2)[0][0].tolist() == [4, 0]
+
+
+def test_router_grouped_masks_to_zero_not_minus_infinity():
+    # the kept group's choices are negative (-0.1, -0.2); the masked group's
+    # experts get choice 0.0 and therefore win (router.py:78, masked_fill 0.0)
+    logits = np.zeros((1, 4), dtype=np.float32)
+    bias = np.array([-0.6, -0.7, -0.8, -0.9], dtype=np.float32)
+    idx, _ = M.route(logits, bias, 2, num_expert_group=2, topk_group=1)
+    assert idx[0].tolist() == [2, 3]
+
+
+@pytest.mark.parametrize("groups", [1, 4, 8])
+def test_router_grouped_with_every_group_kept_is_ungrouped(rng, groups):
+    logits = rng.normal(0, 1, (16, 64)).astype(np.float32)
+    bias = rng.normal(0, 0.1, 64).astype(np.float32)
+    a = M.route(logits, bias, 6, num_expert_group=groups, topk_group=groups)
+    b = M.route(logits, bias, 6)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
 def test_shape_stable_indices_kat():
     kat = KATS["shape_stable_indices"]
     got = M.shape_stable_expert_indices(np.asarray(kat["expert_indices"]), kat["shared_expert_id"])
