@@ -71,7 +71,18 @@ struct Schedule {
   int32_t* tiles;       // [max_tiles, 4] (expert or -1, first row, rows, 0)
   int32_t* tile_count;  // [1]
   int tile_rows;        // rows per tile (16 or 64)
+  // 64-row lists only, when non-null: the same tiles with each bucket's last
+  // tile of at most 16 rows merged into the 64-row tile before it (tiles of
+  // up to 80 rows), so that every entry is work for the direct-load GEMMs
+  int32_t* mtiles;       // [max_tiles, 4]
+  int32_t* mtile_count;  // [1]
 };
+
+// Tiles of a bucket of `cnt` entries in the merged 64-row list.
+__host__ __device__ inline int merged_tiles(int cnt) {
+  const int q = cnt / 64, r = cnt % 64;
+  return cnt == 0 ? 0 : (q == 0 || r > 16) ? q + 1 : q;
+}
 
 __device__ inline int wave_inclusive_scan(int v) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -105,8 +116,8 @@ __device__ inline int wave_exclusive_scan(int* vals, int count) {
 // Places the entries of one chunk: tot[b] = entries of bucket b overall,
 // before[b] = entries of bucket b in earlier chunks. Block 0 also writes the
 // bucket offsets and the tile list (it reuses `before`, all zero there).
-__device__ void place_chunk(int64_t n, int nb, int* tot, int* before, int* start, bool valid,
-                            int64_t entry, int b, int rank, const Schedule& sc) {
+__device__ void place_chunk(int64_t n, int nb, int* tot, int* before, int* start, int* mbefore,
+                            bool valid, int64_t entry, int b, int rank, const Schedule& sc) {
   for (int i = threadIdx.x; i < nb; i += blockDim.x) start[i] = tot[i];
   __syncthreads();
   if (threadIdx.x < kWave) wave_exclusive_scan(start, nb);
@@ -130,6 +141,21 @@ __device__ void place_chunk(int64_t n, int nb, int* tot, int* before, int* start
       *out = make_int4(expert, start[bb] + row, min(tr, cnt - row), 0);
   }
   if (threadIdx.x == 0) *sc.tile_count = total_tiles;
+  if (sc.mtiles == nullptr) return;  // uniform over the block
+  for (int i = threadIdx.x; i < nb; i += blockDim.x) mbefore[i] = merged_tiles(tot[i]);
+  __syncthreads();
+  int merged_total = 0;
+  if (threadIdx.x < kWave) merged_total = wave_exclusive_scan(mbefore, nb);
+  __syncthreads();
+  for (int bb = threadIdx.x; bb < nb; bb += blockDim.x) {
+    const int cnt = tot[bb];
+    const int mt = merged_tiles(cnt);
+    const int expert = bb < nb - 1 ? bb : -1;
+    int4* out = reinterpret_cast<int4*>(sc.mtiles) + mbefore[bb];
+    for (int j = 0; j < mt; ++j)
+      out[j] = make_int4(expert, start[bb] + 64 * j, j + 1 < mt ? 64 : cnt - 64 * j, 0);
+  }
+  if (threadIdx.x == 0) *sc.mtile_count = merged_total;
 }
 
 // One chunk of kSchedThreads entries per block: per-wave bitmaps of the
@@ -140,7 +166,7 @@ __global__ void __launch_bounds__(kSchedThreads)
 schedule_count_kernel(const RouteTable rt, int64_t n, Schedule sc) {
   __shared__ uint32_t bits[kSchedWaves * kMaxBuckets * 2];
   __shared__ int pre[kSchedWaves * kMaxBuckets];
-  __shared__ int tot[kMaxBuckets], before[kMaxBuckets], start[kMaxBuckets];
+  __shared__ int tot[kMaxBuckets], before[kMaxBuckets], start[kMaxBuckets], mbefore[kMaxBuckets];
   const int nb = static_cast<int>(rt.experts) + 1;
   for (int i = threadIdx.x; i < kSchedWaves * nb * 2; i += kSchedThreads) bits[i] = 0u;
   __syncthreads();
@@ -171,7 +197,7 @@ schedule_count_kernel(const RouteTable rt, int64_t n, Schedule sc) {
     rank = pre[w * nb + b] + below;
   }
   if (gridDim.x == 1) {
-    place_chunk(n, nb, tot, before, start, valid, entry, b, rank, sc);
+    place_chunk(n, nb, tot, before, start, mbefore, valid, entry, b, rank, sc);
   } else if (valid) {
     sc.rank[entry] = rank;
   }
@@ -179,7 +205,7 @@ schedule_count_kernel(const RouteTable rt, int64_t n, Schedule sc) {
 
 __global__ void __launch_bounds__(kSchedThreads)
 schedule_place_kernel(const RouteTable rt, int64_t n, int chunks, Schedule sc) {
-  __shared__ int tot[kMaxBuckets], before[kMaxBuckets], start[kMaxBuckets];
+  __shared__ int tot[kMaxBuckets], before[kMaxBuckets], start[kMaxBuckets], mbefore[kMaxBuckets];
   const int nb = static_cast<int>(rt.experts) + 1;
   const int c = blockIdx.x;
   for (int bb = threadIdx.x; bb < nb; bb += kSchedThreads) {
@@ -205,7 +231,7 @@ schedule_place_kernel(const RouteTable rt, int64_t n, int chunks, Schedule sc) {
   const bool valid = entry < n;
   const int b = valid ? rt.bucket(entry) : 0;
   const int rank = valid ? sc.rank[entry] : 0;
-  place_chunk(n, nb, tot, before, start, valid, entry, b, rank, sc);
+  place_chunk(n, nb, tot, before, start, mbefore, valid, entry, b, rank, sc);
 }
 
 // Schedule of up to kFuseThreads token-routes over at most 257 bank entries
@@ -234,7 +260,8 @@ schedule_one_kernel(const RouteTable rt, int64_t n, Schedule sc, const float* __
   __shared__ int32_t sel[ROUTE ? kFuseThreads : 1];  // [tokens][top_k] selections
   __shared__ uint32_t bits[kFuseWaves * kFuseBuckets * 2];
   __shared__ int pre[kFuseWaves * kFuseBuckets];
-  __shared__ int tot[kFuseBuckets], before[kFuseBuckets], start[kFuseBuckets];
+  __shared__ int tot[kFuseBuckets], before[kFuseBuckets], start[kFuseBuckets],
+      mbefore[kFuseBuckets];
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
   const int nb = static_cast<int>(rt.experts) + 1;  // bank entries and the invalid bucket
@@ -280,7 +307,7 @@ schedule_one_kernel(const RouteTable rt, int64_t n, Schedule sc, const float* __
                                 : __popc(lo) + __popc(hi & ((1u << (lane - 32)) - 1u));
     rank = pre[w * nb + b] + below;
   }
-  place_chunk(n, nb, tot, before, start, valid, entry, b, rank, sc);
+  place_chunk(n, nb, tot, before, start, mbefore, valid, entry, b, rank, sc);
 }
 
 // ---------------------------------------------------------------------------
@@ -310,6 +337,10 @@ struct GemmArgs {
   const int32_t* perm;       // sorted position -> entry (gather / scatter modes)
   const int32_t* tiles;      // [*, 4] tile list (schedule modes)
   const int32_t* tile_count;
+  // the merged 64-row list of the same schedule (tails of <= 16 rows joined
+  // to the tile before them): what the direct-load launches walk
+  const int32_t* mtiles;
+  const int32_t* mtile_count;
   const uint8_t* wp[3];      // packed weights per output matrix (two-matrix: gate, up)
   const void* ws[3];         // scales: bf16 (W4A16) or E8M0 bytes (MXFP4)
   uint16_t* out[3];
@@ -1524,21 +1555,14 @@ w4a16_stream_kernel(const GemmArgs g) {
   constexpr bool kDirect = MT > 1 && WIDE && (FMT == kFmtW4A16 || FMT == kFmtMxBf16) &&
                            GATHER != SCATTER && !DENSE;
   if constexpr (kDirect) {
-    // an expert's last tile of <= 16 rows rides with the 64-row tile before
-    // it: that tile's block makes one pass over the expert's weights for up
-    // to 80 rows, and this tile's block has nothing left to do
-    const int4* const td = reinterpret_cast<const int4*>(g.tiles);
-    if (rows <= 16 && tile > 0) {
-      const int4 pv = td[tile - 1];
-      if (pv.x == expert && pv.z == 64 && pv.y + 64 == row0) return;
-    }
-    if (rows == 64 && tile + 1 < *g.tile_count) {
-      const int4 nx = td[tile + 1];
-      if (nx.x == expert && nx.z <= 16 && nx.y == row0 + 64) {
-        stream_tile<FMT, MATS, NT, 5, WIDE, GATHER, SCATTER, DENSE, true>(g, expert, row0,
-                                                                          64 + nx.z, cb, osel);
-        return;
-      }
+    // the merged list: an expert's last tile of <= 16 rows is already part of
+    // the 64-row tile before it, one pass over the expert's weights for up to
+    // 80 rows (and every entry of the list is a tile with rows to compute, so
+    // consecutive entries, which go to consecutive XCDs, carry equal work)
+    if (rows > 64) {
+      stream_tile<FMT, MATS, NT, 5, WIDE, GATHER, SCATTER, DENSE, true>(g, expert, row0, rows, cb,
+                                                                        osel);
+      return;
     }
   }
   // a tile of at most 16 rows (an expert's last rows) takes the 16-row path:
@@ -2133,7 +2157,7 @@ size_t split_bytes(int64_t elems) {
 
 struct MoeLayout {
   SchedLayout sched;
-  size_t offsets, perm, tiles, count, act, eo, x_split, act_split;
+  size_t offsets, perm, tiles, count, mtiles, act, eo, x_split, act_split;
   size_t x_pair, x_neg, act_neg;  // paired W4A16 input and group sums (direct loads)
   size_t total;
 };
@@ -2164,8 +2188,12 @@ MoeLayout moe_layout(int64_t entries, int64_t experts, int64_t act_cols, int64_t
   at += align_up(static_cast<size_t>(entries) * 4);
   l.tiles = at;
   at += align_up(static_cast<size_t>(l.sched.max_tiles) * 16);
-  l.count = at;
+  l.count = at;  // the tile count, and at +4 bytes the merged 64-row list's
   at += 256;
+  // the merged 64-row tile list (direct-load expert GEMMs); its launches read
+  // descriptors up to the bound rounded up to 8 tiles before checking the count
+  l.mtiles = at;
+  at += align_up(static_cast<size_t>((max_tiles_for(entries, experts, kTileRows) + 7) / 8 * 8) * 16);
   l.act = at;
   at += align_up(static_cast<size_t>(entries) * act_cols * 2);
   l.eo = at;
@@ -2203,13 +2231,16 @@ bool route_schedule_fits(int64_t tokens, int64_t routed, int64_t top_k) {
 int route_schedule_launch(const float* logits, const float* bias, int64_t* idx, float* weights,
                           int64_t tokens, int64_t routed, int64_t top_k, float scaling,
                           int renormalize, int32_t* offsets, int32_t* perm, int32_t* tiles,
-                          int32_t* tile_count, int tile_rows, hipStream_t s) {
+                          int32_t* tile_count, int tile_rows, int32_t* mtiles,
+                          int32_t* mtile_count, hipStream_t s) {
   Schedule sc{};
   sc.offsets = offsets;
   sc.perm = perm;
   sc.tiles = tiles;
   sc.tile_count = tile_count;
   sc.tile_rows = tile_rows;
+  sc.mtiles = tile_rows == kTileRows ? mtiles : nullptr;
+  sc.mtile_count = mtile_count;
   const RouteTable rt{idx, top_k, top_k + 1, routed + 1, routed};
   schedule_one_kernel<true><<<1, kFuseThreads, 0, s>>>(rt, tokens * (top_k + 1), sc, logits, bias,
                                                        idx, weights, static_cast<int>(top_k),
@@ -2219,8 +2250,9 @@ int route_schedule_launch(const float* logits, const float* bias, int64_t* idx, 
 
 int schedule_launch(const RouteTable& rt, int64_t entries, char* ws, const SchedLayout& sl,
                     int32_t* offsets, int32_t* perm, int32_t* tiles, int32_t* tile_count,
-                    int tile_rows, hipStream_t s) {
-  Schedule sc;
+                    int tile_rows, hipStream_t s, int32_t* mtiles = nullptr,
+                    int32_t* mtile_count = nullptr) {
+  Schedule sc{};
   sc.rank = reinterpret_cast<int32_t*>(ws + sl.rank);
   sc.hist = reinterpret_cast<int32_t*>(ws + sl.hist);
   sc.offsets = offsets;
@@ -2228,6 +2260,8 @@ int schedule_launch(const RouteTable& rt, int64_t entries, char* ws, const Sched
   sc.tiles = tiles;
   sc.tile_count = tile_count;
   sc.tile_rows = tile_rows;
+  sc.mtiles = tile_rows == kTileRows ? mtiles : nullptr;
+  sc.mtile_count = mtile_count;
   // one block of 16 waves where one chunk of kSchedThreads would not cover
   // the table (otherwise the chunk kernel, at 8 waves, is the faster one launch)
   if (entries > kSchedThreads && entries <= kFuseThreads && rt.experts + 1 <= kFuseBuckets &&
@@ -2459,6 +2493,9 @@ int stream_launch(GemmArgs g, Mode mode, int64_t tiles, int mt, hipStream_t s, c
     LK_REQUIRE(FMT != kFmtW4A16 || (g.a_pair && g.a_neg), "%s: paired activations missing", what);
     LK_REQUIRE(g.n % 8 == 0 && (!g.out_neg || (MATS == 2 && g.n % 128 == 0)),
                "%s: output width %lld unsupported for direct loads", what, (long long)g.n);
+    LK_REQUIRE(g.mtiles && g.mtile_count, "%s: merged tile list missing", what);
+    g.tiles = g.mtiles;
+    g.tile_count = g.mtile_count;
   }
   g.col_blocks = static_cast<int>((g.n + kStWaves * NT * 16 - 1) / (kStWaves * NT * 16));
   const int64_t blocks = (tiles + 7) / 8 * 8 * g.col_blocks * g.outputs;
@@ -2903,6 +2940,8 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   auto* perm = reinterpret_cast<int32_t*>(ws + l.perm);
   auto* tiles = reinterpret_cast<int32_t*>(ws + l.tiles);
   auto* count = reinterpret_cast<int32_t*>(ws + l.count);
+  auto* mtiles = reinterpret_cast<int32_t*>(ws + l.mtiles);
+  int32_t* const mcount = count + 1;
   auto* act = reinterpret_cast<uint16_t*>(ws + l.act);
   auto* eo = reinterpret_cast<uint16_t*>(ws + l.eo);
   const int64_t group = mx ? 32 : group_size;
@@ -2916,14 +2955,15 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   if (route_schedule_fits(tokens, experts - 1, top_k)) {
     if (int rc = route_schedule_launch(logits, bias, expert_indices, weights, tokens, experts - 1,
                                        top_k, routed_scaling_factor, renormalize, offsets, perm,
-                                       tiles, count, tr, s))
+                                       tiles, count, tr, mtiles, mcount, s))
       return rc;
   } else {
     if (int rc = lk_moe_router(logits, bias, expert_indices, weights, tokens, experts - 1, top_k,
                                routed_scaling_factor, renormalize, stream))
       return rc;
     const RouteTable rt{expert_indices, top_k, routes, experts, experts - 1};
-    if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, tr, s))
+    if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, tr, s,
+                                 mtiles, mcount))
       return rc;
   }
 
@@ -2940,6 +2980,8 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.perm = perm;
   g.tiles = tiles;
   g.tile_count = count;
+  g.mtiles = mtiles;
+  g.mtile_count = mcount;
   g.group = group;
   g.routes = routes;
   g.outputs = 1;
