@@ -256,6 +256,26 @@ LK_API int lk_w4a16_fused_qkv(const uint16_t* x, const uint8_t* q_packed,
                               uint16_t* v, int64_t m, int64_t n, int64_t k, int64_t group_size,
                               void* stream);
 
+/* ---- the two GEMMs above with a caller-owned workspace (same outputs):
+ *      engine/kernels/__init__.py:82-125 (w4a16_dense), w4a16_fused_qkv.py:342-389
+ * From 16 rows at G = 128 (k % 128 == 0) a pre-pass writes x paired in the
+ * weight decode's k order with its 128-wide group sums into the workspace and
+ * the 64-row GEMM loads its rows from there straight into LDS. The workspace
+ * holds lk_w4a16_dense_gemm_workspace(m, k, group) bytes (0 where that form
+ * does not apply; -1 on bad input); a smaller one is refused before any launch. */
+LK_API int64_t lk_w4a16_dense_gemm_workspace(int64_t m, int64_t k, int64_t group_size);
+LK_API int lk_w4a16_dense_gemm_ws(const uint16_t* x, const uint8_t* packed,
+                                  const uint16_t* scales, uint16_t* y, int64_t m, int64_t n,
+                                  int64_t k, int64_t group_size, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
+LK_API int lk_w4a16_fused_qkv_ws(const uint16_t* x, const uint8_t* q_packed,
+                                 const uint16_t* q_scales, const uint8_t* k_packed,
+                                 const uint16_t* k_scales, const uint8_t* v_packed,
+                                 const uint16_t* v_scales, uint16_t* q, uint16_t* k_out,
+                                 uint16_t* v, int64_t m, int64_t n, int64_t k,
+                                 int64_t group_size, void* workspace, int64_t workspace_bytes,
+                                 void* stream);
+
 /* ---- the grouped W4A16 MoE block with its router, expert-major (batched
  *      decode and prefill): engine/klinear/moe.py:278-334 +
  *      engine/klinear/router.py:47-85, evaluated per expert as in

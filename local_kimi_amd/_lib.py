@@ -48,6 +48,9 @@ SIGNATURES: dict[str, list] = {
                              _P, _I64, _P],
     "lk_w4a16_dense_gemm": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "lk_w4a16_fused_qkv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "lk_w4a16_dense_gemm_ws": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
+    "lk_w4a16_fused_qkv_ws": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                              _P, _I64, _P],
     "lk_w4a16_moe_forward": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                              _I64, _I64, _I64, _I64, _I64, _F, _I, _I64, _P],
     "lk_w4a16_moe_forward_static": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
@@ -78,6 +81,7 @@ SIGNATURES: dict[str, list] = {
 QUERIES: dict[str, list] = {
     "lk_w4a16_moe_decode_workspace": [_I64, _I64, _I64, _I64, _I64],
     "lk_w4a16_moe_forward_static_capacity": [],
+    "lk_w4a16_dense_gemm_workspace": [_I64, _I64, _I64],
     "lk_w4a16_grouped_gemm_workspace": [_I64, _I64, _I64],
     "lk_w4a16_moe_forward_workspace": [_I64, _I64, _I64, _I64, _I64],
     "lk_mxfp4_moe_forward_workspace": [_I64, _I64, _I64, _I64, _I64],

@@ -922,8 +922,9 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
   constexpr int kPassUnits = MT == 1 ? 1 : (kRows * kPS * 16 + kThreads - 1) / kThreads;
   constexpr bool kDirect = DIRECT;
   static_assert(!kDirect || (WIDE && (FMT == kFmtW4A16 || FMT == kFmtMxBf16) &&
-                             GATHER != SCATTER && !DENSE),
-                "direct loads: 128-wide k-steps of an expert-major gather or scatter");
+                             (DENSE ? !GATHER && !SCATTER : GATHER != SCATTER)),
+                "direct loads: 128-wide k-steps of a dense product or an expert-major gather "
+                "or scatter");
   static_assert(MT == 1 || MT == 4 || (MT == 5 && kDirect), "tile heights 16, 64, direct 80");
   extern __shared__ uint4 smem[];
   __shared__ int64_t row_index[kRows];  // activation row of each tile row
@@ -1507,7 +1508,8 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
 // double buffered, the next pass loaded while the current one computes, one
 // barrier per pass); every wave streams its own columns over all of k with
 // kStDepth k-steps of weights in flight and stores its outputs itself.
-template <int FMT, int MATS, int NT, int MT, bool WIDE, bool GATHER, bool SCATTER, bool DENSE>
+template <int FMT, int MATS, int NT, int MT, bool WIDE, bool GATHER, bool SCATTER, bool DENSE,
+          bool DDIRECT = false>
 __global__ void __launch_bounds__(kStWaves * kWave, 2)
 w4a16_stream_kernel(const GemmArgs g) {
   constexpr int kThreads = kStWaves * kWave;
@@ -1552,8 +1554,10 @@ w4a16_stream_kernel(const GemmArgs g) {
   }
   // 64-row gather / scatter launches with 128-wide k-steps take their
   // activations by direct loads, in every tile path below
+  // (DDIRECT: a dense product whose rows are loaded directly, W4A16 from the
+  // paired copy)
   constexpr bool kDirect = MT > 1 && WIDE && (FMT == kFmtW4A16 || FMT == kFmtMxBf16) &&
-                           GATHER != SCATTER && !DENSE;
+                           (DENSE ? DDIRECT : GATHER != SCATTER);
   if constexpr (kDirect) {
     // the merged list: an expert's last tile of <= 16 rows is already part of
     // the 64-row tile before it, one pass over the expert's weights for up to
@@ -2351,10 +2355,11 @@ int gemm_launch(GemmArgs g, Mode mode, int64_t tiles, bool wide_cols, hipStream_
   return check_launch(what);
 }
 
-template <int FMT, int MATS, int MT, bool WIDE, bool GATHER, bool SCATTER, bool DENSE>
+template <int FMT, int MATS, int MT, bool WIDE, bool GATHER, bool SCATTER, bool DENSE,
+          bool DDIRECT = false>
 void stream_one(const GemmArgs& g, unsigned blocks, size_t lds, hipStream_t s) {
   constexpr int NT = MATS == 2 ? 1 : 2;
-  auto* fn = &w4a16_stream_kernel<FMT, MATS, NT, MT, WIDE, GATHER, SCATTER, DENSE>;
+  auto* fn = &w4a16_stream_kernel<FMT, MATS, NT, MT, WIDE, GATHER, SCATTER, DENSE, DDIRECT>;
   static bool limit_set = false;  // the attribute is per function; set once per process
   if (!limit_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -2368,7 +2373,8 @@ void stream_one(const GemmArgs& g, unsigned blocks, size_t lds, hipStream_t s) {
 bool persist_disabled() { return path_choice(kKnobMoePersist) == 1; }
 
 template <int FMT, int MATS, int MT, bool WIDE>
-void stream_dispatch(const GemmArgs& g, Mode mode, unsigned blocks, size_t lds, hipStream_t s) {
+void stream_dispatch(const GemmArgs& g, Mode mode, unsigned blocks, size_t lds, hipStream_t s,
+                     bool dense_direct = false) {
   if constexpr (FMT == kFmtMxF16) {
     stream_one<FMT, MATS, MT, false, false, false, true>(g, blocks, lds, s);
   } else {
@@ -2378,7 +2384,15 @@ void stream_dispatch(const GemmArgs& g, Mode mode, unsigned blocks, size_t lds, 
       case Mode::GatherScatter:
         stream_one<FMT, MATS, MT, WIDE, true, true, false>(g, blocks, lds, s);
         break;
-      case Mode::Dense: stream_one<FMT, MATS, MT, WIDE, false, false, true>(g, blocks, lds, s); break;
+      case Mode::Dense:
+        if constexpr (MT > 1 && WIDE && (FMT == kFmtW4A16 || FMT == kFmtMxBf16)) {
+          if (dense_direct) {
+            stream_one<FMT, MATS, MT, WIDE, false, false, true, true>(g, blocks, lds, s);
+            break;
+          }
+        }
+        stream_one<FMT, MATS, MT, WIDE, false, false, true>(g, blocks, lds, s);
+        break;
     }
   }
 }
@@ -2497,6 +2511,13 @@ int stream_launch(GemmArgs g, Mode mode, int64_t tiles, int mt, hipStream_t s, c
     g.tiles = g.mtiles;
     g.tile_count = g.mtile_count;
   }
+  // dense 64-row launches load their rows directly as well when they can:
+  // MXFP4 from the rows themselves, W4A16 from a paired copy with its group
+  // sums (a_pair / a_neg, made by the caller's pre-pass)
+  const bool dense_direct = mt > 1 && wide && mode == Mode::Dense && g.n % 8 == 0 &&
+                            g.a_rows > 0 &&
+                            g.a_rows * g.k * 2 <= static_cast<int64_t>(kMaxDirectBytes) &&
+                            (FMT == kFmtMxBf16 || (FMT == kFmtW4A16 && g.a_pair && g.a_neg));
   g.col_blocks = static_cast<int>((g.n + kStWaves * NT * 16 - 1) / (kStWaves * NT * 16));
   const int64_t blocks = (tiles + 7) / 8 * 8 * g.col_blocks * g.outputs;
   LK_REQUIRE(blocks > 0 && blocks < (1LL << 31), "%s: too many blocks", what);
@@ -2513,7 +2534,7 @@ int stream_launch(GemmArgs g, Mode mode, int64_t tiles, int mt, hipStream_t s, c
     if (wide) stream_dispatch<FMT, MATS, 1, kWideOk>(g, mode, nb, lds, s);
     else stream_dispatch<FMT, MATS, 1, false>(g, mode, nb, lds, s);
   } else {
-    if (wide) stream_dispatch<FMT, MATS, 4, kWideOk>(g, mode, nb, lds, s);
+    if (wide) stream_dispatch<FMT, MATS, 4, kWideOk>(g, mode, nb, lds, s, dense_direct);
     else stream_dispatch<FMT, MATS, 4, false>(g, mode, nb, lds, s);
   }
   return check_launch(what);
@@ -2608,6 +2629,34 @@ void dense_args(GemmArgs& g, const uint16_t* x, int64_t m, int64_t n, int64_t k,
   g.dense_rows = static_cast<int>(m);
   g.outputs = 1;
   g.act = kActSwiglu;
+}
+
+// Workspace of a dense W4A16 product whose 64-row launches load their rows
+// directly: the rows paired in the weight decode's k order and their group
+// sums (G = 128, k % 128 == 0, from 16 rows); 0 where that form does not apply.
+int64_t dense_pair_bytes(int64_t m, int64_t k, int64_t group) {
+  if (m < 16 || group != 128 || k % 128 != 0) return 0;
+  return static_cast<int64_t>(align_up(static_cast<size_t>(m * k * 2)) +
+                              align_up(static_cast<size_t>(m * (k / 128) * 4)));
+}
+
+// The pre-pass of the direct form: pairs x into the workspace and points the
+// launch at it.
+int dense_pairs(GemmArgs& g, const uint16_t* x, int64_t m, int64_t k, int64_t group,
+                void* workspace, int64_t workspace_bytes, hipStream_t s, const char* what) {
+  const int64_t need = dense_pair_bytes(m, k, group);
+  if (need == 0) return LK_OK;
+  LK_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+             "%s: workspace too small: %lld < %lld bytes", what, (long long)workspace_bytes,
+             (long long)need);
+  auto* xp = static_cast<uint16_t*>(workspace);
+  auto* neg = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                       align_up(static_cast<size_t>(m * k * 2)));
+  if (int rc = pair_rows_launch(x, xp, neg, m, k, s)) return rc;
+  g.a_pair = xp;
+  g.a_neg = neg;
+  g.a_rows = m;
+  return LK_OK;
 }
 
 }  // namespace
@@ -2790,6 +2839,7 @@ int lk_mxfp4_gemm(const uint16_t* x, const uint8_t* packed, const uint8_t* scale
   LK_REQUIRE(m < (1LL << 30), "too many rows");
   GemmArgs g{};
   dense_args(g, x, m, n, k, 32);
+  g.a_rows = m;  // bf16 rows load directly (the fp16 form stages them)
   g.wp[0] = g.wp[1] = g.wp[2] = packed;
   g.ws[0] = g.ws[1] = g.ws[2] = scale;
   g.out[0] = g.out[1] = g.out[2] = y;
@@ -2873,6 +2923,72 @@ int lk_w4a16_fused_qkv(const uint16_t* x, const uint8_t* q_packed, const uint16_
   g.outputs = 3;
   const int64_t tiles = (m + kTileRows - 1) / kTileRows;
   return dense_launch<kFmtW4A16>(g, tiles, as_stream(stream), "lk_w4a16_fused_qkv");
+}
+
+int64_t lk_w4a16_dense_gemm_workspace(int64_t m, int64_t k, int64_t group_size) {
+  if (m < 0 || k <= 0 || group_size <= 0) return -1;
+  return dense_pair_bytes(m, k, group_size);
+}
+
+int lk_w4a16_dense_gemm_ws(const uint16_t* x, const uint8_t* packed, const uint16_t* scales,
+                           uint16_t* y, int64_t m, int64_t n, int64_t k, int64_t group_size,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+  LK_REQUIRE(packed && scales && y, "null pointer argument");
+  LK_REQUIRE(m >= 0 && n > 0, "invalid dense dimensions m=%lld n=%lld", (long long)m,
+             (long long)n);
+  if (int rc = check_pow2_group(k, group_size)) return rc;
+  if (m == 0) return LK_OK;
+  LK_REQUIRE(x != nullptr, "null activation pointer");
+  LK_REQUIRE(m < (1LL << 30), "too many rows");
+  GemmArgs g{};
+  dense_args(g, x, m, n, k, group_size);
+  g.wp[0] = g.wp[1] = g.wp[2] = packed;
+  g.ws[0] = g.ws[1] = g.ws[2] = scales;
+  g.out[0] = g.out[1] = g.out[2] = y;
+  hipStream_t s = as_stream(stream);
+  if (int rc = dense_pairs(g, x, m, k, group_size, workspace, workspace_bytes, s,
+                           "lk_w4a16_dense_gemm_ws"))
+    return rc;
+  const int64_t tiles = (m + kTileRows - 1) / kTileRows;
+  return dense_launch<kFmtW4A16>(g, tiles, s, "lk_w4a16_dense_gemm_ws");
+}
+
+int lk_w4a16_fused_qkv_ws(const uint16_t* x, const uint8_t* q_packed, const uint16_t* q_scales,
+                          const uint8_t* k_packed, const uint16_t* k_scales,
+                          const uint8_t* v_packed, const uint16_t* v_scales, uint16_t* q,
+                          uint16_t* k_out, uint16_t* v, int64_t m, int64_t n, int64_t k,
+                          int64_t group_size, void* workspace, int64_t workspace_bytes,
+                          void* stream) {
+  LK_REQUIRE(q_packed && q_scales && k_packed && k_scales && v_packed && v_scales && q && k_out &&
+                 v,
+             "null pointer argument");
+  LK_REQUIRE(m >= 0 && n > 0, "invalid QKV dimensions m=%lld n=%lld", (long long)m,
+             (long long)n);
+  if (int rc = check_pow2_group(k, group_size)) return rc;
+  if (m == 0) return LK_OK;
+  LK_REQUIRE(x != nullptr, "null activation pointer");
+  if (m < 16)  // decode rows: the GEMV path needs no workspace
+    return lk_w4a16_fused_qkv(x, q_packed, q_scales, k_packed, k_scales, v_packed, v_scales, q,
+                              k_out, v, m, n, k, group_size, stream);
+  LK_REQUIRE(m < (1LL << 30), "too many rows");
+  GemmArgs g{};
+  dense_args(g, x, m, n, k, group_size);
+  g.wp[0] = q_packed;
+  g.wp[1] = k_packed;
+  g.wp[2] = v_packed;
+  g.ws[0] = q_scales;
+  g.ws[1] = k_scales;
+  g.ws[2] = v_scales;
+  g.out[0] = q;
+  g.out[1] = k_out;
+  g.out[2] = v;
+  g.outputs = 3;
+  hipStream_t s = as_stream(stream);
+  if (int rc = dense_pairs(g, x, m, k, group_size, workspace, workspace_bytes, s,
+                           "lk_w4a16_fused_qkv_ws"))
+    return rc;
+  const int64_t tiles = (m + kTileRows - 1) / kTileRows;
+  return dense_launch<kFmtW4A16>(g, tiles, s, "lk_w4a16_fused_qkv_ws");
 }
 
 int64_t lk_w4a16_moe_forward_workspace(int64_t tokens, int64_t experts, int64_t h, int64_t i,

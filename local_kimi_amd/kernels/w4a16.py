@@ -105,6 +105,22 @@ def _dense(entry: str, activations, packed_weights, scales):
     return out
 
 
+def _dense_gemm(activations, packed_weights, scales):
+    """The MFMA GEMM with its direct-load workspace (the paired rows and their
+    group sums, G = 128) from the torch caching allocator."""
+    m, n, k, g = _validate_dense(activations, packed_weights, scales)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=activations.device)
+    if m == 0:
+        return out
+    ws = workspace(_lib.query("lk_w4a16_dense_gemm_workspace", m, k, g), activations.device)
+    x, p, s = _c(activations), _c(packed_weights), _c(scales)
+    with torch.cuda.device(activations.device):
+        _lib.call("lk_w4a16_dense_gemm_ws", x.data_ptr(), p.data_ptr(), s.data_ptr(),
+                  out.data_ptr(), m, n, k, g, ws.data_ptr(), ws.numel(),
+                  _stream(activations.device))
+    return out
+
+
 def w4a16_dense(activations: torch.Tensor, packed_weights: torch.Tensor,
                 scales: torch.Tensor) -> torch.Tensor:
     """``y[M, N] = x @ dequant(W).T`` (registered as ``hip``).
@@ -113,14 +129,14 @@ def w4a16_dense(activations: torch.Tensor, packed_weights: torch.Tensor,
     MFMA GEMM (weights read once per 64-row tile).
     """
     if activations.ndim == 2 and activations.shape[0] >= DENSE_GEMM_MIN_ROWS:
-        return _dense("lk_w4a16_dense_gemm", activations, packed_weights, scales)
+        return _dense_gemm(activations, packed_weights, scales)
     return _dense("lk_w4a16_dense", activations, packed_weights, scales)
 
 
 def w4a16_dense_gemm(activations: torch.Tensor, packed_weights: torch.Tensor,
                      scales: torch.Tensor) -> torch.Tensor:
     """The MFMA GEMM form of :func:`w4a16_dense` at any row count."""
-    return _dense("lk_w4a16_dense_gemm", activations, packed_weights, scales)
+    return _dense_gemm(activations, packed_weights, scales)
 
 
 def w4a16_dense_reference(activations: torch.Tensor, packed_weights: torch.Tensor,
@@ -408,9 +424,11 @@ def fused_qkv_w4a16(activations, q_packed, q_scales, k_packed, k_scales, v_packe
         return tuple(outs)
     x = _c(activations)
     w = [_c(t) for t in (q_packed, q_scales, k_packed, k_scales, v_packed, v_scales)]
+    ws = workspace(_lib.query("lk_w4a16_dense_gemm_workspace", m, k, g), dev)
     with torch.cuda.device(dev):
-        _lib.call("lk_w4a16_fused_qkv", x.data_ptr(), *(t.data_ptr() for t in w),
-                  *(o.data_ptr() for o in outs), m, n, k, g, _stream(dev))
+        _lib.call("lk_w4a16_fused_qkv_ws", x.data_ptr(), *(t.data_ptr() for t in w),
+                  *(o.data_ptr() for o in outs), m, n, k, g, ws.data_ptr(), ws.numel(),
+                  _stream(dev))
     return tuple(outs)
 
 

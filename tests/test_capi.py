@@ -56,6 +56,19 @@ def test_argument_errors_are_reported_without_touching_the_gpu(lib):
         _lib.call("lk_moe_router", 1, None, 1, 1, 1, 4, 9, 1.0, 1, None)
 
 
+def test_dense_workspace_sizes_and_refusals(lib):
+    # paired rows (2 bytes per value) + group sums (4 bytes per 128 values), 256-byte aligned
+    assert lib.lk_w4a16_dense_gemm_workspace(2048, 2304, 128) == 2048 * 2304 * 2 + 2048 * 18 * 4
+    assert lib.lk_w4a16_dense_gemm_workspace(8, 2304, 128) == 0     # decode rows: the GEMV
+    assert lib.lk_w4a16_dense_gemm_workspace(2048, 2304, 64) == 0   # other groups: staged rows
+    assert lib.lk_w4a16_dense_gemm_workspace(-1, 2304, 128) == -1
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        _lib.call("lk_w4a16_dense_gemm_ws", 1, 1, 1, 1, 64, 256, 512, 128, 1, 16, None)
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        _lib.call("lk_w4a16_fused_qkv_ws", 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 64, 256, 512, 128,
+                  None, 0, None)
+
+
 def test_grouped_router_argument_errors(lib):
     # (logits, bias, idx, w, tokens, experts, top_k, groups, topk_group, scale, renorm, stream)
     with pytest.raises(RuntimeError, match="divisible"):

@@ -141,6 +141,38 @@ def test_fused_qkv_matches_oracle(rng, monkeypatch, m, form):
         assert_close_bf16(to_bits(a), e, what=f"fused qkv {name} m={m}")
 
 
+@pytest.mark.parametrize("m,n,k", [(16, 256, 512), (100, 384, 1024), (130, 256, 2304),
+                                   (2048, 512, 2304)])
+def test_direct_load_dense_forms_match_the_staged_forms(rng, m, n, k):
+    """The workspace entry points (rows paired by a pre-pass, loaded straight
+    into LDS) against the entry points without a workspace (rows staged through
+    registers): the same products in the same order, so bit-identical."""
+    import torch
+
+    from local_kimi_amd import _lib
+    from local_kimi_amd.kernels import fused_qkv_w4a16, w4a16_dense_gemm
+
+    g = 128
+    mats = [OW.quantise(random_bf16_bits(rng, (n, k), 0.02), g) for _ in range(3)]
+    x = _dev(random_bf16_bits(rng, (m, k)))
+    flat = [_dev(a) for pair in mats for a in pair]
+    got = fused_qkv_w4a16(x, *flat)
+    staged = [torch.empty((m, n), dtype=torch.bfloat16, device=DEV) for _ in range(3)]
+    _lib.call("lk_w4a16_fused_qkv", x.data_ptr(), *(t.data_ptr() for t in flat),
+              *(o.data_ptr() for o in staged), m, n, k, g, torch.cuda.current_stream().cuda_stream)
+    for name, a, b in zip("qkv", got, staged):
+        assert torch.equal(a, b), f"fused qkv {name} m={m} n={n} k={k}"
+    y = w4a16_dense_gemm(x, flat[0], flat[1])
+    ys = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    _lib.call("lk_w4a16_dense_gemm", x.data_ptr(), flat[0].data_ptr(), flat[1].data_ptr(),
+              ys.data_ptr(), m, n, k, g, torch.cuda.current_stream().cuda_stream)
+    assert torch.equal(y, ys)
+    sel = np.unique(rng.choice(m, size=min(m, 8), replace=False))
+    xh = to_bits(x)[sel]
+    assert_close_bf16(to_bits(y)[sel], OW.dense(xh, mats[0][0], mats[0][1], g),
+                      what=f"direct dense m={m}")
+
+
 # ---------------------------------------------------------------------------
 # grouped GEMMs
 
