@@ -241,15 +241,15 @@ schedule_place_kernel(const RouteTable rt, int64_t n, int chunks, Schedule sc) {
 // block first routes the batch (engine/klinear/router.py:47-85), one token
 // per wave, writing the selections and weights to the caller's tables and the
 // selections to LDS, and schedules from LDS: one launch instead of the
-// router's and the schedule's. The routing then runs on one CU, where each
-// token's selection rounds are a dependent chain: 4 tokens take 7.3 us here
-// against 9.7 us for the two launches; at 8 tokens the whole step is the same
-// either way (52.3 against 52.7 us) and at 16 the two launches win (70.8
-// against 72.0 us), so ROUTE serves batches of at most kFuseRouteTokens;
-// larger ones route on a grid of one block per token.
+// router's and the schedule's. The routing then runs on one CU, one token per
+// wave: 4 tokens take 7.3 us here against 9.7 us for the two launches; with
+// the merged-list selection 12 tokens take 64.0-64.2 against 64.9-65.1 us per
+// step and 16 tokens the same either way (73.1-73.7 against 73.3-73.4 us), so
+// ROUTE serves batches of at most kFuseRouteTokens (one wave each); larger
+// ones route on a grid of one block per token.
 constexpr int kFuseThreads = 1024;
 constexpr int kFuseWaves = kFuseThreads / kWave;
-constexpr int kFuseRouteTokens = 8;
+constexpr int kFuseRouteTokens = 16;
 constexpr int kFuseBuckets = 258;  // 256 routed experts, the shared one, invalid routes
 
 template <bool ROUTE>
@@ -1693,7 +1693,14 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   const int cgs = static_cast<int>((N + NT * 16 - 1) / (NT * 16));
   const int total = *g.tile_count * cgs;
   const int per = (total + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
-  const int ub = static_cast<int>(blockIdx.x) * per;
+  // ranges go to XCDs in contiguous runs (block b runs on XCD b % 8): the
+  // blocks on one XCD take consecutive ranges, so an expert's consecutive
+  // tiles, which read the same weights, meet in that XCD's L2 instead of
+  // each fetching them from HBM
+  const int grid = static_cast<int>(gridDim.x);
+  const int bid = static_cast<int>(blockIdx.x);
+  const int range = grid % 8 == 0 ? (bid % 8) * (grid / 8) + bid / 8 : bid;
+  const int ub = range * per;
   const int ue = min(ub + per, total);
   if (ub >= ue) return;  // block-uniform
   const int t_first = ub / cgs;

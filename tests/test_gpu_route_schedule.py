@@ -76,8 +76,9 @@ def _fused_and_split(monkeypatch, fn, *args):
 @pytest.mark.parametrize("weights", ["w4a16", "mxfp4"])
 @pytest.mark.parametrize("tokens,top_k,bias,ties", [
     (4, 8, False, False),
-    (8, 8, True, True),      # the largest batch routed in the schedule's block
-    (9, 8, False, False),    # routed on a grid, scheduled in one launch
+    (8, 8, True, True),
+    (16, 8, True, True),     # the largest batch routed in the schedule's block
+    (17, 8, False, False),   # routed on a grid, scheduled in one launch
     (23, 8, True, False),
     (64, 8, False, True),
     (113, 8, True, False),   # 1017 token-routes: the largest one-launch schedule
