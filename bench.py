@@ -531,7 +531,10 @@ def run_qkv_prefill(plan: Plan, dev, cpu: bool) -> dict:
 
 def run_floor(plan: Plan, dev, banks) -> dict:
     """Memory floors: empty-kernel launches, a streaming read of one dense
-    weight (11 MB) and of one batch-1 MoE layer's 27 matrices (33 MB)."""
+    weight (11 MB), of one batch-1 MoE layer's 27 matrices (33 MB), and of
+    the gate/up weights the batched-decode expert GEMMs read at 16 and 64
+    tokens (the mean distinct experts of the Zipf routing, plus the shared
+    expert; one contiguous region, four copies rotated)."""
     from local_kimi_amd import _lib
 
     lib = _lib.load()
@@ -563,9 +566,25 @@ def run_floor(plan: Plan, dev, banks) -> dict:
     den = time_graph(capture(lambda: [probe([d]) for d in dense], stream), stream,
                      DENSE_COPIES, plan)
     d_bytes = dense[0].numel()
+    del dense
+    gateup = {}
+    for m in (16, 64):
+        rng_m = np.random.default_rng(20260731 + m)
+        unions = [int(torch.unique(cpu_router(torch.from_numpy(zipf_logits(rng_m, m)))[0]).numel())
+                  for _ in range(LAYERS)]
+        nbytes = int(np.mean(unions) + 1) * (EXPERT_BYTES * 2 // 3) // 16 * 16
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3) for _ in range(4)]
+        t = time_graph(capture(lambda: [probe([b]) for b in bufs], stream), stream, 4, plan)
+        gateup[m] = (nbytes, t["us"])
+        del bufs
     log(f"[bench] floor: empty {empty['us']:.2f} us, 11 MB {den['us']:.2f} us, "
-        f"{layer_bytes / 1e6:.1f} MB in 27 regions {moe['us']:.2f} us")
+        f"{layer_bytes / 1e6:.1f} MB in 27 regions {moe['us']:.2f} us, "
+        + ", ".join(f"M={m} gate/up {b / 1e6:.0f} MB {u:.2f} us ({b / (u * 1e3):.0f} GB/s)"
+                    for m, (b, u) in gateup.items()))
     return {"empty_kernel_us": round(empty["us"], 3),
+            **{f"read_gateup_m{m}_{k}": v for m, (b, u) in gateup.items()
+               for k, v in (("bytes", b), ("us", round(u, 3)),
+                            ("gbps", round(b / (u * 1e3), 1)))},
             "read_11MB_us": round(den["us"], 3), "read_11MB_bytes": d_bytes,
             "read_11MB_gbps": round(d_bytes / (den["us"] * 1e3), 1),
             "read_moe_layer_us": round(moe["us"], 3), "read_moe_layer_bytes": layer_bytes,

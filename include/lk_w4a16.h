@@ -56,6 +56,8 @@ LK_API int lk_abi_version(void);
  *   "dense_gemm"         auto | lds       (dense GEMM / fused QKV from 16 rows)
  *   "mxfp4_mfma"         auto | fp4 | bf16 (MXFP4 expert GEMM MFMA form)
  *   "moe_fused_schedule" auto | off       (router + schedule in one launch)
+ *   "moe_split_swiglu"   auto | off       (split gate/up units, SwiGLU in the
+ *                                          down GEMM's staging)
  * Process-wide; set it between calls, not while another thread launches.
  * lk_get_path returns the current choice's index (0 = auto), -1 for an
  * unknown knob. */
@@ -300,9 +302,9 @@ LK_API int lk_w4a16_moe_forward(const uint16_t* x, const float* logits, const fl
  * no reference counterpart. For code under HIP graph capture, tight serving
  * loops and harnesses that forbid hipMalloc: the same arguments minus the
  * workspace, which here is a static device array of
- * lk_w4a16_moe_forward_static_capacity() bytes (8 MiB) per GPU, held until
+ * lk_w4a16_moe_forward_static_capacity() bytes (12 MiB) per GPU, held until
  * the process ends. Calls whose lk_w4a16_moe_forward_workspace() exceeds it
- * are rejected before anything is launched (up to 139 tokens at the
+ * are rejected before anything is launched (up to 160 tokens at the
  * Kimi-Linear shape: hidden 2304, intermediate 1024, 257 experts, top-8).
  * Nothing is allocated or freed; the scratch needs no clearing (every table
  * and row in it is written before it is read). Every call on one GPU shares

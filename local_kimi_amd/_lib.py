@@ -163,6 +163,7 @@ PATH_KNOBS: dict[str, tuple[str, ...]] = {
     "dense_gemm": ("auto", "lds"),
     "mxfp4_mfma": ("auto", "fp4", "bf16"),
     "moe_fused_schedule": ("auto", "off"),
+    "moe_split_swiglu": ("auto", "off"),
 }
 
 

@@ -29,6 +29,7 @@ enum Knob : int {
   kKnobDenseGemm,         // 0 auto, 1 lds
   kKnobMxfp4Mfma,         // 0 auto, 1 fp4, 2 bf16
   kKnobMoeFusedSchedule,  // 0 auto, 1 off
+  kKnobMoeSplitSwiglu,    // 0 auto, 1 off
   kKnobCount
 };
 int path_choice(Knob knob);

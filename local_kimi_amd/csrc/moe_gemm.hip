@@ -1598,7 +1598,25 @@ w4a16_stream_kernel(const GemmArgs g) {
 // per-unit epilogue touches no global memory but its stores.
 constexpr int kPsMaxSegs = 8;     // tiles one block may cover (checked on the host)
 constexpr int kPsHalfMax = 12;    // staging units per thread and LDS buffer (k-steps <= 24)
+constexpr int kPsSwiHalfMax = 4;  // the same for activations staged through the SwiGLU (k-steps <= 8)
 constexpr int kPsBatch = 6;       // staging units in flight per thread in a later phase
+
+// Eight SwiGLU outputs from eight bf16 gate and eight bf16 up values (the
+// gate/up GEMM's outputs, already rounded to bf16): swiglu_bf16's steps after
+// its two input roundings, which leave bf16 values unchanged, so the result
+// is the fused epilogue's bits.
+__device__ inline uint32_t swiglu_bf16_pair(uint32_t gate2, uint32_t up2) {
+  const float g0 = __uint_as_float(gate2 << 16), g1 = __uint_as_float(gate2 & 0xFFFF0000u);
+  const float u0 = __uint_as_float(up2 << 16), u1 = __uint_as_float(up2 & 0xFFFF0000u);
+  const uint32_t lo = f32_to_bf16(round_bf16(silu_fast_f32(g0)) * u0);
+  const uint32_t hi = f32_to_bf16(round_bf16(silu_fast_f32(g1)) * u1);
+  return lo | (hi << 16);
+}
+
+__device__ inline uint4 swiglu_x8(const uint4 gate, const uint4 up) {
+  return make_uint4(swiglu_bf16_pair(gate.x, up.x), swiglu_bf16_pair(gate.y, up.y),
+                    swiglu_bf16_pair(gate.z, up.z), swiglu_bf16_pair(gate.w, up.w));
+}
 constexpr int kPsEarlyPairs = 1;  // ring pairs issued before the first staging completes
 
 template <int FMT>
@@ -1672,14 +1690,28 @@ struct PsPair {
   }
 };
 
-template <int FMT, int MATS, int DEPTH, bool GATHER, bool SCATTER>
+//
+// Split SwiGLU (SPLIT, SWI; decode batches of the MoE block): the gate/up
+// GEMM runs with SPLIT, its units one matrix wide (16 columns of w1, or of
+// w3, for a tile), and writes the two products rounded to bf16 side by side,
+// [rows, 2n] (gate then up). The down GEMM runs with SWI: its activation
+// rows are those [rows, 2k] pairs, and the staging applies the SwiGLU
+// (swiglu_x8) before the values go into LDS. Units of half the bytes shorten
+// the tail of the gate/up launch, where the last units of each block stream
+// alone; the SwiGLU is applied to the same bf16-rounded values as in the
+// fused epilogue, so the block's output is the same bits.
+template <int FMT, int MATS, int DEPTH, bool GATHER, bool SCATTER, bool SPLIT = false,
+          bool SWI = false>
 __global__ void __launch_bounds__(kStWaves * kWave)
 w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   static_assert(FMT == kFmtW4A16 || FMT == kFmtMxBf16, "bf16 activations, 16-byte weight loads");
   static_assert(DEPTH % 2 == 0, "the ring holds pairs of k-steps");
+  static_assert(!SPLIT || MATS == 1, "split units hold one matrix");
+  static_assert(!SWI || (MATS == 1 && !SPLIT), "SwiGLU staging feeds the down GEMM");
   constexpr int kPairs = DEPTH / 2;
   static_assert(kPsEarlyPairs < kPairs, "the staging barrier sits inside the first round");
-  constexpr int NT = MATS == 2 ? 1 : 2;
+  constexpr int NT = SPLIT ? 1 : (MATS == 2 ? 1 : 2);
+  constexpr int kHalfCap = SWI ? kPsSwiHalfMax : kPsHalfMax;
   constexpr bool kMx = FMT != kFmtW4A16;
   extern __shared__ uint4 smem[];
   __shared__ int64_t seg_row[kPsMaxSegs][16];  // activation row of tile row m
@@ -1690,7 +1722,8 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   const int64_t N = g.n, K = g.k;
   const int ksteps = static_cast<int>(K >> 7);  // k % 128 == 0
   const int rounds = ksteps / DEPTH;  // DEPTH divides ksteps (host-checked)
-  const int cgs = static_cast<int>((N + NT * 16 - 1) / (NT * 16));
+  const int cgs1 = static_cast<int>((N + NT * 16 - 1) / (NT * 16));  // column groups per matrix
+  const int cgs = SPLIT ? 2 * cgs1 : cgs1;
   const int total = *g.tile_count * cgs;
   const int per = (total + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
   // ranges go to XCDs in contiguous runs (block b runs on XCD b % 8): the
@@ -1746,7 +1779,8 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   // is left outstanding on any path (the compiler would otherwise wait for
   // every load in flight inside the weight loop).
   const int sc = tid & 15, sm = (tid >> 4) & 15, sl = tid >> 8;
-  const int half = ksteps >> 1;  // ksteps is even (DEPTH is); half <= kPsHalfMax (host-checked)
+  const int half = ksteps >> 1;  // ksteps is even (DEPTH is); half <= kHalfCap (host-checked)
+  const int64_t astride = SWI ? 2 * K : K;  // SWI: gate values, then up values
   const uint16_t* rp[2];
   auto stage_rows = [&](int p) {
 #pragma unroll
@@ -1754,28 +1788,90 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
       const int s = p * nbuf + sb;
       const bool ok = sb < nbuf && s < nseg && sm < seg_rows[s];
       const int64_t row = ok ? seg_row[s][sm] : seg_row[0][0];
-      rp[sb] = g.a + row * K + sl * 128 + sc * 8;
+      rp[sb] = g.a + row * astride + sl * 128 + sc * 8;
     }
   };
   // buffers holding a tile of the block in phase p (block-uniform; the same
   // predicate guards a buffer's loads and its stores)
   auto stage_live = [&](int p, int sb) { return sb < nbuf && p * nbuf + sb < nseg; };
-  auto stage_loads = [&](int p, uint4 (&v)[2][kPsHalfMax]) {
+  auto stage_loads = [&](int p, uint4 (&v)[2][kHalfCap]) {
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-      for (int ii = 0; ii < kPsHalfMax; ++ii)
+      for (int ii = 0; ii < kHalfCap; ++ii)
         if (stage_live(p, sb) && ii < half)
           v[sb][ii] = *reinterpret_cast<const uint4*>(rp[sb] + ii * 256);
   };
-  auto stage_stores = [&](int p, const uint4 (&v)[2][kPsHalfMax]) {
+  auto stage_stores = [&](int p, const uint4 (&v)[2][kHalfCap]) {
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       if (!stage_live(p, sb)) continue;
       const int fb = sb * ksteps + sl;
 #pragma unroll
-      for (int ii = 0; ii < kPsHalfMax; ++ii)
+      for (int ii = 0; ii < kHalfCap; ++ii)
         if (ii < half) ps_stage_store<FMT>(afrag, offs, (fb + 2 * ii) * 4, sc, sm, v[sb][ii]);
+    }
+  };
+  // SWI staging: the SwiGLU runs on the tiles' own rows only (most decode
+  // tiles hold a few rows of their 16). Each 16-lane group takes (tile, row,
+  // k-step) items of the phase's tiles, rows of the first tile first, spread
+  // over the block's 32 groups, two items per pass; rows past a tile's end
+  // are not staged (their MFMA rows are never stored). The passes are a short
+  // rolled loop (it runs once per phase with a cold instruction cache: the
+  // unrolled form took 2-3 us longer to stage), each pass's loads issued
+  // before the previous pass is stored.
+  struct SwiPass {
+    uint4 gv[2], uv[2];
+    int frag[2], row[2];
+    bool ok[2];
+  };
+  constexpr int kGroups = kStWaves * kWave / 16;
+  const int sgid = tid >> 4;
+  // item j < 2 tiles x 16 rows x 8 k-steps + one pass = 320: j / ksteps as
+  // (j * ceil(2^16 / ksteps)) >> 16, exact there
+  const int kinv = (65536 + ksteps - 1) / ksteps;
+  auto swi_count = [&](int p, int& n0) {
+    const int s0 = p * nbuf;
+    n0 = s0 < nseg ? seg_rows[s0] * ksteps : 0;
+    return n0 + (nbuf > 1 && s0 + 1 < nseg ? seg_rows[s0 + 1] * ksteps : 0);
+  };
+  auto swi_load = [&](int p, int j0, SwiPass& sp) {
+    int n0;
+    const int n = swi_count(p, n0);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int j = j0 + q * kGroups;
+      const int sb = j < n0 ? 0 : 1;
+      const int jj = j - sb * n0;
+      const int r = (jj * kinv) >> 16;
+      const int step = jj - r * ksteps;
+      sp.ok[q] = j < n;
+      sp.frag[q] = (sb * ksteps + step) * 4;
+      sp.row[q] = r;
+      if (sp.ok[q]) {
+        const uint16_t* a = g.a + seg_row[p * nbuf + sb][r] * astride + step * 128 + sc * 8;
+        sp.gv[q] = *reinterpret_cast<const uint4*>(a);
+        sp.uv[q] = *reinterpret_cast<const uint4*>(a + K);
+      }
+    }
+  };
+  auto swi_store = [&](const SwiPass& sp) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      if (sp.ok[q])
+        ps_stage_store<FMT>(afrag, offs, sp.frag[q], sc, sp.row[q], swiglu_x8(sp.gv[q], sp.uv[q]));
+  };
+  // stores the pass `cur` (loaded from item sgid) and the rest of phase p
+  auto swi_drain = [&](int p, SwiPass& cur) {
+    int n0;
+    const int n = swi_count(p, n0);
+    for (int j0 = sgid + 2 * kGroups;; j0 += 2 * kGroups) {
+      SwiPass nxt;
+      const bool more = j0 < n;
+      if (more) swi_load(p, j0, nxt);
+      swi_store(cur);
+      if (!more) break;
+      cur = nxt;
     }
   };
 
@@ -1799,17 +1895,21 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
     int s, cgi;
     unit_tile(u, s, cgi);
     const int64_t e = max(seg_exp[s], 0);  // invalid routes: read expert 0, store zeros
+    const bool second = SPLIT && cgi >= cgs1;  // SPLIT: a unit of the second matrix
+    if (second) cgi -= cgs1;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int64_t col = static_cast<int64_t>(cgi) * (NT * 16) + nt * 16 + ln;
       const int64_t cc = col < N ? col : N - 1;
 #pragma unroll
       for (int mi = 0; mi < MATS; ++mi) {
-        lw[mi][nt] = g.wp[mi] + e * g.wstride + cc * rowb;
+        const uint8_t* wpm = SPLIT ? (second ? g.wp[1] : g.wp[0]) : g.wp[mi];
+        const void* wsm = SPLIT ? (second ? g.ws[1] : g.ws[0]) : g.ws[mi];
+        lw[mi][nt] = wpm + e * g.wstride + cc * rowb;
         if constexpr (kMx)
-          lsr[mi][nt] = static_cast<const uint8_t*>(g.ws[mi]) + e * g.sstride + cc * spr;
+          lsr[mi][nt] = static_cast<const uint8_t*>(wsm) + e * g.sstride + cc * spr;
         else
-          lsr[mi][nt] = static_cast<const uint16_t*>(g.ws[mi]) + e * g.sstride + cc * spr;
+          lsr[mi][nt] = static_cast<const uint16_t*>(wsm) + e * g.sstride + cc * spr;
       }
     }
   };
@@ -1818,9 +1918,14 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   // pairs of k-steps of weights; the rest of the first round goes out once the
   // activations are staged, so the activation rows that miss L2 do not queue
   // behind every CU's whole first round
-  stage_rows(0);
-  uint4 sv[2][kPsHalfMax];
-  stage_loads(0, sv);
+  uint4 sv[2][kHalfCap];
+  SwiPass swp;
+  if constexpr (SWI) {
+    swi_load(0, sgid, swp);
+  } else {
+    stage_rows(0);
+    stage_loads(0, sv);
+  }
   PsPair<FMT, MATS, NT> w[kPairs];
   int lu = claim(), lr = 0;  // load cursor: unit, round
   if (lu < ue) set_ptrs(lu);
@@ -1829,7 +1934,10 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
 #pragma unroll
   for (int j = 0; j < kPairs; ++j) {
     if (j == kPsEarlyPairs) {
-      stage_stores(0, sv);
+      if constexpr (SWI)
+        swi_drain(0, swp);
+      else
+        stage_stores(0, sv);
       __syncthreads();
     }
     w[j].load(lw, lsr, lu < ue ? 2 * j : ksteps, jq, ksteps, dummy);
@@ -1916,19 +2024,25 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
       __syncthreads();
       // a later phase (blocks covering more tiles than buffers): batches of
       // kPsBatch units, in a rolled loop to keep registers for the ring
-      stage_rows(p);
-      for (int sb = 0; sb < nbuf; ++sb) {
-        if (!stage_live(p, sb)) continue;
-        for (int i0 = 0; i0 < half; i0 += kPsBatch) {
-          uint4 pv[kPsBatch];
+      if constexpr (SWI) {
+        swi_load(p, sgid, swp);
+        swi_drain(p, swp);
+      } else {
+        stage_rows(p);
+        for (int sb = 0; sb < nbuf; ++sb) {
+          if (!stage_live(p, sb)) continue;
+          for (int i0 = 0; i0 < half; i0 += kPsBatch) {
+            uint4 pv[kPsBatch];
 #pragma unroll
-          for (int b = 0; b < kPsBatch; ++b)
-            if (i0 + b < half)
-              pv[b] = *reinterpret_cast<const uint4*>(rp[sb] + (i0 + b) * 256);
+            for (int b = 0; b < kPsBatch; ++b)
+              if (i0 + b < half)
+                pv[b] = *reinterpret_cast<const uint4*>(rp[sb] + (i0 + b) * 256);
 #pragma unroll
-          for (int b = 0; b < kPsBatch; ++b)
-            if (i0 + b < half)
-              ps_stage_store<FMT>(afrag, offs, (sb * ksteps + sl + 2 * (i0 + b)) * 4, sc, sm, pv[b]);
+            for (int b = 0; b < kPsBatch; ++b)
+              if (i0 + b < half)
+                ps_stage_store<FMT>(afrag, offs, (sb * ksteps + sl + 2 * (i0 + b)) * 4, sc, sm,
+                                    pv[b]);
+          }
         }
       }
       __syncthreads();
@@ -1959,6 +2073,11 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
       if (++cr == rounds) {  // the unit is complete: store it
         const int rows = seg_rows[cseg];
         const bool zero = seg_exp[cseg] < 0;
+        // SPLIT: rows of [gate | up], 2n wide
+        const bool second = SPLIT && ccg >= cgs1;
+        const int ocg = second ? ccg - cgs1 : ccg;
+        const int64_t ostride = SPLIT ? 2 * N : N;
+        const int64_t ocol0 = second ? N : 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int m = jq * 4 + i;
@@ -1966,7 +2085,7 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
           const int64_t orow = seg_out[cseg][m];
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt) {
-            const int64_t col = static_cast<int64_t>(ccg) * (NT * 16) + nt * 16 + ln;
+            const int64_t col = static_cast<int64_t>(ocg) * (NT * 16) + nt * 16 + ln;
             if (col >= N) continue;
             uint16_t v;
             if constexpr (MATS == 2)
@@ -1975,7 +2094,7 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
                                     : swiglu_bf16(tot[0][nt][i], tot[1][nt][i]);
             else
               v = store_value<FMT>(tot[0][nt][i]);
-            out[orow * N + col] = zero ? static_cast<uint16_t>(0) : v;
+            out[orow * ostride + ocol0 + col] = zero ? static_cast<uint16_t>(0) : v;
           }
         }
 #pragma unroll
@@ -2189,7 +2308,7 @@ SplitBufs split_bufs(char* base, int64_t elems) {
 }
 
 MoeLayout moe_layout(int64_t entries, int64_t experts, int64_t act_cols, int64_t out_cols,
-                     int64_t split_x_elems = 0, int64_t pair_rows = 0) {
+                     int64_t split_x_elems = 0, int64_t pair_rows = 0, int act_mult = 1) {
   MoeLayout l;
   l.sched = sched_layout(entries, experts);
   size_t at = l.sched.total;
@@ -2205,8 +2324,9 @@ MoeLayout moe_layout(int64_t entries, int64_t experts, int64_t act_cols, int64_t
   // descriptors up to the bound rounded up to 8 tiles before checking the count
   l.mtiles = at;
   at += align_up(static_cast<size_t>((max_tiles_for(entries, experts, kTileRows) + 7) / 8 * 8) * 16);
+  // (act_mult 2: the split SwiGLU's [gate | up] rows)
   l.act = at;
-  at += align_up(static_cast<size_t>(entries) * act_cols * 2);
+  at += align_up(static_cast<size_t>(entries) * act_cols * 2 * act_mult);
   l.eo = at;
   at += align_up(static_cast<size_t>(entries) * out_cols * 2);
   // fp8 hi/lo splits of the gathered input and of the activations (MXFP4 on
@@ -2415,9 +2535,10 @@ bool stream_fits(int64_t k, int mt, int64_t group, bool mx) {
 
 constexpr int kPsMaxLds = 160 * 1024 - 2048;  // dynamic LDS of one persistent block
 
-template <int FMT, int MATS, int DEPTH, bool GATHER, bool SCATTER>
-int persist_one(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hipStream_t s) {
-  auto* fn = &w4a16_persist_kernel<FMT, MATS, DEPTH, GATHER, SCATTER>;
+template <int FMT, int MATS, int DEPTH, bool GATHER, bool SCATTER, bool SPLIT, bool SWI>
+int persist_one(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hipStream_t s,
+                bool launch) {
+  auto* fn = &w4a16_persist_kernel<FMT, MATS, DEPTH, GATHER, SCATTER, SPLIT, SWI>;
   struct Cfg {
     int device = -1, blocks_per_cu = 0, cus = 0;
     size_t lds = 0;
@@ -2439,37 +2560,48 @@ int persist_one(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hi
     c = Cfg{dev, per_cu, cus, lds};
   }
   const int64_t grid = static_cast<int64_t>(c.cus) * c.blocks_per_cu;
-  constexpr int NT = MATS == 2 ? 1 : 2;
-  const int64_t cgs = (g.n + NT * 16 - 1) / (NT * 16);
+  constexpr int NT = SPLIT ? 1 : (MATS == 2 ? 1 : 2);
+  const int64_t cgs = (SPLIT ? 2 : 1) * ((g.n + NT * 16 - 1) / (NT * 16));
   // a block's range covers at most (per - 1) / cgs + 2 tiles; its tables hold kPsMaxSegs
   const int64_t per = (tiles_bound * cgs + grid - 1) / grid;
   if ((per - 1) / cgs + 2 > kPsMaxSegs) return -1;
   if (tiles_bound * cgs >= (1LL << 31)) return -1;
-  fn<<<static_cast<unsigned>(grid), kStWaves * kWave, lds, s>>>(g, nbuf);
+  if (launch) fn<<<static_cast<unsigned>(grid), kStWaves * kWave, lds, s>>>(g, nbuf);
   return 0;
 }
 
-template <int FMT, int MATS, bool GATHER, bool SCATTER>
-int persist_depth(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hipStream_t s) {
+template <int FMT, int MATS, bool GATHER, bool SCATTER, bool SPLIT, bool SWI>
+int persist_depth(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hipStream_t s,
+                  bool launch) {
   // the ring depth divides the k-steps (at least one whole round per unit)
   const int64_t ksteps = g.k / 128;
   if (ksteps >= 6 && ksteps % 6 == 0)
-    return persist_one<FMT, MATS, 6, GATHER, SCATTER>(g, nbuf, lds, tiles_bound, s);
+    return persist_one<FMT, MATS, 6, GATHER, SCATTER, SPLIT, SWI>(g, nbuf, lds, tiles_bound, s,
+                                                                  launch);
   if (ksteps >= 8 && ksteps % 8 == 0)
-    return persist_one<FMT, MATS, 8, GATHER, SCATTER>(g, nbuf, lds, tiles_bound, s);
+    return persist_one<FMT, MATS, 8, GATHER, SCATTER, SPLIT, SWI>(g, nbuf, lds, tiles_bound, s,
+                                                                  launch);
   if (ksteps >= 4 && ksteps % 4 == 0)
-    return persist_one<FMT, MATS, 4, GATHER, SCATTER>(g, nbuf, lds, tiles_bound, s);
+    return persist_one<FMT, MATS, 4, GATHER, SCATTER, SPLIT, SWI>(g, nbuf, lds, tiles_bound, s,
+                                                                  launch);
   return -1;
 }
+
+// Forms of the persistent GEMM: one launch per product (fused gate/up with
+// its SwiGLU epilogue, or a single matrix), or the split SwiGLU pair of the
+// MoE block (gate/up as one-matrix units writing [rows, 2n], then the down
+// GEMM staging its activations through the SwiGLU).
+enum class PsForm { Plain, SplitGateUp, SwiDown };
 
 // Launches the persistent 16-row GEMM when it applies (schedule modes, 16-byte
 // weight loads, the block's tiles fit in LDS) and returns the launch status;
 // returns kPsNotApplicable when it does not, so the caller takes the per-tile
-// streaming kernel.
+// streaming kernel. With launch == false it only answers whether it applies
+// (0) or not (kPsNotApplicable).
 constexpr int kPsNotApplicable = -1000;
 template <int FMT, int MATS>
 int persist_launch(const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_t s,
-                   const char* what) {
+                   const char* what, PsForm form = PsForm::Plain, bool launch = true) {
   if constexpr (FMT != kFmtW4A16 && FMT != kFmtMxBf16) {
     return kPsNotApplicable;
   } else {
@@ -2482,16 +2614,34 @@ int persist_launch(const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_
     if (nbuf == 0) return kPsNotApplicable;
     const size_t lds = nbuf * one;
     // a phase's activations are staged from one batch of registers per thread
-    if (g.k / 128 > 2 * kPsHalfMax) return kPsNotApplicable;
+    const int half_cap = form == PsForm::SwiDown ? kPsSwiHalfMax : kPsHalfMax;
+    if (g.k / 128 > 2 * half_cap) return kPsNotApplicable;
     int rc = -1;
-    switch (mode) {
-      case Mode::Gather: rc = persist_depth<FMT, MATS, true, false>(g, nbuf, lds, tiles_bound, s); break;
-      case Mode::Scatter: rc = persist_depth<FMT, MATS, false, true>(g, nbuf, lds, tiles_bound, s); break;
-      case Mode::GatherScatter: rc = persist_depth<FMT, MATS, true, true>(g, nbuf, lds, tiles_bound, s); break;
-      default: break;
+    if constexpr (MATS == 1) {
+      if (form == PsForm::SplitGateUp) {
+        if (mode != Mode::Gather || g.act != kActSwiglu) return kPsNotApplicable;
+        rc = persist_depth<FMT, 1, true, false, true, false>(g, nbuf, lds, tiles_bound, s, launch);
+      } else if (form == PsForm::SwiDown) {
+        if (mode != Mode::Scatter || g.act != kActSwiglu) return kPsNotApplicable;
+        rc = persist_depth<FMT, 1, false, true, false, true>(g, nbuf, lds, tiles_bound, s, launch);
+      }
+    }
+    if (form == PsForm::Plain) {
+      switch (mode) {
+        case Mode::Gather:
+          rc = persist_depth<FMT, MATS, true, false, false, false>(g, nbuf, lds, tiles_bound, s, launch);
+          break;
+        case Mode::Scatter:
+          rc = persist_depth<FMT, MATS, false, true, false, false>(g, nbuf, lds, tiles_bound, s, launch);
+          break;
+        case Mode::GatherScatter:
+          rc = persist_depth<FMT, MATS, true, true, false, false>(g, nbuf, lds, tiles_bound, s, launch);
+          break;
+        default: break;
+      }
     }
     if (rc < 0) return kPsNotApplicable;
-    return check_launch(what);
+    return launch ? check_launch(what) : 0;
   }
 }
 
@@ -2616,6 +2766,18 @@ int stream_tile_mt(int64_t entries) {
 // workspace query and the call agree through this; calls whose group is not
 // 128 leave them unused).
 bool moe_pairs(int64_t entries, bool mx) { return !mx && stream_tile_mt(entries) == 4; }
+
+// Whether an expert-major call of `entries` token-routes sizes its activation
+// region for the split SwiGLU of the 16-row launches ([gate | up] rows, twice
+// the SwiGLU's width); the workspace query and the call agree through this.
+int moe_act_mult(int64_t entries) { return stream_tile_mt(entries) == 1 ? 2 : 1; }
+
+template <int MATS>
+int persist_fmt(bool mx, const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_t s,
+                const char* what, PsForm form, bool launch) {
+  if (mx) return persist_launch<kFmtMxBf16, MATS>(g, mode, tiles_bound, s, what, form, launch);
+  return persist_launch<kFmtW4A16, MATS>(g, mode, tiles_bound, s, what, form, launch);
+}
 
 // W4A16: a power-of-two group (multiple of 32) dividing k; MXFP4: 32.
 int check_format(bool mx, int64_t k, int64_t group) {
@@ -3003,15 +3165,19 @@ int64_t lk_w4a16_moe_forward_workspace(int64_t tokens, int64_t experts, int64_t 
   if (tokens < 0 || experts < 2 || h <= 0 || i <= 0 || top_k <= 0) return -1;
   if (check_schedule_dims(tokens, top_k + 1, experts)) return -1;
   const int64_t entries = tokens * (top_k + 1);
-  return static_cast<int64_t>(
-      moe_layout(entries, experts, i, h, 0, moe_pairs(entries, false) ? tokens : 0).total);
+  return static_cast<int64_t>(moe_layout(entries, experts, i, h, 0,
+                                         moe_pairs(entries, false) ? tokens : 0,
+                                         moe_act_mult(entries))
+                                  .total);
 }
 
 int64_t lk_mxfp4_moe_forward_workspace(int64_t tokens, int64_t experts, int64_t h, int64_t i,
                                        int64_t top_k) {
   if (tokens < 0 || experts < 2 || h <= 0 || i <= 0 || top_k <= 0) return -1;
   if (check_schedule_dims(tokens, top_k + 1, experts)) return -1;
-  return static_cast<int64_t>(moe_layout(tokens * (top_k + 1), experts, i, h, tokens * h).total);
+  const int64_t entries = tokens * (top_k + 1);
+  return static_cast<int64_t>(
+      moe_layout(entries, experts, i, h, tokens * h, 0, moe_act_mult(entries)).total);
 }
 
 int lk_mxfp4_split_activations(const uint16_t* x, uint8_t* hi, uint8_t* lo, uint16_t* scales,
@@ -3052,8 +3218,8 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   LK_REQUIRE(x && logits && workspace, "null pointer argument");
   const int64_t routes = top_k + 1;
   const int64_t entries = tokens * routes;
-  const MoeLayout l =
-      moe_layout(entries, experts, i, h, mx ? tokens * h : 0, moe_pairs(entries, mx) ? tokens : 0);
+  const MoeLayout l = moe_layout(entries, experts, i, h, mx ? tokens * h : 0,
+                                 moe_pairs(entries, mx) ? tokens : 0, moe_act_mult(entries));
   LK_REQUIRE(workspace_bytes >= static_cast<int64_t>(l.total),
              "MoE workspace too small: %lld < %lld bytes", (long long)workspace_bytes,
              (long long)l.total);
@@ -3141,40 +3307,62 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   // route that uses it rather than once per call.
   const bool w2_rows = !mx && tokens <= kW2RowsMaxTokens && w2_rows_fits(routes, i);
   const Mode gu_mode = w2_rows ? Mode::GatherScatter : Mode::Gather;
+  // down projection: sorted activation rows, outputs scattered to (token, route) rows
+  auto down_args = [&](GemmArgs d) {
+    d.a = act;
+    d.a_hi = as.hi;
+    d.a_lo = as.lo;
+    d.a_sc = as.sc;
+    d.a_rows = entries;
+    if (paired) {  // written paired by the gate/up GEMM, with their group sums
+      d.a_pair = act;
+      d.a_neg = d.out_neg;
+      d.out_neg = nullptr;
+    }
+    d.wp[0] = d.wp[1] = d.wp[2] = w2_packed;
+    d.ws[0] = d.ws[1] = d.ws[2] = w2_scales;
+    d.out[0] = d.out[1] = d.out[2] = eo;
+    d.n = h;
+    d.k = i;
+    d.wstride = h * i / 2;
+    d.sstride = h * (i / group);
+    return d;
+  };
+  // Decode batches on the persistent kernels take the split SwiGLU (gate and
+  // up as separate one-matrix units into [gate | up] rows, the SwiGLU applied
+  // by the down GEMM's staging) when both of its launches apply; the results
+  // are the fused form's bits (the path knob moe_split_swiglu=off keeps the
+  // fused form). The act region holds 2i per row for it (moe_act_mult). At
+  // 64 tokens of the Kimi-Linear layer the gate/up launch takes 73.1 us split
+  // against 81.4 us fused, at 16 tokens 34.8 against 38.1 us: units of half
+  // the bytes shorten the launch's tail, where each block's last units
+  // stream alone.
+  const bool split =
+      mt == 1 && !f8 && !w2_rows && moe_act_mult(entries) == 2 &&
+      path_choice(kKnobMoeSplitSwiglu) != 1 &&
+      persist_fmt<1>(mx, g, Mode::Gather, tb, s, "", PsForm::SplitGateUp, false) == 0 &&
+      persist_fmt<1>(mx, down_args(g), Mode::Scatter, tb, s, "", PsForm::SwiDown, false) == 0;
   if (int rc = f8 ? stream_launch<kFmtMxF8, 2>(g, Mode::Gather, tb, mt, s, "moe gate/up gemm")
-               : mt ? stream_fmt<2>(mx, g, gu_mode, tb, mt, s, "moe gate/up gemm")
-                    : launch_fmt<2>(mx, g, gu_mode, tb, wide_cols_for(tb, i), s,
-                                    "moe gate/up gemm"))
+               : split ? persist_fmt<1>(mx, g, Mode::Gather, tb, s, "moe gate/up gemm",
+                                        PsForm::SplitGateUp, true)
+               : mt    ? stream_fmt<2>(mx, g, gu_mode, tb, mt, s, "moe gate/up gemm")
+                       : launch_fmt<2>(mx, g, gu_mode, tb, wide_cols_for(tb, i), s,
+                                       "moe gate/up gemm"))
     return rc;
   if (w2_rows)
     return w2_combine_rows(act, expert_indices, top_k, experts - 1, weights, top_k, w2_packed,
                            static_cast<const uint16_t*>(w2_scales), y, tokens, routes, experts,
                            h, i, group, s);
-  // down projection: sorted activation rows, outputs scattered to (token, route) rows
   if (f8) {
     if (int rc = split_launch(act, as.hi, as.lo, as.sc, entries, i, s)) return rc;
   }
-  g.a = act;
-  g.a_hi = as.hi;
-  g.a_lo = as.lo;
-  g.a_sc = as.sc;
-  g.a_rows = entries;
-  if (paired) {  // written paired by the gate/up GEMM, with their group sums
-    g.a_pair = act;
-    g.a_neg = g.out_neg;
-    g.out_neg = nullptr;
-  }
-  g.wp[0] = g.wp[1] = g.wp[2] = w2_packed;
-  g.ws[0] = g.ws[1] = g.ws[2] = w2_scales;
-  g.out[0] = g.out[1] = g.out[2] = eo;
-  g.n = h;
-  g.k = i;
-  g.wstride = h * i / 2;
-  g.sstride = h * (i / group);
+  g = down_args(g);
   if (int rc = f8 ? stream_launch<kFmtMxF8, 1>(g, Mode::Scatter, tb, mt, s, "moe down gemm")
-               : mt ? stream_fmt<1>(mx, g, Mode::Scatter, tb, mt, s, "moe down gemm")
-                    : launch_fmt<1>(mx, g, Mode::Scatter, tb, wide_cols_for(tb, h), s,
-                                    "moe down gemm"))
+               : split ? persist_fmt<1>(mx, g, Mode::Scatter, tb, s, "moe down gemm",
+                                        PsForm::SwiDown, true)
+               : mt    ? stream_fmt<1>(mx, g, Mode::Scatter, tb, mt, s, "moe down gemm")
+                       : launch_fmt<1>(mx, g, Mode::Scatter, tb, wide_cols_for(tb, h), s,
+                                       "moe down gemm"))
     return rc;
   const int64_t work = tokens * (h / 8);
   moe_combine_kernel<<<static_cast<unsigned>((work + 255) / 256), 256, 0, s>>>(
@@ -3202,7 +3390,7 @@ int lk_w4a16_moe_forward(const uint16_t* x, const float* logits, const float* bi
 // the process ends. Host code never passes the array's name to a kernel (on
 // the host it is a stand-in, not a device address); it uses the address
 // hipGetSymbolAddress returns for the current device.
-constexpr size_t kStaticScratchBytes = size_t{8} << 20;
+constexpr size_t kStaticScratchBytes = size_t{12} << 20;
 static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
 
 namespace lk {

@@ -57,6 +57,7 @@ constexpr KnobSpec kKnobs[kKnobCount] = {
     {"dense_gemm", {"auto", "lds", nullptr, nullptr}},
     {"mxfp4_mfma", {"auto", "fp4", "bf16", nullptr}},
     {"moe_fused_schedule", {"auto", "off", nullptr, nullptr}},
+    {"moe_split_swiglu", {"auto", "off", nullptr, nullptr}},
 };
 
 std::atomic<int> g_knobs[kKnobCount];  // zero-initialised: "auto"

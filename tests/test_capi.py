@@ -154,12 +154,12 @@ def test_token_major_decode_route_limit_is_checked_before_any_launch(lib):
 
 
 def test_static_scratch_entry_point_refuses_oversized_calls_on_the_host(lib):
-    # 140 Kimi-Linear tokens need more than the static scratch holds: refused
+    # 161 Kimi-Linear tokens need more than the static scratch holds: refused
     # before the device is touched (null device pointers are never read)
     cap = lib.lk_w4a16_moe_forward_static_capacity()
-    assert cap == 8 << 20
-    assert lib.lk_w4a16_moe_forward_workspace(139, 257, 2304, 1024, 8) <= cap
-    assert lib.lk_w4a16_moe_forward_workspace(140, 257, 2304, 1024, 8) > cap
+    assert cap == 12 << 20
+    assert lib.lk_w4a16_moe_forward_workspace(160, 257, 2304, 1024, 8) <= cap
+    assert lib.lk_w4a16_moe_forward_workspace(161, 257, 2304, 1024, 8) > cap
     with pytest.raises(RuntimeError, match="static scratch holds"):
         _lib.call("lk_w4a16_moe_forward_static", 1, 1, None, 1, 1, 1, 1, 1, 1, 1, 1, 1,
-                  140, 257, 2304, 1024, 8, 1.0, 1, 128, None)
+                  161, 257, 2304, 1024, 8, 1.0, 1, 128, None)

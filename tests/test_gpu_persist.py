@@ -201,3 +201,59 @@ def test_persistent_block_under_graph_replay(rng):
         torch.cuda.synchronize()
         assert torch.equal(gy, eager)
         assert torch.equal(gidx, eidx)
+
+
+@pytest.mark.parametrize("weights,tokens", [("w4a16", 16), ("w4a16", 64), ("w4a16", 150),
+                                            ("mxfp4", 64)])
+def test_split_swiglu_matches_the_fused_epilogue(rng, weights, tokens):
+    """The Kimi-Linear layer (hidden 2304, intermediate 1024, 256 routed
+    experts + shared, top-8): split gate/up units with the SwiGLU in the down
+    GEMM's staging against the fused gate/up epilogue (path knob
+    moe_split_swiglu=off), bit-identical, and the oracle on three tokens."""
+    from local_kimi_amd._lib import forced_path
+    from local_kimi_amd.kernels import mxfp4_moe_block, w4a16_moe_forward
+    from local_kimi_amd.quant import quantize_mxfp4
+    from local_kimi_amd.workloads import zipf_router_logits
+
+    e_routed, h, inter, k = 256, 2304, 1024, 8
+    gen = torch.Generator(device=DEV).manual_seed(20260802 + tokens)
+    if weights == "w4a16":
+        banks = (*_gpu_w4_bank(gen, e_routed + 1, inter, h),
+                 *_gpu_w4_bank(gen, e_routed + 1, inter, h),
+                 *_gpu_w4_bank(gen, e_routed + 1, h, inter))
+        block = w4a16_moe_forward
+    else:
+        def mx_bank(n, kk):
+            enc = [quantize_mxfp4((torch.randn(n, kk, device=DEV, generator=gen) * 0.02)
+                                  .to(torch.bfloat16)) for _ in range(e_routed + 1)]
+            return torch.stack([p for p, _ in enc]), torch.stack([q for _, q in enc])
+        banks = (*mx_bank(inter, h), *mx_bank(inter, h), *mx_bank(h, inter))
+        block = mxfp4_moe_block
+    x = random_bf16_bits(rng, (tokens, h))
+    logits = zipf_router_logits(rng, tokens, e_routed)
+    args = (_dev(x), _dev(logits), None, *banks, k, 2.446)
+    with forced_path("moe_gemm", "auto"):
+        y, idx, w = block(*args)
+        torch.cuda.synchronize()
+        with forced_path("moe_split_swiglu", "off"):
+            y0, idx0, w0 = block(*args)
+            torch.cuda.synchronize()
+    assert torch.equal(idx, idx0) and torch.equal(w, w0)
+    assert torch.equal(y, y0), "split and fused SwiGLU forms differ"
+    # oracle on three tokens, with only the experts they route to
+    sel = np.array([0, tokens // 2, tokens - 1])
+    eidx, ew = OM.route(logits[sel], None, k, routed_scaling_factor=2.446)
+    assert np.array_equal(idx.cpu().numpy()[sel], eidx)
+    used = sorted(set(eidx.reshape(-1).tolist()) | {e_routed})
+    remap = {e: j for j, e in enumerate(used)}
+    stable = np.array([[remap[e] for e in row] + [remap[e_routed]] for row in eidx.tolist()])
+    sub = [b[used].cpu().numpy() if b.dtype == torch.uint8 else to_bits(b[used]) for b in banks]
+    cw = np.concatenate((ew, np.ones((len(sel), 1), np.float32)), 1)
+    if weights == "w4a16":
+        act = OW.swiglu(x[sel], stable, sub[0], sub[1], sub[2], sub[3], 128)
+        ey = OM.w2_combine(act, stable, cw, sub[4], sub[5], 128)
+    else:
+        act = X.swiglu(x[sel], stable, sub[0], sub[1], sub[2], sub[3])
+        eo = X.grouped(act.reshape(len(sel) * (k + 1), -1), stable.reshape(-1, 1), sub[4], sub[5])
+        ey = OM.combine(eo.reshape(len(sel), k + 1, -1), cw)
+    assert_close_bf16(to_bits(y)[sel], ey, what=f"{weights} split SwiGLU T={tokens}")

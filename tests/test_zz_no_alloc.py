@@ -85,7 +85,7 @@ def test_static_scratch_matches_the_workspace_entry_point(banks):
 
 def test_static_scratch_refuses_calls_past_its_size(banks):
     cap = _lib.query("lk_w4a16_moe_forward_static_capacity")
-    too_many = 140
+    too_many = 161
     assert _lib.query("lk_w4a16_moe_forward_workspace", too_many, ROUTED + 1, H, INTER,
                       TOP_K) > cap
     x, logits = _inputs(np.random.default_rng(1), too_many)
