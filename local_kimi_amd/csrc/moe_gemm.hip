@@ -1710,7 +1710,10 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   static_assert(!SWI || (MATS == 1 && !SPLIT), "SwiGLU staging feeds the down GEMM");
   constexpr int kPairs = DEPTH / 2;
   static_assert(kPsEarlyPairs < kPairs, "the staging barrier sits inside the first round");
-  constexpr int NT = SPLIT ? 1 : (MATS == 2 ? 1 : 2);
+  // units are 16 columns (one MFMA column tile per matrix): at 64 tokens of
+  // the Kimi-Linear layer the down GEMM takes 40.5 us with them against
+  // 43.1 us with 32-column units, whose longer last units stretch the tail
+  constexpr int NT = 1;
   constexpr int kHalfCap = SWI ? kPsSwiHalfMax : kPsHalfMax;
   constexpr bool kMx = FMT != kFmtW4A16;
   extern __shared__ uint4 smem[];
@@ -2560,7 +2563,7 @@ int persist_one(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hi
     c = Cfg{dev, per_cu, cus, lds};
   }
   const int64_t grid = static_cast<int64_t>(c.cus) * c.blocks_per_cu;
-  constexpr int NT = SPLIT ? 1 : (MATS == 2 ? 1 : 2);
+  constexpr int NT = 1;  // 16-column units, as in the kernel
   const int64_t cgs = (SPLIT ? 2 : 1) * ((g.n + NT * 16 - 1) / (NT * 16));
   // a block's range covers at most (per - 1) / cgs + 2 tiles; its tables hold kPsMaxSegs
   const int64_t per = (tiles_bound * cgs + grid - 1) / grid;
