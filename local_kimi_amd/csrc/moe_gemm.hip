@@ -94,59 +94,59 @@ __device__ inline int wave_inclusive_scan(int v) {
   return v;
 }
 
-// In-place exclusive prefix sum of vals[0, count) by one whole wave; every
-// lane of the wave gets the total.
-__device__ inline int wave_exclusive_scan(int* vals, int count) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int per = (count + kWave - 1) / kWave;
-  const int b = min(count, lane * per);
-  const int e = min(count, b + per);
-  int s = 0;
-  for (int i = b; i < e; ++i) s += vals[i];
-  const int incl = wave_inclusive_scan(s);
-  int run = incl - s;
-  for (int i = b; i < e; ++i) {
-    const int v = vals[i];
-    vals[i] = run;
-    run += v;
-  }
-  return __shfl(incl, kWave - 1, kWave);
-}
-
 // Places the entries of one chunk: tot[b] = entries of bucket b overall,
 // before[b] = entries of bucket b in earlier chunks. Block 0 also writes the
-// bucket offsets and the tile list (it reuses `before`, all zero there).
-__device__ void place_chunk(int64_t n, int nb, int* tot, int* before, int* start, int* mbefore,
-                            bool valid, int64_t entry, int b, int rank, const Schedule& sc) {
-  for (int i = threadIdx.x; i < nb; i += blockDim.x) start[i] = tot[i];
-  __syncthreads();
-  if (threadIdx.x < kWave) wave_exclusive_scan(start, nb);
+// bucket offsets and the tile lists. One wave takes the three prefix sums
+// over the buckets in one pass (entries, tile_rows-row tiles, merged 64-row
+// tiles): one barrier before the writes instead of a scan and barriers each.
+__device__ void place_chunk(int64_t n, int nb, const int* tot, const int* before, int* start,
+                            int* tbefore, int* mbefore, bool valid, int64_t entry, int b,
+                            int rank, const Schedule& sc) {
+  const int tshift = sc.tile_rows == kTileRows ? 6 : 4;  // 64- or 16-row tiles
+  if (threadIdx.x < kWave) {
+    const int lane = threadIdx.x;
+    const int per = (nb + kWave - 1) / kWave;
+    const int b0 = min(nb, lane * per);
+    const int b1 = min(nb, b0 + per);
+    int se = 0, st = 0, sm = 0;
+    for (int i = b0; i < b1; ++i) {
+      const int c = tot[i];
+      se += c;
+      st += (c + (1 << tshift) - 1) >> tshift;
+      sm += merged_tiles(c);
+    }
+    const int ie = wave_inclusive_scan(se);
+    const int it = wave_inclusive_scan(st);
+    const int im = wave_inclusive_scan(sm);
+    int re = ie - se, rt = it - st, rm = im - sm;
+    for (int i = b0; i < b1; ++i) {
+      const int c = tot[i];
+      start[i] = re;
+      tbefore[i] = rt;
+      mbefore[i] = rm;
+      re += c;
+      rt += (c + (1 << tshift) - 1) >> tshift;
+      rm += merged_tiles(c);
+    }
+    if (lane == kWave - 1 && blockIdx.x == 0) {
+      *sc.tile_count = it;
+      if (sc.mtiles != nullptr) *sc.mtile_count = im;
+    }
+  }
   __syncthreads();
   if (valid) sc.perm[start[b] + before[b] + rank] = static_cast<int32_t>(entry);
   if (blockIdx.x != 0) return;
   for (int i = threadIdx.x; i < nb; i += blockDim.x) sc.offsets[i] = start[i];
   if (threadIdx.x == 0) sc.offsets[nb] = static_cast<int32_t>(n);
-  __syncthreads();
-  const int tr = sc.tile_rows;
-  for (int i = threadIdx.x; i < nb; i += blockDim.x) before[i] = (tot[i] + tr - 1) / tr;
-  __syncthreads();
-  int total_tiles = 0;
-  if (threadIdx.x < kWave) total_tiles = wave_exclusive_scan(before, nb);
-  __syncthreads();
+  const int tr = 1 << tshift;
   for (int bb = threadIdx.x; bb < nb; bb += blockDim.x) {
     const int cnt = tot[bb];
     const int expert = bb < nb - 1 ? bb : -1;
-    int4* out = reinterpret_cast<int4*>(sc.tiles) + before[bb];
+    int4* out = reinterpret_cast<int4*>(sc.tiles) + tbefore[bb];
     for (int row = 0; row < cnt; row += tr, ++out)
       *out = make_int4(expert, start[bb] + row, min(tr, cnt - row), 0);
   }
-  if (threadIdx.x == 0) *sc.tile_count = total_tiles;
   if (sc.mtiles == nullptr) return;  // uniform over the block
-  for (int i = threadIdx.x; i < nb; i += blockDim.x) mbefore[i] = merged_tiles(tot[i]);
-  __syncthreads();
-  int merged_total = 0;
-  if (threadIdx.x < kWave) merged_total = wave_exclusive_scan(mbefore, nb);
-  __syncthreads();
   for (int bb = threadIdx.x; bb < nb; bb += blockDim.x) {
     const int cnt = tot[bb];
     const int mt = merged_tiles(cnt);
@@ -155,7 +155,6 @@ __device__ void place_chunk(int64_t n, int nb, int* tot, int* before, int* start
     for (int j = 0; j < mt; ++j)
       out[j] = make_int4(expert, start[bb] + 64 * j, j + 1 < mt ? 64 : cnt - 64 * j, 0);
   }
-  if (threadIdx.x == 0) *sc.mtile_count = merged_total;
 }
 
 // One chunk of kSchedThreads entries per block: per-wave bitmaps of the
@@ -166,7 +165,8 @@ __global__ void __launch_bounds__(kSchedThreads)
 schedule_count_kernel(const RouteTable rt, int64_t n, Schedule sc) {
   __shared__ uint32_t bits[kSchedWaves * kMaxBuckets * 2];
   __shared__ int pre[kSchedWaves * kMaxBuckets];
-  __shared__ int tot[kMaxBuckets], before[kMaxBuckets], start[kMaxBuckets], mbefore[kMaxBuckets];
+  __shared__ int tot[kMaxBuckets], before[kMaxBuckets], start[kMaxBuckets], mbefore[kMaxBuckets],
+      tbefore[kMaxBuckets];
   const int nb = static_cast<int>(rt.experts) + 1;
   for (int i = threadIdx.x; i < kSchedWaves * nb * 2; i += kSchedThreads) bits[i] = 0u;
   __syncthreads();
@@ -197,7 +197,7 @@ schedule_count_kernel(const RouteTable rt, int64_t n, Schedule sc) {
     rank = pre[w * nb + b] + below;
   }
   if (gridDim.x == 1) {
-    place_chunk(n, nb, tot, before, start, mbefore, valid, entry, b, rank, sc);
+    place_chunk(n, nb, tot, before, start, tbefore, mbefore, valid, entry, b, rank, sc);
   } else if (valid) {
     sc.rank[entry] = rank;
   }
@@ -205,7 +205,8 @@ schedule_count_kernel(const RouteTable rt, int64_t n, Schedule sc) {
 
 __global__ void __launch_bounds__(kSchedThreads)
 schedule_place_kernel(const RouteTable rt, int64_t n, int chunks, Schedule sc) {
-  __shared__ int tot[kMaxBuckets], before[kMaxBuckets], start[kMaxBuckets], mbefore[kMaxBuckets];
+  __shared__ int tot[kMaxBuckets], before[kMaxBuckets], start[kMaxBuckets], mbefore[kMaxBuckets],
+      tbefore[kMaxBuckets];
   const int nb = static_cast<int>(rt.experts) + 1;
   const int c = blockIdx.x;
   for (int bb = threadIdx.x; bb < nb; bb += kSchedThreads) {
@@ -231,7 +232,7 @@ schedule_place_kernel(const RouteTable rt, int64_t n, int chunks, Schedule sc) {
   const bool valid = entry < n;
   const int b = valid ? rt.bucket(entry) : 0;
   const int rank = valid ? sc.rank[entry] : 0;
-  place_chunk(n, nb, tot, before, start, mbefore, valid, entry, b, rank, sc);
+  place_chunk(n, nb, tot, before, start, tbefore, mbefore, valid, entry, b, rank, sc);
 }
 
 // Schedule of up to kFuseThreads token-routes over at most 257 bank entries
@@ -261,7 +262,7 @@ schedule_one_kernel(const RouteTable rt, int64_t n, Schedule sc, const float* __
   __shared__ uint32_t bits[kFuseWaves * kFuseBuckets * 2];
   __shared__ int pre[kFuseWaves * kFuseBuckets];
   __shared__ int tot[kFuseBuckets], before[kFuseBuckets], start[kFuseBuckets],
-      mbefore[kFuseBuckets];
+      mbefore[kFuseBuckets], tbefore[kFuseBuckets];
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
   const int nb = static_cast<int>(rt.experts) + 1;  // bank entries and the invalid bucket
@@ -307,7 +308,7 @@ schedule_one_kernel(const RouteTable rt, int64_t n, Schedule sc, const float* __
                                 : __popc(lo) + __popc(hi & ((1u << (lane - 32)) - 1u));
     rank = pre[w * nb + b] + below;
   }
-  place_chunk(n, nb, tot, before, start, mbefore, valid, entry, b, rank, sc);
+  place_chunk(n, nb, tot, before, start, tbefore, mbefore, valid, entry, b, rank, sc);
 }
 
 // ---------------------------------------------------------------------------
