@@ -1816,32 +1816,35 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
         if (ii < half) ps_stage_store<FMT>(afrag, offs, (fb + 2 * ii) * 4, sc, sm, v[sb][ii]);
     }
   };
-  // SWI staging: the SwiGLU runs on the tiles' own rows only (most decode
-  // tiles hold a few rows of their 16). Each 16-lane group takes (tile, row,
-  // k-step) items of the phase's tiles, rows of the first tile first, spread
-  // over the block's 32 groups, two items per pass; rows past a tile's end
-  // are not staged (their MFMA rows are never stored). The passes are a short
-  // rolled loop (it runs once per phase with a cold instruction cache: the
-  // unrolled form took 2-3 us longer to stage), each pass's loads issued
-  // before the previous pass is stored.
-  struct SwiPass {
+  // Compact staging: only the tiles' own rows (most decode tiles hold a few
+  // rows of their 16). Each 16-lane group takes (tile, row, k-step) items of
+  // the phase's tiles, rows of the first tile first, spread over the block's
+  // 32 groups, two items per pass; rows past a tile's end are not staged
+  // (their MFMA rows are never stored). The passes are a short rolled loop
+  // (it runs once per phase with a cold instruction cache: an unrolled form
+  // of the SwiGLU staging took 2-3 us longer), each pass's loads issued
+  // before the previous pass is stored. SWI stages through the SwiGLU this
+  // way always; the other forms when the phase holds at most kCompactItems
+  // items, else every row of both buffers at once (stage_loads).
+  struct CPass {
     uint4 gv[2], uv[2];
     int frag[2], row[2];
     bool ok[2];
   };
   constexpr int kGroups = kStWaves * kWave / 16;
+  constexpr int kCompactItems = 8 * kGroups;  // four passes
   const int sgid = tid >> 4;
-  // item j < 2 tiles x 16 rows x 8 k-steps + one pass = 320: j / ksteps as
+  // item j < 2 tiles x 16 rows x 24 k-steps + one pass = 832: j / ksteps as
   // (j * ceil(2^16 / ksteps)) >> 16, exact there
   const int kinv = (65536 + ksteps - 1) / ksteps;
-  auto swi_count = [&](int p, int& n0) {
+  auto cs_count = [&](int p, int& n0) {
     const int s0 = p * nbuf;
     n0 = s0 < nseg ? seg_rows[s0] * ksteps : 0;
     return n0 + (nbuf > 1 && s0 + 1 < nseg ? seg_rows[s0 + 1] * ksteps : 0);
   };
-  auto swi_load = [&](int p, int j0, SwiPass& sp) {
+  auto cs_load = [&](int p, int j0, CPass& sp) {
     int n0;
-    const int n = swi_count(p, n0);
+    const int n = cs_count(p, n0);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int j = j0 + q * kGroups;
@@ -1855,28 +1858,33 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
       if (sp.ok[q]) {
         const uint16_t* a = g.a + seg_row[p * nbuf + sb][r] * astride + step * 128 + sc * 8;
         sp.gv[q] = *reinterpret_cast<const uint4*>(a);
-        sp.uv[q] = *reinterpret_cast<const uint4*>(a + K);
+        if constexpr (SWI) sp.uv[q] = *reinterpret_cast<const uint4*>(a + K);
       }
     }
   };
-  auto swi_store = [&](const SwiPass& sp) {
+  auto cs_store = [&](const CPass& sp) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
       if (sp.ok[q])
-        ps_stage_store<FMT>(afrag, offs, sp.frag[q], sc, sp.row[q], swiglu_x8(sp.gv[q], sp.uv[q]));
+        ps_stage_store<FMT>(afrag, offs, sp.frag[q], sc, sp.row[q],
+                            SWI ? swiglu_x8(sp.gv[q], sp.uv[q]) : sp.gv[q]);
   };
   // stores the pass `cur` (loaded from item sgid) and the rest of phase p
-  auto swi_drain = [&](int p, SwiPass& cur) {
+  auto cs_drain = [&](int p, CPass& cur) {
     int n0;
-    const int n = swi_count(p, n0);
+    const int n = cs_count(p, n0);
     for (int j0 = sgid + 2 * kGroups;; j0 += 2 * kGroups) {
-      SwiPass nxt;
+      CPass nxt;
       const bool more = j0 < n;
-      if (more) swi_load(p, j0, nxt);
-      swi_store(cur);
+      if (more) cs_load(p, j0, nxt);
+      cs_store(cur);
       if (!more) break;
       cur = nxt;
     }
+  };
+  auto cs_compact = [&](int p) {
+    int n0;
+    return SWI || cs_count(p, n0) <= kCompactItems;
   };
 
   // Waves claim the block's units in order, one at a time, when their ring
@@ -1923,10 +1931,11 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   // activations are staged, so the activation rows that miss L2 do not queue
   // behind every CU's whole first round
   uint4 sv[2][kHalfCap];
-  SwiPass swp;
-  if constexpr (SWI) {
-    swi_load(0, sgid, swp);
-  } else {
+  CPass csp;
+  const bool compact0 = cs_compact(0);  // block-uniform
+  if (compact0) {
+    cs_load(0, sgid, csp);
+  } else if constexpr (!SWI) {
     stage_rows(0);
     stage_loads(0, sv);
   }
@@ -1938,9 +1947,9 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
 #pragma unroll
   for (int j = 0; j < kPairs; ++j) {
     if (j == kPsEarlyPairs) {
-      if constexpr (SWI)
-        swi_drain(0, swp);
-      else
+      if (compact0)
+        cs_drain(0, csp);
+      else if constexpr (!SWI)
         stage_stores(0, sv);
       __syncthreads();
     }
@@ -2028,10 +2037,10 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
       __syncthreads();
       // a later phase (blocks covering more tiles than buffers): batches of
       // kPsBatch units, in a rolled loop to keep registers for the ring
-      if constexpr (SWI) {
-        swi_load(p, sgid, swp);
-        swi_drain(p, swp);
-      } else {
+      if (cs_compact(p)) {
+        cs_load(p, sgid, csp);
+        cs_drain(p, csp);
+      } else if constexpr (!SWI) {
         stage_rows(p);
         for (int sb = 0; sb < nbuf; ++sb) {
           if (!stage_live(p, sb)) continue;
