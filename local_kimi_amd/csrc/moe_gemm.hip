@@ -1587,16 +1587,18 @@ w4a16_stream_kernel(const GemmArgs g) {
 // ---------------------------------------------------------------------------
 // Persistent streaming GEMM over 16-row tiles (decode batches; 16-byte
 // weight loads). The grid is one resident block (8 waves) per CU slot. Block b
-// takes an equal contiguous range of units (tile, 16 * NT-column group) in
-// tile order, and its waves claim the units of the range one at a time, in
-// order, so there are no rounds of blocks and a CU's waves finish together. Each wave keeps DEPTH k-steps of weights in flight across its units:
+// takes an equal contiguous range of units (tile, 16-column group) in tile
+// order, and its waves claim the units of the range one at a time, in order,
+// so there are no rounds of blocks and a CU's waves finish together. Each
+// wave keeps DEPTH k-steps of weights in flight across its units:
 // the loads of a unit's first k-steps are issued while the previous unit's
 // last k-steps are computed, so the weight stream never drains between tiles.
 // The block's tiles (segments) are staged in LDS once, nbuf at a time (a range
-// covering more tiles advances in phases with a block barrier between them);
-// their activation loads are issued before the weight ring, so staging does
-// not wait behind the ring. Tile descriptors and output rows sit in LDS: the
-// per-unit epilogue touches no global memory but its stores.
+// covering more tiles advances in phases with a block barrier between them),
+// only their own rows when a phase holds few; their activation loads are
+// issued before the weight ring, so staging does not wait behind the ring.
+// Tile descriptors and output rows sit in LDS: the per-unit epilogue touches
+// no global memory but its stores.
 constexpr int kPsMaxSegs = 8;     // tiles one block may cover (checked on the host)
 constexpr int kPsHalfMax = 12;    // staging units per thread and LDS buffer (k-steps <= 24)
 constexpr int kPsSwiHalfMax = 4;  // the same for activations staged through the SwiGLU (k-steps <= 8)
