@@ -2563,15 +2563,20 @@ int persist_one(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hi
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return -1;
   Cfg& c = cfg[dev];
   if (c.device != dev || c.lds != lds) {
+    // a failed query leaves no error behind for the fallback kernel's launch check
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kPsMaxLds) != hipSuccess)
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kPsMaxLds) != hipSuccess) {
+      (void)hipGetLastError();
       return -1;
+    }
     int per_cu = 0, cus = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kStWaves * kWave, lds) !=
             hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        per_cu < 1 || cus < 1)
+        per_cu < 1 || cus < 1) {
+      (void)hipGetLastError();
       return -1;
+    }
     c = Cfg{dev, per_cu, cus, lds};
   }
   const int64_t grid = static_cast<int64_t>(c.cus) * c.blocks_per_cu;
