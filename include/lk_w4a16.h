@@ -140,11 +140,12 @@ LK_API int lk_w4a16_w2_combine(const uint16_t* activated, const int64_t* expert_
                         int64_t group_size, void* stream);
 
 /* ---- router logits: engine/klinear/router.py:50-51
- * logits fp32 [T,E] = fp32(x bf16 [T,H]) . fp32(w bf16 [E,H])^T, products exact,
+ * logits fp32 [T,E] = fp32(x bf16 [T,H]) . fp32(w [E,H])^T with the router
+ * weight w in bf16 (weight_f32 = 0; products exact) or fp32 (weight_f32 = 1);
  * fp32 sums in a fixed order (reruns bit-identical; not torch's order).
  * Requires H % 8 == 0 and H <= 4096. */
-LK_API int lk_router_logits(const uint16_t* x, const uint16_t* w, float* logits, int64_t tokens,
-                            int64_t experts, int64_t h, void* stream);
+LK_API int lk_router_logits(const uint16_t* x, const void* w, float* logits, int64_t tokens,
+                            int64_t experts, int64_t h, int weight_f32, void* stream);
 
 /* ---- router: engine/klinear/router.py:47-85 (on precomputed fp32 logits)
  * idx int64 [T,top_k] in descending choice score (sigmoid + bias), ties to the
@@ -249,8 +250,9 @@ LK_API int lk_w4a16_dense_gemm(const uint16_t* x, const uint8_t* packed, const u
                                int64_t group_size, void* stream);
 
 /* ---- fused QKV: engine/kernels/w4a16_fused_qkv.py:342-389
- * (q, k, v) bf16 [M,N] each = x . dequant(Wq|Wk|Wv)^T. M >= 16: one MFMA GEMM
- * launch over the three matrices; fewer rows: the decode GEMV per matrix. */
+ * (q, k, v) bf16 [M,N] each = x . dequant(Wq|Wk|Wv)^T, one launch: M >= 16 the
+ * MFMA GEMM over the three matrices; fewer rows the decode K-split GEMV over
+ * the three matrices' row blocks (the reference's K7, grid (3, N/64) at M=1). */
 LK_API int lk_w4a16_fused_qkv(const uint16_t* x, const uint8_t* q_packed,
                               const uint16_t* q_scales, const uint8_t* k_packed,
                               const uint16_t* k_scales, const uint8_t* v_packed,

@@ -35,7 +35,7 @@ SIGNATURES: dict[str, list] = {
     "lk_w4a16_w2_combine": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
     "lk_moe_router": [_P, _P, _P, _P, _I64, _I64, _I64, _F, _I, _P],
     "lk_moe_router_grouped": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _P],
-    "lk_router_logits": [_P, _P, _P, _I64, _I64, _I64, _P],
+    "lk_router_logits": [_P, _P, _P, _I64, _I64, _I64, _I, _P],
     "lk_w4a16_moe_gateup": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                             _I64, _I64, _I64, _I64, _I64, _F, _I, _I64, _P],
     "lk_w4a16_moe_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
@@ -73,6 +73,9 @@ SIGNATURES: dict[str, list] = {
                      _I, _P],
     "lk_kda_decode_layer": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                             _I64, _I64, _I64, _F, _F, _I, _I, _I, _I, _P],
+    "lk_rms_norm": [_P, _P, _P, _I64, _I64, _F, _I, _I, _P],
+    "lk_add_rms_norm": [_P, _P, _P, _P, _P, _I64, _I64, _F, _I, _I, _P],
+    "lk_rms_gated_norm": [_P, _P, _P, _P, _I64, _I64, _F, _I, _I, _I, _I, _P],
     "lk_probe_stream_read": [_P, _P, _I, _P, _P],
     "lk_probe_empty": [_P],
 }

@@ -47,6 +47,18 @@ int w2_combine_rows(const uint16_t* act, const int64_t* idx, int64_t idx_stride,
                     int64_t shared_id, const float* cw, int64_t cw_stride, const uint8_t* w2p,
                     const uint16_t* w2s, uint16_t* y, int64_t tokens, int64_t routes,
                     int64_t experts, int64_t h, int64_t inter, int64_t group, hipStream_t s);
+// Up to three W4A16 matrices of one shape [n, k] and their outputs [m, n].
+struct DenseMats {
+  const uint8_t* packed[3];
+  const uint16_t* scales[3];
+  uint16_t* y[3];
+};
+
+// y_z = x . W_z^T for z < count in one launch of the decode K-split GEMV
+// (w4a16_gemv.hip); the group size must already be checked.
+int dense_multi(const uint16_t* x, const DenseMats& mats, int count, int64_t m, int64_t n,
+                int64_t k, int64_t group_size, hipStream_t s, const char* name);
+
 // LK_OK when k > 0 and group is a positive multiple of 32 that divides k.
 int check_group(int64_t k, int64_t group);
 // check_group, and group is a power of two.

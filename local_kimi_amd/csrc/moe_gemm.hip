@@ -2558,10 +2558,17 @@ int persist_one(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hi
     int device = -1, blocks_per_cu = 0, cus = 0;
     size_t lds = 0;
   };
-  static Cfg cfg[16];  // per device; the attribute is per function
+  // per device (the attribute is per function); filled and read under one
+  // lock, so threads making their first calls at once see a whole entry
+  static Cfg cfg[16];
+  static std::mutex cfg_lock;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return -1;
-  Cfg& c = cfg[dev];
+  Cfg c;
+  {
+    std::lock_guard<std::mutex> hold(cfg_lock);
+    c = cfg[dev];
+  }
   if (c.device != dev || c.lds != lds) {
     // a failed query leaves no error behind for the fallback kernel's launch check
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -2578,8 +2585,11 @@ int persist_one(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hi
       return -1;
     }
     c = Cfg{dev, per_cu, cus, lds};
+    std::lock_guard<std::mutex> hold(cfg_lock);
+    cfg[dev] = c;
   }
   const int64_t grid = static_cast<int64_t>(c.cus) * c.blocks_per_cu;
+  if (grid <= 0) return -1;
   constexpr int NT = 1;  // 16-column units, as in the kernel
   const int64_t cgs = (SPLIT ? 2 : 1) * ((g.n + NT * 16 - 1) / (NT * 16));
   // a block's range covers at most (per - 1) / cgs + 2 tiles; its tables hold kPsMaxSegs
@@ -3091,11 +3101,10 @@ int lk_w4a16_fused_qkv(const uint16_t* x, const uint8_t* q_packed, const uint16_
   if (int rc = check_pow2_group(k, group_size)) return rc;
   if (m == 0) return LK_OK;
   LK_REQUIRE(x != nullptr, "null activation pointer");
-  if (m < 16) {  // decode rows: the GEMV path, one launch per projection
-    if (int rc = lk_w4a16_dense(x, q_packed, q_scales, q, m, n, k, group_size, stream)) return rc;
-    if (int rc = lk_w4a16_dense(x, k_packed, k_scales, k_out, m, n, k, group_size, stream))
-      return rc;
-    return lk_w4a16_dense(x, v_packed, v_scales, v, m, n, k, group_size, stream);
+  if (m < 16) {  // decode rows: one K-split GEMV launch over the three projections
+    const DenseMats mats{{q_packed, k_packed, v_packed}, {q_scales, k_scales, v_scales},
+                         {q, k_out, v}};
+    return dense_multi(x, mats, 3, m, n, k, group_size, as_stream(stream), "lk_w4a16_fused_qkv");
   }
   LK_REQUIRE(m < (1LL << 30), "too many rows");
   GemmArgs g{};

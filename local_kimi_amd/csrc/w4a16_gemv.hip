@@ -377,22 +377,26 @@ inline KGeom kgeom(int64_t k) {
   return g;
 }
 
-// dense: y[tok, n] for NTOK tokens per block (blockIdx.y = token block)
-template <int NR, int NTOK, int CI>
+// dense: y[tok, n] for NTOK tokens per block (blockIdx.y = token block); up
+// to three matrices of one shape in one launch (blockIdx.z picks the matrix:
+// the fused QKV projection at decode)
+template <int NR, int NTOK, int CI, bool MULTI>
 __global__ void __launch_bounds__(1024)
-dense_ksplit_kernel(const uint16_t* __restrict__ x, const uint8_t* __restrict__ packed,
-                    const uint16_t* __restrict__ scales, uint16_t* __restrict__ y, int64_t m,
-                    int64_t n, int64_t k, int64_t group) {
+dense_ksplit_kernel(const uint16_t* __restrict__ x, DenseMats mats, int64_t m, int64_t n,
+                    int64_t k, int64_t group) {
   __shared__ float red[kMaxKWaves][NR * NTOK * 8];
   const int kw = blockDim.x / kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const Shape sh = make_shape(k, group);
+  // one matrix: its pointers straight from the kernel arguments
+  const int z = MULTI ? static_cast<int>(blockIdx.z) : 0;
   const int64_t tok0 = static_cast<int64_t>(blockIdx.y) * NTOK;
   const int nt = static_cast<int>(min<int64_t>(NTOK, m - tok0));
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 8 * NR;
   const Rows<NR> rows(row0, n);
-  const uint8_t* const wp[1] = {packed};
-  const uint16_t* const ws[1] = {scales};
+  const uint8_t* const wp[1] = {mats.packed[z]};
+  const uint16_t* const ws[1] = {mats.scales[z]};
+  uint16_t* __restrict__ y = mats.y[z];
   KSplit<1, NR, NTOK, CI> ks;
   ks.load_x(x + tok0 * k, k, nt, wave, kw, sh.cpr);
   ks.load_w(wp, ws, rows, sh, wave, kw);
@@ -1045,20 +1049,39 @@ constexpr size_t kMaxLds = 64 * 1024;
 
 // ---------------------------------------------------------------------------
 // Router logits (engine/klinear/router.py:50-51): logits[t, e] =
-// sum_k fp32(x[t, k]) * fp32(w[e, k]) for bf16 x and router weight w (each
-// product is exact in fp32). One wave per (expert row, tile of up to
-// kLogitTokens tokens): lane l holds the 16-byte chunks l, l + 64, ... of the
-// expert's row (loaded once for the tile), and for each token of the tile
-// loads the same chunks of x, sums them in chunk order, then the wave reduces
-// in a fixed order (DPP within 8 lanes, then the 8 group sums in lane order).
-// Every output therefore has the same summation order whatever the batch
-// size, so a token's logits (and its routing) do not depend on the batch, and
-// reruns are bit-identical.
+// sum_k fp32(x[t, k]) * fp32(w[e, k]) for bf16 x and a bf16 or fp32 router
+// weight w (each product of a bf16 x with a bf16 w is exact in fp32). One wave
+// per (expert row, tile of up to kLogitTokens tokens): lane l holds the
+// 8-value chunks l, l + 64, ... of the expert's row (loaded once for the
+// tile: one 16-byte load per chunk for bf16, two for fp32), and for each
+// token of the tile loads the same chunks of x, sums them in chunk order, then
+// the wave reduces in a fixed order (DPP within 8 lanes, then the 8 group sums
+// in lane order). Every output therefore has the same summation order whatever
+// the batch size, so a token's logits (and its routing) do not depend on the
+// batch, and reruns are bit-identical.
 constexpr int kLogitWaves = 4;
 constexpr int kLogitIters = 8;   // chunks per lane: h <= 64 * 8 * 8 = 4096
 constexpr int kLogitTokens = 16;  // tokens per wave (the weight row is reused)
 
-__device__ inline float logit_dot(const uint4 (&xv)[kLogitIters], const uint4 (&wv)[kLogitIters],
+// WORDS = 16-byte loads per 8-value weight chunk: 1 (bf16) or 2 (fp32)
+template <int WORDS>
+struct LogitRow {
+  uint4 v[kLogitIters][WORDS];
+  // value j (0..7) of chunk i as fp32
+  __device__ inline float at(int i, int j) const {
+    if constexpr (WORDS == 1) {
+      const uint32_t b[4] = {v[i][0].x, v[i][0].y, v[i][0].z, v[i][0].w};
+      return bf16_to_f32((j & 1) ? (b[j >> 1] >> 16) : (b[j >> 1] & 0xFFFFu));
+    } else {
+      const uint4 q = v[i][j >> 2];
+      const uint32_t b[4] = {q.x, q.y, q.z, q.w};
+      return __uint_as_float(b[j & 3]);
+    }
+  }
+};
+
+template <int WORDS>
+__device__ inline float logit_dot(const uint4 (&xv)[kLogitIters], const LogitRow<WORDS>& wr,
                                   int lane, int64_t chunks) {
   // a chunk past the row keeps acc (a select, not a branch, so the loads
   // stay batched)
@@ -1067,12 +1090,11 @@ __device__ inline float logit_dot(const uint4 (&xv)[kLogitIters], const uint4 (&
   for (int i = 0; i < kLogitIters; ++i) {
     const bool ok = lane + kWave * i < chunks;
     const uint32_t a[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-    const uint32_t b[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
     float part = acc;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      part = fmaf(bf16_to_f32(a[j] & 0xFFFFu), bf16_to_f32(b[j] & 0xFFFFu), part);
-      part = fmaf(bf16_to_f32(a[j] >> 16), bf16_to_f32(b[j] >> 16), part);
+      part = fmaf(bf16_to_f32(a[j] & 0xFFFFu), wr.at(i, 2 * j), part);
+      part = fmaf(bf16_to_f32(a[j] >> 16), wr.at(i, 2 * j + 1), part);
     }
     acc = ok ? part : acc;
   }
@@ -1084,8 +1106,9 @@ __device__ inline float logit_dot(const uint4 (&xv)[kLogitIters], const uint4 (&
   return total;
 }
 
+template <int WORDS>
 __global__ void __launch_bounds__(kLogitWaves * 64)
-router_logits_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+router_logits_kernel(const uint16_t* __restrict__ x, const void* __restrict__ w,
                      float* __restrict__ logits, int64_t tokens, int64_t experts, int64_t h) {
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
@@ -1094,18 +1117,20 @@ router_logits_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict_
   if (e >= experts) return;  // wave-uniform
   const int64_t chunks = h / 8;
   const int nt = static_cast<int>(min<int64_t>(kLogitTokens, tokens - t0));
-  const uint4* wr = reinterpret_cast<const uint4*>(w + e * h);
-  uint4 wv[kLogitIters], xv[kLogitIters];
+  const uint4* wrow = reinterpret_cast<const uint4*>(w) + e * chunks * WORDS;
+  LogitRow<WORDS> wv;
+  uint4 xv[kLogitIters];
   const uint4* xr = reinterpret_cast<const uint4*>(x + t0 * h);
 #pragma unroll
   for (int i = 0; i < kLogitIters; ++i) {
     const int64_t c = lane + kWave * i;
     const int64_t cc = c < chunks ? c : 0;
     xv[i] = xr[cc];
-    wv[i] = wr[cc];
+#pragma unroll
+    for (int q = 0; q < WORDS; ++q) wv.v[i][q] = wrow[cc * WORDS + q];
   }
   for (int t = 0; t < nt; ++t) {
-    const float total = logit_dot(xv, wv, lane, chunks);
+    const float total = logit_dot<WORDS>(xv, wv, lane, chunks);
     if (t + 1 < nt) {  // the next token's chunks (wave-uniform)
       const uint4* xn = reinterpret_cast<const uint4*>(x + (t0 + t + 1) * h);
 #pragma unroll
@@ -1127,10 +1152,11 @@ extern "C" {
 
 constexpr int kNR = 2;  // weight rows per lane in the K-split kernels
 
-int lk_router_logits(const uint16_t* x, const uint16_t* w, float* logits, int64_t tokens,
-                     int64_t experts, int64_t h, void* stream) {
+int lk_router_logits(const uint16_t* x, const void* w, float* logits, int64_t tokens,
+                     int64_t experts, int64_t h, int weight_f32, void* stream) {
   LK_REQUIRE(w && logits, "null pointer argument");
   LK_REQUIRE(experts > 0 && h > 0 && tokens >= 0, "invalid router dimensions");
+  LK_REQUIRE(weight_f32 == 0 || weight_f32 == 1, "weight_f32 must be 0 (bf16) or 1 (fp32)");
   LK_REQUIRE(h % 8 == 0 && h <= 64 * 8 * kLogitIters,
              "router logits need hidden %% 8 == 0 and hidden <= %d, got %lld", 64 * 8 * kLogitIters,
              (long long)h);
@@ -1141,36 +1167,46 @@ int lk_router_logits(const uint16_t* x, const uint16_t* w, float* logits, int64_
   LK_REQUIRE(x != nullptr, "null activation pointer");
   dim3 grid(static_cast<unsigned>((experts + kLogitWaves - 1) / kLogitWaves),
             static_cast<unsigned>(token_tiles));
-  router_logits_kernel<<<grid, kLogitWaves * kWave, 0, as_stream(stream)>>>(x, w, logits, tokens,
-                                                                            experts, h);
+  if (weight_f32)
+    router_logits_kernel<2><<<grid, kLogitWaves * kWave, 0, as_stream(stream)>>>(x, w, logits, tokens,
+                                                                                experts, h);
+  else
+    router_logits_kernel<1><<<grid, kLogitWaves * kWave, 0, as_stream(stream)>>>(x, w, logits, tokens,
+                                                                                experts, h);
   return check_launch("lk_router_logits");
 }
 
-int lk_w4a16_dense(const uint16_t* x, const uint8_t* packed, const uint16_t* scales, uint16_t* y,
-                   int64_t m, int64_t n, int64_t k, int64_t group_size, void* stream) {
-  LK_REQUIRE(packed && scales && y, "null pointer argument");
-  LK_REQUIRE(m >= 0 && n > 0, "invalid dense dimensions m=%lld n=%lld", (long long)m,
-             (long long)n);
-  if (int rc = check_pow2_group(k, group_size)) return rc;
-  if (m == 0) return LK_OK;
-  LK_REQUIRE(x != nullptr, "null activation pointer");
-  hipStream_t s = as_stream(stream);
+}  // extern "C"
+
+namespace lk {
+
+// The K-split GEMV over `count` matrices of one shape in one launch (K <=
+// 8192), or one LDS-staged launch per matrix beyond that.
+int dense_multi(const uint16_t* x, const DenseMats& mats, int count, int64_t m, int64_t n,
+                int64_t k, int64_t group_size, hipStream_t s, const char* name) {
   const KGeom g = kgeom(k);
   const int ntok = m >= 4 ? 4 : m >= 2 ? 2 : 1;
   LK_REQUIRE((m + ntok - 1) / ntok <= 65535, "too many tokens for one call");
   if (g.ci <= 2) {
     dim3 grid(static_cast<unsigned>((n + 8 * kNR - 1) / (8 * kNR)),
-              static_cast<unsigned>((m + ntok - 1) / ntok));
+              static_cast<unsigned>((m + ntok - 1) / ntok), static_cast<unsigned>(count));
     const int threads = g.kw * kWave;
-#define LK_DENSE_KS(NT, CIV) \
-  dense_ksplit_kernel<kNR, NT, CIV><<<grid, threads, 0, s>>>(x, packed, scales, y, m, n, k, group_size)
+#define LK_DENSE_KS(NT, CIV)                                                                  \
+  do {                                                                                         \
+    if (count > 1)                                                                             \
+      dense_ksplit_kernel<kNR, NT, CIV, true><<<grid, threads, 0, s>>>(x, mats, m, n, k,        \
+                                                                       group_size);            \
+    else                                                                                       \
+      dense_ksplit_kernel<kNR, NT, CIV, false><<<grid, threads, 0, s>>>(x, mats, m, n, k,       \
+                                                                        group_size);           \
+  } while (0)
     if (g.ci == 1) {
       if (ntok == 1) LK_DENSE_KS(1, 1); else if (ntok == 2) LK_DENSE_KS(2, 1); else LK_DENSE_KS(4, 1);
     } else {
       if (ntok == 1) LK_DENSE_KS(1, 2); else if (ntok == 2) LK_DENSE_KS(2, 2); else LK_DENSE_KS(4, 2);
     }
 #undef LK_DENSE_KS
-    return check_launch("lk_w4a16_dense");
+    return check_launch(name);
   }
   // very wide reductions (K > 8192): LDS-staged kernel
   const int cpr = static_cast<int>(k / 32);
@@ -1182,17 +1218,42 @@ int lk_w4a16_dense(const uint16_t* x, const uint8_t* packed, const uint16_t* sca
             static_cast<unsigned>((m + nt2 - 1) / nt2));
   const size_t lds = stage_bytes(nt2, cpr);
   const int iters = pick_iters(cpr);
+  for (int z = 0; z < count; ++z) {
+    const uint8_t* packed = mats.packed[z];
+    const uint16_t* scales = mats.scales[z];
+    uint16_t* y = mats.y[z];
 #define LK_DENSE_LAUNCH(NT)                                                                 \
   LK_ITERS_CASES(iters, (dense_gemv_kernel<1, NT, IT><<<grid, nw * kWave, lds, s>>>(        \
                             x, packed, scales, y, m, n, k, group_size)))
-  switch (nt2) {
-    case 1: LK_DENSE_LAUNCH(1); break;
-    case 2: LK_DENSE_LAUNCH(2); break;
-    case 4: LK_DENSE_LAUNCH(4); break;
-    default: LK_DENSE_LAUNCH(8); break;
-  }
+    switch (nt2) {
+      case 1: LK_DENSE_LAUNCH(1); break;
+      case 2: LK_DENSE_LAUNCH(2); break;
+      case 4: LK_DENSE_LAUNCH(4); break;
+      default: LK_DENSE_LAUNCH(8); break;
+    }
 #undef LK_DENSE_LAUNCH
-  return check_launch("lk_w4a16_dense");
+    if (int rc = check_launch(name)) return rc;
+  }
+  return LK_OK;
+}
+
+}  // namespace lk
+
+extern "C" {
+
+int lk_w4a16_dense(const uint16_t* x, const uint8_t* packed, const uint16_t* scales, uint16_t* y,
+                   int64_t m, int64_t n, int64_t k, int64_t group_size, void* stream) {
+  LK_REQUIRE(packed && scales && y, "null pointer argument");
+  LK_REQUIRE(m >= 0 && n > 0, "invalid dense dimensions m=%lld n=%lld", (long long)m,
+             (long long)n);
+  if (int rc = check_pow2_group(k, group_size)) return rc;
+  if (m == 0) return LK_OK;
+  LK_REQUIRE(x != nullptr, "null activation pointer");
+  DenseMats mats{};
+  mats.packed[0] = packed;
+  mats.scales[0] = scales;
+  mats.y[0] = y;
+  return dense_multi(x, mats, 1, m, n, k, group_size, as_stream(stream), "lk_w4a16_dense");
 }
 
 static int grouped_common(const uint16_t* x, const int64_t* idx, const uint8_t* p0,

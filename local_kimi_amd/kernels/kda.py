@@ -271,7 +271,8 @@ def kda_decode_layer(q_in: torch.Tensor, k_in: torch.Tensor, v_in: torch.Tensor,
     """
     batch, channels = _validate_conv(q_in, k_in, v_in, q_state, k_state, v_state, q_weight,
                                      k_weight, v_weight)
-    _validate_gates(raw_decay, dt_bias, a_log, raw_beta, q_in, k_in, num_heads=num_heads,
+    ins = [_w._c(t) for t in (q_in, k_in, v_in)]  # strided projections (one fused buffer) are copied
+    _validate_gates(raw_decay, dt_bias, a_log, raw_beta, ins[0], ins[1], num_heads=num_heads,
                     head_dim=head_dim, eps=eps)
     if raw_decay.shape[:2] != (batch, 1):
         raise ValueError("raw_decay must hold one token per batch row")
@@ -290,7 +291,6 @@ def kda_decode_layer(q_in: torch.Tensor, k_in: torch.Tensor, v_in: torch.Tensor,
         weights = [w.float() for w in weights]
     wcode = _DTYPE_CODES[weights[0].dtype]
     weights = [_w._c(w) for w in weights]
-    ins = [_w._c(t) for t in (q_in, k_in, v_in)]
     conv_states = [q_state, k_state, v_state]
     conv_work = [s if s.is_contiguous() else s.contiguous() for s in conv_states]
     work = _dense(state)

@@ -134,16 +134,19 @@ def moe_router(logits: torch.Tensor, bias: torch.Tensor | None, top_k: int, *,
 def router_logits(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """``fp32(hidden) @ fp32(weight).T`` -> float32 ``[T, E]`` (router.py:50-51).
 
-    bf16 ``hidden [T, H]`` and bf16 ``weight [E, H]`` with ``H % 8 == 0`` and
-    ``H <= 4096``, on the GPU: one HIP launch for any token count. Products
-    are exact in fp32 and every logit is summed in the same fixed order
-    whatever the batch size, so a token's logits, and therefore its expert
-    selection, do not depend on how many tokens share the call.
+    bf16 ``hidden [T, H]`` with ``H % 8 == 0`` and ``H <= 4096``, and a router
+    ``weight [E, H]`` in bf16 or fp32 (fp16 is widened to fp32 first, which is
+    exact), on the GPU: one HIP launch for any token count. Every logit is
+    summed in the same fixed order whatever the batch size, so a token's
+    logits, and therefore its expert selection, do not depend on how many
+    tokens share the call.
     """
     if hidden.ndim != 2 or weight.ndim != 2 or hidden.shape[1] != weight.shape[1]:
         raise ValueError("router logits need hidden [T, H] and weight [E, H]")
-    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
-        raise TypeError("router logits need BF16 hidden states and a BF16 router weight")
+    if hidden.dtype != torch.bfloat16:
+        raise TypeError("router logits need BF16 hidden states")
+    if weight.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError("the router weight must be BF16, FP16 or FP32")
     if hidden.device != weight.device:
         raise ValueError("router inputs must share one device")
     if hidden.device.type != "cuda":
@@ -156,10 +159,12 @@ def router_logits(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     out = torch.empty((tokens, experts), dtype=torch.float32, device=hidden.device)
     if tokens == 0:
         return out
+    if weight.dtype == torch.float16:
+        weight = weight.float()
     x, w = _w._c(hidden), _w._c(weight)
     with torch.cuda.device(hidden.device):
         _lib.call("lk_router_logits", x.data_ptr(), w.data_ptr(), out.data_ptr(), tokens, experts, h,
-                  _w._stream(hidden.device))
+                  int(w.dtype == torch.float32), _w._stream(hidden.device))
     return out
 
 

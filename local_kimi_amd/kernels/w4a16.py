@@ -409,8 +409,9 @@ def _validate_qkv(activations, q_packed, q_scales, k_packed, k_scales, v_packed,
 def fused_qkv_w4a16(activations, q_packed, q_scales, k_packed, k_scales, v_packed, v_scales):
     """Q, K and V projections of one activation matrix -> ``(q, k, v)``.
 
-    From 16 rows one MFMA GEMM launch covers all three matrices; decode rows
-    run the GEMV once per matrix.
+    One launch either way: from 16 rows the MFMA GEMM over all three
+    matrices, for decode rows the K-split GEMV over the three matrices' row
+    blocks (the reference's one-launch K7, w4a16_fused_qkv.py:342-389).
     """
     _validate_qkv(activations, q_packed, q_scales, k_packed, k_scales, v_packed, v_scales)
     m, k = activations.shape

@@ -290,16 +290,21 @@ def _layer_inputs(rng, b, h, d, name):
     return ins, conv_states, conv_w, raw_decay, raw_beta, dt_bias, a_log, rec
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype,wdtype", [(torch.bfloat16, None), (torch.float16, None),
+                                           (torch.float32, None), (torch.bfloat16, torch.float32)])
 @pytest.mark.parametrize("b,h,d", [(1, 32, 128), (2, 4, 72), (3, 2, 8)])
-def test_layer_matches_the_oracle_chain(rng, dtype, b, h, d):
+def test_layer_matches_the_oracle_chain(rng, dtype, wdtype, b, h, d):
     """Convolutions (states bit-exact), gates and step against the oracle's
-    composition, within the step's single-step bound (3e-5)."""
+    composition, within the step's single-step bound (3e-5). Covers fp32
+    values (conv outputs not rounded) and fp32 conv weights with bf16 values."""
     from local_kimi_amd.kernels import kda_decode_layer
 
     name = _STORAGE[dtype]
     ins, conv_states, conv_w, raw_decay, raw_beta, dt_bias, a_log, rec = _layer_inputs(
         rng, b, h, d, name)
+    # weights of another dtype keep their bf16 values (stored as fp32), so the
+    # conv products stay exact and the bf16-rounded outputs stay comparable
+    wdtype = wdtype or dtype
     (qo, ko, vo), states_want = K.short_conv_triple(*ins, *conv_states, *conv_w, name)
     decay, beta, qn, kn = K.gates(raw_decay, dt_bias, a_log, raw_beta, qo, ko, h, d, 1e-6)
     want_state, want_out = K.decode_step(rec, qn[:, 0], kn[:, 0], vo.reshape(b, h, d),
@@ -307,7 +312,7 @@ def test_layer_matches_the_oracle_chain(rng, dtype, b, h, d):
     dev_states = [_t(s, dtype) for s in conv_states]
     st = _t(rec)
     out = kda_decode_layer(*(_t(x, dtype) for x in ins), *dev_states,
-                           *(_t(w, dtype) for w in conv_w), _t(raw_decay, dtype), _t(dt_bias),
+                           *(_t(w, wdtype) for w in conv_w), _t(raw_decay, dtype), _t(dt_bias),
                            _t(a_log), _t(raw_beta, dtype), st, num_heads=h, head_dim=d)
     for s, want in zip(dev_states, states_want):
         assert np.array_equal(_np(s), want)

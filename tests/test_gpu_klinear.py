@@ -90,6 +90,23 @@ def test_router_logits(rng, tokens, experts, h):
     assert torch.equal(got, router_logits(from_bits(x, DEV), from_bits(w, DEV)))
 
 
+@pytest.mark.parametrize("wdtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("tokens,experts,h", [(1, 256, 2304), (37, 24, 512), (3, 7, 8)])
+def test_router_logits_with_a_float_router_weight(rng, tokens, experts, h, wdtype):
+    """fp32 and fp16 router weights go through the same HIP launch (fp16
+    widened exactly); the fp32 products are rounded, so the bound is a few
+    fp32 ulps of the row's magnitude against a float64 sum."""
+    from local_kimi_amd.kernels import router_logits
+
+    x = random_bf16_bits(rng, (tokens, h))
+    w = torch.from_numpy(rng.normal(0, 0.05, (experts, h)).astype(np.float32)).to(wdtype)
+    got = router_logits(from_bits(x, DEV), w.to(DEV))
+    want = bf16_values(x).astype(np.float64) @ w.double().numpy().T
+    scale = np.abs(bf16_values(x)).astype(np.float64) @ np.abs(w.double().numpy()).T
+    assert np.all(np.abs(got.cpu().numpy() - want) <= 4e-6 * scale + 1e-30)
+    assert torch.equal(got, router_logits(from_bits(x, DEV), w.to(DEV)))
+
+
 def test_router_logits_do_not_depend_on_the_batch(rng):
     """Every token's logits are summed in the same order whatever the batch size
     (decode T=1, a 64-token tile boundary, a 300-token prefill)."""

@@ -141,6 +141,27 @@ def test_fused_qkv_matches_oracle(rng, monkeypatch, m, form):
         assert_close_bf16(to_bits(a), e, what=f"fused qkv {name} m={m}")
 
 
+@pytest.mark.parametrize("m", [1, 4, 15])
+def test_decode_fused_qkv_is_one_launch_at_the_kda_shape(rng, m):
+    """Decode rows at the KDA q/k/v shape, 3 x [4096, 2304] at G = 128: one
+    K-split launch over the three matrices, against the oracle and
+    bit-identical to three single dense GEMV calls (same kernel, same order)."""
+    import torch
+
+    from local_kimi_amd.kernels import fused_qkv_w4a16, w4a16_dense
+
+    n, k, g = 4096, 2304, 128
+    mats = [OW.quantise(random_bf16_bits(rng, (n, k), 0.02), g) for _ in range(3)]
+    x = random_bf16_bits(rng, (m, k))
+    flat = [a for pair in mats for a in pair]
+    dev = [_dev(a) for a in flat]
+    got = fused_qkv_w4a16(_dev(x), *dev)
+    want = OW.fused_qkv(x, *flat, g)
+    for j, name in enumerate("qkv"):
+        assert_close_bf16(to_bits(got[j]), want[j], what=f"decode fused qkv {name} m={m}")
+        assert torch.equal(got[j], w4a16_dense(_dev(x), dev[2 * j], dev[2 * j + 1]))
+
+
 @pytest.mark.parametrize("m,n,k", [(16, 256, 512), (100, 384, 1024), (130, 256, 2304),
                                    (2048, 512, 2304)])
 def test_direct_load_dense_forms_match_the_staged_forms(rng, m, n, k):
