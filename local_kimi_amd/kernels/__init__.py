@@ -18,6 +18,7 @@ raises on first call.
 
 from . import registry
 from .kda import fused_kda_gates, fused_short_conv_triple, kda_decode_layer, kda_decode_step
+from .norm import add_rms_norm, rms_gated_norm, rms_norm
 from .moe import (moe_router, moe_schedule, router_logits, shape_stable_expert_indices, w4a16_moe_block,
                   w4a16_moe_block_reference, w4a16_moe_decode, w4a16_moe_forward,
                   w4a16_moe_gateup, w4a16_moe_routed)
@@ -142,7 +143,7 @@ _register_mxfp4()
 
 __all__ = [
     "registry", "kda_decode_step", "kda_decode_layer", "fused_short_conv_triple",
-    "fused_kda_gates",
+    "fused_kda_gates", "rms_norm", "add_rms_norm", "rms_gated_norm",
     "W4A16_GROUPED", "W4A16_DENSE", "W4A16_SWIGLU", "W4A16_FUSED_QKV",
     "W4A16_W2_COMBINE", "W4A16_MOE_BLOCK", "moe_router", "router_logits",
     "shape_stable_expert_indices",

@@ -6,12 +6,17 @@
 * :class:`KLinearMoE` -- the grouped W4A16 route of ``KLinearMoE``
   (engine/klinear/moe.py:278-334) with the router of
   engine/klinear/router.py:47-85: ``logits = fp32(x) fp32(Wg)^T`` (one HIP
-  launch for bf16 router weights and decode batches, else torch's fp32 GEMM),
-  then the ``w4a16_moe_block`` op (selection, SwiGLU experts, W2, combine,
+  launch for every batch size; the router weight in bf16, fp16 or fp32), then the ``w4a16_moe_block`` op (selection, SwiGLU experts, W2, combine,
   shared expert with weight 1) over banks with the shared expert last.
 * :class:`MoEDecodeGraph` -- one MoE layer's decode step captured once in a
   HIP graph and replayed on a static input buffer, the counterpart of
   ``CUDAGraphDecodeRunner`` (engine/generate.py:226-306).
+* :class:`RMSNorm`, :class:`RMSGatedNorm` -- engine/klinear/norm.py:16-52 on
+  the HIP norm kernels (same constructor arguments and forward).
+* :class:`MoELayerTail` -- the post-attention half of ``KLinearDecoderLayer.
+  forward`` (engine/klinear/layer.py:155-170): residual add and
+  post_attention_layernorm in one launch, the MoE, and the second residual
+  add fused with the next layer's input_layernorm when one is given.
 """
 
 from __future__ import annotations
@@ -21,6 +26,7 @@ from torch import nn
 
 from .checkpoint import MoeBanks, W4A16Index, build_moe_banks
 from .kernels import W4A16_DENSE, W4A16_MOE_BLOCK, registry, router_logits
+from .kernels.norm import add_rms_norm, rms_gated_norm, rms_norm
 from .quant.w4a16 import W4A16Tensor
 
 HIDDEN = 2304         # Kimi-Linear hidden size (engine/klinear/config.py:42)
@@ -28,6 +34,36 @@ INTERMEDIATE = 1024   # moe_intermediate_size (config.py:62)
 ROUTED_EXPERTS = 256  # config.py:59-61
 TOP_K = 8             # config.py:60
 ROUTED_SCALING_FACTOR = 2.446  # config.py:67
+RMS_NORM_EPS = 1e-5   # config.py:49
+
+
+class RMSNorm(nn.Module):
+    """engine/klinear/norm.py:16-30 on ``lk_rms_norm``."""
+
+    def __init__(self, hidden_size: int, eps: float = 1e-6, *,
+                 device: torch.device | str | None = None, dtype: torch.dtype | None = None) -> None:
+        super().__init__()
+        self.variance_epsilon = eps
+        self.weight = nn.Parameter(torch.ones(hidden_size, device=device, dtype=dtype))
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        return rms_norm(hidden_states, self.weight.detach(), self.variance_epsilon)
+
+
+class RMSGatedNorm(nn.Module):
+    """engine/klinear/norm.py:33-52 on ``lk_rms_gated_norm``. ``input_dtype``
+    rounds the values first (fp32 KDA outputs to bf16, attention.py:324)."""
+
+    def __init__(self, hidden_size: int, eps: float = 1e-5, *,
+                 device: torch.device | str | None = None, dtype: torch.dtype | None = None) -> None:
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(hidden_size, device=device, dtype=dtype))
+
+    def forward(self, values: torch.Tensor, gate: torch.Tensor,
+                input_dtype: torch.dtype | None = None) -> torch.Tensor:
+        return rms_gated_norm(values, gate, self.weight.detach(), self.eps,
+                              input_dtype=input_dtype)
 
 
 class W4A16Linear(nn.Module):
@@ -84,8 +120,14 @@ class KLinearMoE(nn.Module):
             raise ValueError("num_experts must be divisible by num_expert_group")
         self.num_expert_group = num_expert_group
         self.topk_group = topk_group
-        # the router computes in fp32 (router.py:51) from the weight as stored
-        # (bf16 in the checkpoint layout, exact in fp32)
+        # the router computes in fp32 (router.py:51) from the weight as stored:
+        # bf16 in the checkpoint layout; fp16 is widened once here (exactly)
+        if gate_weight.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+            raise TypeError("the router weight must be BF16, FP16 or FP32")
+        if hidden % 8 or hidden > 4096:
+            raise ValueError(f"the HIP router needs hidden % 8 == 0 and hidden <= 4096, got {hidden}")
+        if gate_weight.dtype == torch.float16:
+            gate_weight = gate_weight.float()
         self.register_buffer("gate_weight", gate_weight.contiguous(), persistent=False)
         bias = None if e_score_correction_bias is None else e_score_correction_bias.float().contiguous()
         self.register_buffer("e_score_correction_bias", bias, persistent=False)
@@ -150,3 +192,27 @@ class MoEDecodeGraph:
         self.static_input.copy_(hidden_states)
         self.graph.replay()
         return self.static_output
+
+
+class MoELayerTail(nn.Module):
+    """The post-attention half of a MoE decoder layer (engine/klinear/layer.py:155-170).
+
+    ``forward(residual, attended)`` returns ``hidden = (residual + attended) +
+    moe(post_attention_layernorm(residual + attended))``. With ``next_norm``
+    (the following layer's input_layernorm) the final residual add runs fused
+    with that norm and ``(hidden, next_norm(hidden))`` is returned.
+    """
+
+    def __init__(self, moe: KLinearMoE, post_attention_layernorm: RMSNorm) -> None:
+        super().__init__()
+        self.moe = moe
+        self.post_attention_layernorm = post_attention_layernorm
+
+    def forward(self, residual: torch.Tensor, attended: torch.Tensor,
+                next_norm: RMSNorm | None = None):
+        ln = self.post_attention_layernorm
+        hidden, ff_in = add_rms_norm(residual, attended, ln.weight.detach(), ln.variance_epsilon)
+        ff = self.moe(ff_in)
+        if next_norm is None:
+            return hidden + ff
+        return add_rms_norm(hidden, ff, next_norm.weight.detach(), next_norm.variance_epsilon)

@@ -116,3 +116,26 @@ def test_kda_ops_validate_like_the_reference_before_any_launch():
         fused_kda_gates(rd, torch.zeros(8), torch.zeros((1, 1, 2, 1)), torch.zeros((1, 1, 2)),
                         torch.zeros((1, 1, 8)), torch.zeros((1, 1, 8)), num_heads=2,
                         head_dim=4, eps=1e-6)
+
+
+def test_norm_wrappers_refuse_bad_inputs_before_any_launch():
+    from local_kimi_amd.kernels import add_rms_norm, rms_gated_norm, rms_norm
+
+    x = torch.zeros((2, 16), dtype=torch.bfloat16)
+    w = torch.ones(16, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="shape \\[16\\]"):
+        rms_norm(x, torch.ones(8, dtype=torch.bfloat16), 1e-6)
+    with pytest.raises(ValueError, match="multiple of 8"):
+        rms_norm(torch.zeros((2, 12), dtype=torch.bfloat16), torch.ones(12, dtype=torch.bfloat16), 1e-6)
+    with pytest.raises(TypeError, match="float32, float16 or bfloat16"):
+        rms_norm(x.to(torch.int32), w, 1e-6)
+    with pytest.raises(ValueError, match="require CUDA"):
+        rms_norm(x, w, 1e-6)
+    with pytest.raises(TypeError, match="share one dtype"):
+        add_rms_norm(x, x.float(), w, 1e-6)
+    with pytest.raises(ValueError, match="same shape"):
+        add_rms_norm(x, x[:1], w, 1e-6)
+    with pytest.raises(ValueError, match="same shape"):
+        rms_gated_norm(x, x[:, :8], w, 1e-5)
+    with pytest.raises(TypeError, match="input_dtype"):
+        rms_gated_norm(x, x, w, 1e-5, input_dtype=torch.int8)
