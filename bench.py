@@ -9,10 +9,10 @@ quantised at group 128 on the GPU). A step is router + gate/up + SwiGLU + W2
 + weighted combine + shared expert for one token. 26 distinct layer banks
 (24.4 GB) rotate so every step reads its weights from HBM, not from the
 256 MB MALL; the steps of one rotation are captured in a HIP graph and
-replayed; inputs are resident in HBM before the timed region. At least 104
-steps (four rotations) are timed after at least 10 warm-up steps, whatever
-``--steps`` / ``--warmup`` ask; both the requested and the timed counts are
-printed.
+replayed; inputs are resident in HBM before the timed region. Exactly
+``--steps`` steps are timed (520 by default, 20 rotations, captured as one
+graph) after exactly ``--warmup`` warm-up steps (52 by default), for every
+workload of the line.
 
 The line also carries ``configs``: the other four workload shapes, each timed
 the same way and each with its own ``roofline`` and ``cpu_baseline``:
@@ -54,7 +54,8 @@ sys.path.insert(0, ROOT)
 H, E_ROUTED, INTER, TOP_K, G, SCALING = 2304, 256, 1024, 8, 128, 2.446
 DENSE_N, QKV_N, PREFILL_TOKENS = 9216, 4096, 2048
 LAYERS, DENSE_COPIES = 26, 40
-MIN_TIMED_STEPS, MIN_WARMUP_STEPS = 104, 10
+MIN_TIMED_STEPS, MIN_WARMUP_STEPS = 104, 10  # below these the timing is noisier (a warning)
+DEFAULT_STEPS, DEFAULT_WARMUP = 520, 52
 
 HBM_PEAK_GBPS = 8000.0        # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0     # dense bf16 MFMA
@@ -87,16 +88,14 @@ EXPERT_FLOPS = 2 * 3 * INTER * H                                           # per
 
 
 class Plan:
-    """Warm-up and timed step counts: at least MIN_WARMUP_STEPS / MIN_TIMED_STEPS,
-    rounded up to whole replays of a graph of `per_graph` steps."""
+    """Exactly `steps` timed steps after exactly `warmup` warm-up steps, for
+    every workload (the defaults, 520 and 52, are whole rotations of the
+    26-layer banks)."""
 
     def __init__(self, steps: int, warmup: int):
-        self.steps_requested, self.warmup_requested = steps, warmup
-
-    def replays(self, per_graph: int) -> tuple[int, int]:
-        warm = math.ceil(max(self.warmup_requested, MIN_WARMUP_STEPS) / per_graph)
-        timed = math.ceil(max(self.steps_requested, MIN_TIMED_STEPS) / per_graph)
-        return warm, timed
+        if steps < 1 or warmup < 0:
+            raise ValueError("--steps must be at least 1 and --warmup at least 0")
+        self.steps, self.warmup = steps, warmup
 
 
 def capture(fn, stream: torch.cuda.Stream) -> torch.cuda.CUDAGraph:
@@ -110,24 +109,42 @@ def capture(fn, stream: torch.cuda.Stream) -> torch.cuda.CUDAGraph:
     return graph
 
 
-def time_graph(graph, stream, per_graph: int, plan: Plan) -> dict:
-    """Replay warm-ups, then time whole replays with HIP events recorded on the
-    replay stream; returns µs per step and the step counts."""
-    warm, timed = plan.replays(per_graph)
-    with torch.cuda.stream(stream):
-        for _ in range(warm):
-            graph.replay()
+def time_steps(step, count: int, stream, plan: Plan) -> dict:
+    """Time `plan.steps` steps of a rotation of `count` distinct steps.
+
+    `step(i)` enqueues step i (0 <= i < count). The timed steps are captured as
+    one HIP graph that cycles through the rotation (as a decode step captures
+    all of its layers in one graph), so the region holds exactly the timed
+    steps and one graph launch. Warm-ups run first; the last of them (up to
+    one rotation, taken from the end of the rotation, so the timed steps,
+    which start at step 0, still read their weights from HBM) are enqueued
+    back to back with the start event, keeping the GPU busy while the host
+    enqueues the timed graph. The events are recorded on the replay stream."""
+    lead = min(plan.warmup, count)
+
+    def span(first: int, n: int):
+        return capture(lambda: [step((first + i) % count) for i in range(n)], stream)
+
+    early = span(0, plan.warmup - lead) if plan.warmup > lead else None
+    led = span(count - lead, lead) if lead else None
+    timed = span(0, plan.steps)
+
+    if early is not None:
+        with torch.cuda.stream(stream):
+            early.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
+        if led is None:
+            torch.cuda._sleep(2_000_000)  # no warm-up steps: a spin kernel covers the enqueue
+        else:
+            led.replay()
         start.record(stream)
-        for _ in range(timed):
-            graph.replay()
+        timed.replay()
         end.record(stream)
     torch.cuda.synchronize()
     ms = start.elapsed_time(end)
-    steps = timed * per_graph
-    return {"us": ms * 1000.0 / steps, "steps": steps, "warmup": warm * per_graph,
+    return {"us": ms * 1000.0 / plan.steps, "steps": plan.steps, "warmup": plan.warmup,
             "ms_total": ms}
 
 
@@ -309,16 +326,18 @@ def run_moe_decode(plan: Plan, dev, banks, cpu: bool) -> dict:
     logits = [torch.randn((1, E_ROUTED), device=dev, generator=gen) for _ in range(LAYERS)]
     stream = torch.cuda.Stream(device=dev)
 
-    def block_all():
-        for l in range(LAYERS):
-            w4a16_moe_block(xs[l], logits[l], None, *banks[l], TOP_K, SCALING)
+    def block(l):
+        w4a16_moe_block(xs[l], logits[l], None, *banks[l], TOP_K, SCALING)
 
-    def gateup_all():
-        for l in range(LAYERS):
-            w4a16_moe_gateup(xs[l], logits[l], None, *banks[l][:4], TOP_K, SCALING)
+    def gateup(l):
+        w4a16_moe_gateup(xs[l], logits[l], None, *banks[l][:4], TOP_K, SCALING)
 
-    blk = time_graph(capture(block_all, stream), stream, LAYERS, plan)
-    gu = time_graph(capture(gateup_all, stream), stream, LAYERS, plan)
+    blk = time_steps(block, LAYERS, stream, plan)
+    gu = time_steps(gateup, LAYERS, stream, plan)
+    # a short timed region carries the fixed cost of its graph launch and
+    # completion (about 10 us); the steady-state rate beside it, at the default count
+    steady = blk if plan.steps >= DEFAULT_STEPS else time_steps(block, LAYERS, stream,
+                                                                 Plan(DEFAULT_STEPS, plan.warmup))
     step_bytes = (TOP_K + 1) * EXPERT_BYTES + TOKEN_IO_BYTES
     gu_bytes = (TOP_K + 1) * GATEUP_EXPERT_BYTES + H * 2 + E_ROUTED * 4 + (TOP_K + 1) * INTER * 2
     traffic = measured_traffic("moe_gateup_ksplit_kernel")
@@ -329,6 +348,7 @@ def run_moe_decode(plan: Plan, dev, banks, cpu: bool) -> dict:
         "achieved_gbps": round(step_bytes / (blk["us"] * 1e3), 1),
         "pct_hbm_peak": round(100.0 * step_bytes / (blk["us"] * 1e3) / HBM_PEAK_GBPS, 2),
         "algorithmic_bytes_per_step": step_bytes,
+        "us_per_token_at_520_steps": round(steady["us"], 3),
         "roofline": {"kernel": "moe_gateup_ksplit_kernel (router + gate/up + SwiGLU, 9 routes)",
                      "bound": "hbm", "achieved": round(gu_bytes / (gu["us"] * 1e3), 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -354,11 +374,7 @@ def run_dense(plan: Plan, dev, cpu: bool) -> dict:
     x = torch.randn((1, H), device=dev, generator=gen).to(torch.bfloat16)
     stream = torch.cuda.Stream(device=dev)
 
-    def all_copies():
-        for p, s in weights:
-            w4a16_dense(x, p, s)
-
-    t = time_graph(capture(all_copies, stream), stream, DENSE_COPIES, plan)
+    t = time_steps(lambda i: w4a16_dense(x, *weights[i]), DENSE_COPIES, stream, plan)
     nbytes = w4a16_bytes(DENSE_N, H) + H * 2 + DENSE_N * 2
     log(f"[bench] config 1: dense GEMV {t['us']:.2f} us")
     res = {
@@ -402,11 +418,8 @@ def run_moe_batched(plan: Plan, dev, banks, m: int, weights: str, cpu: bool) -> 
     unions = [int(torch.unique(cpu_router(lg.cpu())[0]).numel()) for lg in logits]
     stream = torch.cuda.Stream(device=dev)
 
-    def all_layers():
-        for l in range(LAYERS):
-            block(xs[l], logits[l], None, *banks[l], TOP_K, SCALING)
-
-    t = time_graph(capture(all_layers, stream), stream, LAYERS, plan)
+    t = time_steps(lambda l: block(xs[l], logits[l], None, *banks[l], TOP_K, SCALING), LAYERS,
+                   stream, plan)
     ebytes = MX_EXPERT_BYTES if weights == "mxfp4" else EXPERT_BYTES
     step_bytes = float(np.mean([(u + 1) * ebytes for u in unions])) + m * TOKEN_IO_BYTES
     gbps = step_bytes / (t["us"] * 1e3)
@@ -441,11 +454,8 @@ def run_moe_prefill(plan: Plan, dev, banks, weights: str, cpu: bool) -> dict:
     logits = [torch.randn((m, E_ROUTED), device=dev, generator=gen) for _ in range(layers)]
     stream = torch.cuda.Stream(device=dev)
 
-    def some_layers():
-        for l in range(layers):
-            block(xs[l], logits[l], None, *banks[l], TOP_K, SCALING)
-
-    t = time_graph(capture(some_layers, stream), stream, layers, plan)
+    t = time_steps(lambda l: block(xs[l], logits[l], None, *banks[l], TOP_K, SCALING), layers,
+                   stream, plan)
     ebytes = MX_EXPERT_BYTES if weights == "mxfp4" else EXPERT_BYTES
     nbytes = (E_ROUTED + 1) * ebytes + m * TOKEN_IO_BYTES
     flops = m * (TOP_K + 1) * EXPERT_FLOPS
@@ -492,11 +502,7 @@ def run_qkv_prefill(plan: Plan, dev, cpu: bool) -> dict:
     x = torch.randn((m, H), device=dev, generator=gen).to(torch.bfloat16)
     stream = torch.cuda.Stream(device=dev)
 
-    def all_sets():
-        for s in sets:
-            fused_qkv_w4a16(x, *s)
-
-    t = time_graph(capture(all_sets, stream), stream, copies, plan)
+    t = time_steps(lambda i: fused_qkv_w4a16(x, *sets[i]), copies, stream, plan)
     flops = 2 * m * H * 3 * n
     tflops = flops / (t["us"] * 1e6)
     log(f"[bench] fused QKV: {t['us']:.1f} us ({tflops:.0f} TFLOP/s)")
@@ -529,6 +535,185 @@ def run_qkv_prefill(plan: Plan, dev, cpu: bool) -> dict:
     return res
 
 
+# the reference's published isolated decode figures (L40S, G = 32,
+# engine/kernels/RESULTS.md:37-40): context for the same shapes here, on other
+# hardware and another group size, so never a vs_baseline ratio
+REFERENCE_L40S_US = {"gate_9_routes": 29.7, "w2_9_routes": 30.1, "dense_4096x2304": 55.3,
+                     "dense_2304x4096": 62.8}
+
+
+def _decode_entry(name, t, nbytes, kernel, config, cpu_fn, cpu_sample, cpu):
+    t_us = t["us"]
+    gbps = nbytes / (t_us * 1e3)
+    res = {
+        "metric": f"{name} decode us/call + HBM GB/s at W4A16", "value": round(t_us, 3),
+        "unit": "us/call", "steps": t["steps"], "warmup": t["warmup"], "config": config,
+        "roofline": {"kernel": kernel, "bound": "hbm", "achieved": round(gbps, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": measured_traffic(f"{kernel} ({config['workload']})"),
+                     "bytes_per_launch": nbytes, "avg_launch_us": round(t_us, 3)},
+    }
+    if cpu:
+        threads = cpu_threads()
+        sec = cpu_median(cpu_fn)
+        res["cpu_baseline"] = {"value": round(sec * 1e6, 1), "unit": "us/call", "cores": threads,
+                               "kind": "port", "cpu_model": cpu_model(), "sample": cpu_sample}
+    return res
+
+
+def run_decode_shapes(plan: Plan, dev, banks, cpu: bool) -> dict:
+    """The isolated decode projections whose times the reference publishes
+    (engine/kernels/RESULTS.md:37-40): gate alone over 9 routes (N = 1024, K =
+    2304), W2 over 9 routes (N = 2304, K = 1024; x [9, 1024], one route per
+    row, as moe.py:317-326 calls it), dense N = 4096 x K = 2304 (a KDA q/k/v
+    projection) and dense N = 2304 x K = 4096 (o_proj); each call timed alone
+    in a graph of calls that rotate the 26 layer banks or 60 dense copies, so
+    every call reads HBM."""
+    from local_kimi_amd.kernels import grouped_w4a16_gemv, w4a16_dense
+    from local_kimi_amd.quant import quantise
+
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(20260737)
+    rng = np.random.default_rng(20260737)
+    stream = torch.cuda.Stream(device=dev)
+    idx = [torch.tensor(np.append(rng.choice(E_ROUTED, TOP_K, replace=False), E_ROUTED)[None],
+                        dtype=torch.int64, device=dev) for _ in range(LAYERS)]
+    x = torch.randn((1, H), device=dev, generator=gen).to(torch.bfloat16)
+    act = (torch.randn((TOP_K + 1, INTER), device=dev, generator=gen) * 0.1).to(torch.bfloat16)
+    w2_idx = [i.reshape(TOP_K + 1, 1).contiguous() for i in idx]
+    per_route = w4a16_bytes(INTER, H)
+    host = [t.cpu() for t in banks[0]]
+    hidx = idx[0].cpu()[0]
+
+    t = time_steps(lambda l: grouped_w4a16_gemv(x, idx[l], banks[l][0], banks[l][1]), LAYERS,
+                   stream, plan)
+    out["gate_9_routes"] = _decode_entry(
+        "Grouped gate projection (9 routes)", t,
+        (TOP_K + 1) * per_route + H * 2 + (TOP_K + 1) * INTER * 2, "grouped_ksplit_kernel",
+        {"workload": "grouped_gate_decode_9_routes", "n": INTER, "k": H, "routes": TOP_K + 1,
+         "group_size": G, "reference_l40s_g32_us": REFERENCE_L40S_US["gate_9_routes"]},
+        lambda: [cpu_linear(x.cpu(), cpu_dequant_w4a16(host[0][e], host[1][e])) for e in hidx],
+        "torch restatement: 9 x (dequantise W1[e] to bf16 + F.linear fp32), median of 10", cpu)
+    t = time_steps(lambda l: grouped_w4a16_gemv(act, w2_idx[l], banks[l][4], banks[l][5]),
+                   LAYERS, stream, plan)
+    out["w2_9_routes"] = _decode_entry(
+        "Grouped W2 projection (9 routes)", t,
+        (TOP_K + 1) * w4a16_bytes(H, INTER) + (TOP_K + 1) * (INTER + H) * 2,
+        "grouped_ksplit_kernel",
+        {"workload": "grouped_w2_decode_9_routes", "n": H, "k": INTER, "routes": TOP_K + 1,
+         "group_size": G, "reference_l40s_g32_us": REFERENCE_L40S_US["w2_9_routes"]},
+        lambda: [cpu_linear(act.cpu()[r:r + 1], cpu_dequant_w4a16(host[4][e], host[5][e]))
+                 for r, e in enumerate(hidx)],
+        "torch restatement: 9 x (dequantise W2[e] to bf16 + F.linear fp32), median of 10", cpu)
+    for n, k in ((4096, H), (H, 4096)):
+        enc = quantise((torch.randn((n, k), device=dev, generator=gen) * 0.02).to(torch.bfloat16),
+                       group_size=G)
+        copies = [(enc.packed.clone(), enc.scales.clone()) for _ in range(60)]
+        xk = torch.randn((1, k), device=dev, generator=gen).to(torch.bfloat16)
+        t = time_steps(lambda i: w4a16_dense(xk, *copies[i]), len(copies), stream, plan)
+        key = f"dense_{n}x{k}"
+        hp, hs, hx = enc.packed.cpu(), enc.scales.cpu(), xk.cpu()
+        out[key] = _decode_entry(
+            f"Dense GEMV N={n} K={k}", t, w4a16_bytes(n, k) + k * 2 + n * 2,
+            "dense_ksplit_kernel",
+            {"workload": f"dense_gemv_decode_{n}x{k}", "m": 1, "n": n, "k": k, "group_size": G,
+             "weight_copies_rotated": len(copies), "reference_l40s_g32_us": REFERENCE_L40S_US[key]},
+            lambda: cpu_linear(hx, cpu_dequant_w4a16(hp, hs)),
+            f"torch restatement: dequantise W [{n}, {k}] to bf16 + F.linear fp32, median of 10",
+            cpu)
+        del copies
+    log("[bench] decode shapes: " + ", ".join(f"{k} {v['value']:.2f} us" for k, v in out.items()))
+    return out
+
+
+def run_qkv_decode(plan: Plan, dev, cpu: bool) -> dict:
+    """Fused QKV at decode: x [1, 2304] . 3 x [4096, 2304] at W4A16 G = 128, one
+    launch; 20 weight sets (292 MB) rotated."""
+    from local_kimi_amd.kernels import fused_qkv_w4a16
+    from local_kimi_amd.quant import quantise
+
+    n, copies = QKV_N, 20
+    gen = torch.Generator(device=dev).manual_seed(20260738)
+    mats = []
+    for _ in range(3):
+        enc = quantise((torch.randn((n, H), device=dev, generator=gen) * 0.02).to(torch.bfloat16),
+                       group_size=G)
+        mats += [enc.packed, enc.scales]
+    sets = [mats] + [[t.clone() for t in mats] for _ in range(copies - 1)]
+    x = torch.randn((1, H), device=dev, generator=gen).to(torch.bfloat16)
+    stream = torch.cuda.Stream(device=dev)
+    t = time_steps(lambda i: fused_qkv_w4a16(x, *sets[i]), copies, stream, plan)
+    host = [a.cpu() for a in mats]
+    hx = x.cpu()
+    log(f"[bench] fused QKV decode: {t['us']:.2f} us")
+    res = _decode_entry(
+        "Fused QKV (one launch)", t, 3 * w4a16_bytes(n, H) + H * 2 + 3 * n * 2,
+        "dense_ksplit_kernel",
+        {"workload": "qkv_decode", "m": 1, "n_per_projection": n, "k": H, "group_size": G,
+         "weight_sets_rotated": copies, "launches": 1},
+        lambda: [cpu_linear(hx, cpu_dequant_w4a16(host[2 * j], host[2 * j + 1])) for j in range(3)],
+        "torch restatement: dequantise the three [4096, 2304] matrices + F.linear fp32, "
+        "median of 10", cpu)
+    return res
+
+
+def run_norm_decode(plan: Plan, dev, cpu: bool) -> dict:
+    """The decode norms (next 4): the residual add + RMSNorm of one token's
+    hidden state (hidden 2304), the gated RMSNorm of one KDA output (32 heads
+    of 128, fp32 values rounded to bf16 in the same launch), and the residual
+    add + RMSNorm of a 2048-token prefill (HBM-bound: 37.7 MB moved)."""
+    from local_kimi_amd.kernels import add_rms_norm, rms_gated_norm
+
+    gen = torch.Generator(device=dev).manual_seed(20260739)
+    stream = torch.cuda.Stream(device=dev)
+    bf = torch.bfloat16
+
+    def rnd(shape, dtype=bf, std=1.0):
+        return (torch.randn(shape, device=dev, generator=gen) * std).to(dtype)
+
+    w = (1 + rnd((H,), torch.float32, 0.1)).to(bf)
+    gw = (1 + rnd((128,), torch.float32, 0.1)).to(bf)
+    tok = [(rnd((1, H)), rnd((1, H))) for _ in range(LAYERS)]
+    kda = [(rnd((1, 32, 128), torch.float32), rnd((1, 32, 128))) for _ in range(LAYERS)]
+    pre = [(rnd((PREFILL_TOKENS, H)), rnd((PREFILL_TOKENS, H))) for _ in range(8)]
+    t_add = time_steps(lambda l: add_rms_norm(*tok[l], w, 1e-5), LAYERS, stream, plan)
+    t_gated = time_steps(lambda l: rms_gated_norm(*kda[l], gw, 1e-5, input_dtype=bf), LAYERS,
+                         stream, plan)
+    t_pre = time_steps(lambda l: add_rms_norm(*pre[l], w, 1e-5), len(pre), stream, plan)
+    pre_bytes = 4 * PREFILL_TOKENS * H * 2 + H * 2
+    gbps = pre_bytes / (t_pre["us"] * 1e3)
+    log(f"[bench] norms: add+rmsnorm {t_add['us']:.2f} us, gated {t_gated['us']:.2f} us, "
+        f"prefill add+rmsnorm {t_pre['us']:.2f} us ({gbps:.0f} GB/s)")
+    res = {
+        "metric": "Decode add + RMSNorm us/call (hidden 2304, batch 1)",
+        "value": round(t_add["us"], 3), "unit": "us/call", "steps": t_add["steps"],
+        "warmup": t_add["warmup"], "higher_is_better": False,
+        "config": {"workload": "norm_decode", "hidden": H, "launches": 1},
+        "gated_norm_us": round(t_gated["us"], 3),
+        "prefill_add_rms_norm_us": round(t_pre["us"], 3),
+        "roofline": {"kernel": "norm_kernel (add + RMSNorm, 2048 x 2304 prefill rows)",
+                     "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_launch": pre_bytes, "avg_launch_us": round(t_pre["us"], 3)},
+    }
+    if cpu:
+        threads = cpu_threads()
+        r, d = (a.cpu() for a in tok[0])
+        wh = w.cpu()
+
+        def cpu_add_norm():
+            hidden = r + d
+            v = hidden.float()
+            return hidden, wh * (v * torch.rsqrt(v.square().mean(-1, keepdim=True) + 1e-5)).to(bf)
+
+        sec = cpu_median(cpu_add_norm)
+        res["cpu_baseline"] = {"value": round(sec * 1e6, 1), "unit": "us/call", "cores": threads,
+                               "kind": "port", "cpu_model": cpu_model(),
+                               "sample": "torch restatement of layer.py:156-160 on one token "
+                                         "(bf16 add, rms_norm), median of 10"}
+    return res
+
+
 def run_floor(plan: Plan, dev, banks) -> dict:
     """Memory floors: empty-kernel launches, a streaming read of one dense
     weight (11 MB), of one batch-1 MoE layer's 27 matrices (33 MB), and of
@@ -547,8 +732,7 @@ def run_floor(plan: Plan, dev, banks) -> dict:
         sizes = (ctypes.c_int64 * len(regions))(*[r.numel() * r.element_size() for r in regions])
         _lib.call("lk_probe_stream_read", ptrs, sizes, len(regions), sink.data_ptr(), s_ptr)
 
-    empty = time_graph(capture(lambda: [lib.lk_probe_empty(s_ptr) for _ in range(100)], stream),
-                       stream, 100, plan)
+    empty = time_steps(lambda i: lib.lk_probe_empty(s_ptr), 100, stream, plan)
     # one MoE layer's matrices: 9 experts x (gate, up, down) packed weights + scales, per layer
     rng = np.random.default_rng(5)
     layer_sets = []
@@ -560,11 +744,10 @@ def run_floor(plan: Plan, dev, banks) -> dict:
                 regions.append(banks[l][j][e])
         layer_sets.append(regions)  # 27 packed matrices (scales are 3 % more)
     layer_bytes = sum(r.numel() for r in layer_sets[0])
-    moe = time_graph(capture(lambda: [probe(r) for r in layer_sets], stream), stream, LAYERS, plan)
+    moe = time_steps(lambda l: probe(layer_sets[l]), LAYERS, stream, plan)
     dense = [torch.empty(w4a16_bytes(DENSE_N, H), dtype=torch.uint8, device=dev).fill_(3)
              for _ in range(DENSE_COPIES)]
-    den = time_graph(capture(lambda: [probe([d]) for d in dense], stream), stream,
-                     DENSE_COPIES, plan)
+    den = time_steps(lambda i: probe([dense[i]]), DENSE_COPIES, stream, plan)
     d_bytes = dense[0].numel()
     del dense
     gateup = {}
@@ -574,7 +757,7 @@ def run_floor(plan: Plan, dev, banks) -> dict:
                   for _ in range(LAYERS)]
         nbytes = int(np.mean(unions) + 1) * (EXPERT_BYTES * 2 // 3) // 16 * 16
         bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3) for _ in range(4)]
-        t = time_graph(capture(lambda: [probe([b]) for b in bufs], stream), stream, 4, plan)
+        t = time_steps(lambda i: probe([bufs[i]]), 4, stream, plan)
         gateup[m] = (nbytes, t["us"])
         del bufs
     log(f"[bench] floor: empty {empty['us']:.2f} us, 11 MB {den['us']:.2f} us, "
@@ -626,8 +809,7 @@ def run_copy(dev) -> dict:
 def headline(plan: Plan, res: dict) -> dict:
     out = {
         "metric": METRIC, "value": res["value"], "unit": "us/token", "n_gpus": 1,
-        "steps": res["steps"], "warmup": res["warmup"], "steps_requested": plan.steps_requested,
-        "warmup_requested": plan.warmup_requested, "ms_per_step": res["ms_per_step"],
+        "steps": res["steps"], "warmup": res["warmup"], "ms_per_step": res["ms_per_step"],
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: N(0,0.02) weights quantised W4A16 g128 on the GPU, N(0,1) x and logits",
         "config": {"workload": "moe_decode_batch1", "hidden": H, "routed_experts": E_ROUTED,
@@ -635,8 +817,8 @@ def headline(plan: Plan, res: dict) -> dict:
                    "group_size": G, "tokens_per_step": 1, "layer_banks_rotated": LAYERS,
                    "launches_per_step": 2},
     }
-    for key in ("achieved_gbps", "pct_hbm_peak", "algorithmic_bytes_per_step", "roofline",
-                "cpu_baseline"):
+    for key in ("achieved_gbps", "pct_hbm_peak", "algorithmic_bytes_per_step",
+                "us_per_token_at_520_steps", "roofline", "cpu_baseline"):
         if key in res:
             out[key] = res[key]
     return out
@@ -645,12 +827,12 @@ def headline(plan: Plan, res: dict) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=520)
-    ap.add_argument("--warmup", type=int, default=52)
+    ap.add_argument("--steps", type=int, default=DEFAULT_STEPS)
+    ap.add_argument("--warmup", type=int, default=DEFAULT_WARMUP)
     ap.add_argument("--workload", default="all",
                     choices=["all", "moe_decode", "dense_decode", "moe_batched", "moe_prefill",
                              "qkv_prefill", "stream_floor", "klinear_decode", "kda_decode",
-                             "copy"])
+                             "norm_decode", "qkv_decode", "decode_shapes", "copy"])
     ap.add_argument("--tokens", type=int, default=64, help="moe_batched tokens per step")
     ap.add_argument("--weights", choices=["w4a16", "mxfp4"], default="w4a16",
                     help="moe_batched / moe_prefill expert weight format")
@@ -679,13 +861,21 @@ def main() -> int:
         _lib.set_path(knob, choice)
         forced[knob] = choice
     dev = torch.device("cuda:0")
-    plan = Plan(args.steps, args.warmup)
+    try:
+        plan = Plan(args.steps, args.warmup)
+    except ValueError as err:
+        print(err, file=sys.stderr)
+        return 2
+    if args.steps < MIN_TIMED_STEPS or args.warmup < MIN_WARMUP_STEPS:
+        log(f"[bench] note: fewer than {MIN_TIMED_STEPS} timed or {MIN_WARMUP_STEPS} warm-up "
+            f"steps; the figures are noisier than at the defaults")
     cpu = not args.no_cpu
     log(f"[bench] device {torch.cuda.get_device_name(0)}, workload {args.workload}, "
         f"steps requested {args.steps}, warm-up requested {args.warmup}")
     t0 = time.time()
     w4 = None
-    needs_w4a16 = args.workload in ("all", "moe_decode", "stream_floor", "klinear_decode") or (
+    needs_w4a16 = args.workload in ("all", "moe_decode", "stream_floor", "klinear_decode",
+                                    "decode_shapes") or (
         args.workload in ("moe_batched", "moe_prefill") and args.weights == "w4a16")
     if needs_w4a16:
         w4 = layer_banks("w4a16", torch.Generator(device=dev).manual_seed(20260729), dev)
@@ -699,14 +889,26 @@ def main() -> int:
             configs[f"3_batched_m{m}"] = run_moe_batched(plan, dev, w4, m, "w4a16", cpu)
         configs["4_moe_prefill"] = run_moe_prefill(plan, dev, w4, "w4a16", cpu)
         configs["4_qkv_prefill"] = run_qkv_prefill(plan, dev, cpu)
+        configs["qkv_decode"] = run_qkv_decode(plan, dev, cpu)
+        for key, entry in run_decode_shapes(plan, dev, w4, cpu).items():
+            configs[f"iso_{key}"] = entry
         configs["next1_klinear_decode"] = run_klinear_decode(plan, dev, w4)
         configs["next4_kda_decode"] = run_kda_decode(plan, dev, cpu)
+        configs["next4_norm_decode"] = run_norm_decode(plan, dev, cpu)
         res["floor"] = run_floor(plan, dev, w4)
         del w4
         torch.cuda.empty_cache()
         mx = layer_banks("mxfp4", torch.Generator(device=dev).manual_seed(20260735), dev)
         configs["5_mxfp4_batched_m64"] = run_moe_batched(plan, dev, mx, 64, "mxfp4", cpu)
         configs["5_mxfp4_prefill"] = run_moe_prefill(plan, dev, mx, "mxfp4", cpu)
+        # the scaled fp4 MFMA form of the same two workloads (the default is bf16 MFMA)
+        with _lib.forced_path("mxfp4_mfma", "fp4"):
+            for key, fn in (("5_mxfp4_batched_m64_fp4_mfma",
+                             lambda: run_moe_batched(plan, dev, mx, 64, "mxfp4", False)),
+                            ("5_mxfp4_prefill_fp4_mfma",
+                             lambda: run_moe_prefill(plan, dev, mx, "mxfp4", False))):
+                configs[key] = fn()
+                configs[key]["config"]["mfma_form"] = "fp4 (scaled f8f6f4, fp8 hi/lo activations)"
         res["configs"] = configs
         floor = res["floor"]
         res["roofline"]["frac_of_measured_floor"] = round(
@@ -733,6 +935,12 @@ def main() -> int:
         res = run_klinear_decode(plan, dev, w4)
     elif args.workload == "kda_decode":
         res = run_kda_decode(plan, dev, cpu)
+    elif args.workload == "norm_decode":
+        res = run_norm_decode(plan, dev, cpu)
+    elif args.workload == "qkv_decode":
+        res = run_qkv_decode(plan, dev, cpu)
+    elif args.workload == "decode_shapes":
+        res = run_decode_shapes(plan, dev, w4, cpu)
     else:
         res = run_copy(dev)
     if forced:
@@ -757,11 +965,7 @@ def run_klinear_decode(plan: Plan, dev, banks) -> dict:
     xs = [torch.randn((1, H), device=dev, generator=gen).to(torch.bfloat16) for _ in range(LAYERS)]
     stream = torch.cuda.Stream(device=dev)
 
-    def all_layers():
-        for l in range(LAYERS):
-            mods[l](xs[l])
-
-    t = time_graph(capture(all_layers, stream), stream, LAYERS, plan)
+    t = time_steps(lambda l: mods[l](xs[l]), LAYERS, stream, plan)
     step_bytes = (TOP_K + 1) * EXPERT_BYTES + TOKEN_IO_BYTES + E_ROUTED * H * 2
     return {"metric": "KLinearMoE decode us/token (router logits + MoE block)",
             "value": round(t["us"], 3), "unit": "us/token", "steps": t["steps"],
@@ -805,14 +1009,9 @@ def run_kda_decode(plan: Plan, dev, cpu: bool) -> dict:
         return kda_decode_step(rec[l], qn[:, 0], kn[:, 0], v.view(1, h, d).float(), decay[:, 0],
                                beta[:, 0], scale=scale)
 
-    def all_layers():
-        for l in range(KDA_LAYERS):
-            layer(l)
-
-    def all_layers_one_launch():
-        for l in range(KDA_LAYERS):
-            kda_decode_layer(*ins, *conv_states[l], *conv_w, raw_decay, dt_bias, a_log, raw_beta,
-                             rec[l], num_heads=h, head_dim=d, eps=1e-6, scale=scale)
+    def one_launch(l):
+        kda_decode_layer(*ins, *conv_states[l], *conv_w, raw_decay, dt_bias, a_log, raw_beta,
+                         rec[l], num_heads=h, head_dim=d, eps=1e-6, scale=scale)
 
     qn = torch.randn((1, h, d), device=dev, generator=gen)
     qn = qn / qn.norm(dim=-1, keepdim=True)
@@ -820,13 +1019,12 @@ def run_kda_decode(plan: Plan, dev, cpu: bool) -> dict:
     dd = -(0.005 + 0.075 * torch.rand((1, h, d), device=dev, generator=gen))
     bb = torch.sigmoid(torch.randn((1, h), device=dev, generator=gen))
 
-    def steps_only():
-        for l in range(KDA_LAYERS):
-            kda_decode_step(rec[l], qn, qn, vv, dd, bb, scale=scale)
+    def step_only(l):
+        kda_decode_step(rec[l], qn, qn, vv, dd, bb, scale=scale)
 
-    one = time_graph(capture(all_layers_one_launch, stream), stream, KDA_LAYERS, plan)
-    t = time_graph(capture(all_layers, stream), stream, KDA_LAYERS, plan)
-    st = time_graph(capture(steps_only, stream), stream, KDA_LAYERS, plan)
+    one = time_steps(one_launch, KDA_LAYERS, stream, plan)
+    t = time_steps(layer, KDA_LAYERS, stream, plan)
+    st = time_steps(step_only, KDA_LAYERS, stream, plan)
     state_bytes = h * d * d * 4
     # state in and out; bf16 inputs, conv states (in and out) and weights; small gates
     layer_bytes = (2 * state_bytes + 3 * d * h * 2 * (1 + 4 + 4 + 4) + h * d * (2 + 4) + h * 6
