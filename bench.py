@@ -979,8 +979,10 @@ def run_kda_decode(plan: Plan, dev, cpu: bool) -> dict:
     """KDA decode, batch 1 (next 4): per layer the three short convolutions,
     the gates and the recurrence step on a 32 x 128 x 128 fp32 state; 160
     layers' states (320 MB) rotate so each step reads and writes HBM. `value`
-    is the one-launch layer (kda_decode_layer); the reference's three-launch
-    chain (plus torch's bf16 -> fp32 view of v) is timed beside it."""
+    is the one-launch layer over 8 blocks per head (kda_decode_layer with the
+    conv states double-buffered); the one-block-per-head layer and the
+    reference's three-launch chain (plus torch's bf16 -> fp32 view of v) are
+    timed beside it."""
     from local_kimi_amd.kernels import (fused_kda_gates, fused_short_conv_triple,
                                         kda_decode_layer, kda_decode_step)
 
@@ -998,6 +1000,9 @@ def run_kda_decode(plan: Plan, dev, cpu: bool) -> dict:
     a_log = torch.log(torch.rand((1, 1, h, 1), device=dev, generator=gen) * 15 + 1)
     conv_states = [[torch.zeros((1, c, 4), dtype=bf, device=dev) for _ in range(3)]
                    for _ in range(KDA_LAYERS)]
+    # the split layer's second conv-state set (a caller alternates the two)
+    conv_next = [[torch.zeros((1, c, 4), dtype=bf, device=dev) for _ in range(3)]
+                 for _ in range(KDA_LAYERS)]
     rec = [rnd((1, h, d, d), 0.05, torch.float32) for _ in range(KDA_LAYERS)]
     stream = torch.cuda.Stream(device=dev)
     scale = d ** -0.5
@@ -1011,6 +1016,11 @@ def run_kda_decode(plan: Plan, dev, cpu: bool) -> dict:
 
     def one_launch(l):
         kda_decode_layer(*ins, *conv_states[l], *conv_w, raw_decay, dt_bias, a_log, raw_beta,
+                         rec[l], num_heads=h, head_dim=d, eps=1e-6, scale=scale,
+                         conv_states_out=conv_next[l])
+
+    def one_block_per_head(l):
+        kda_decode_layer(*ins, *conv_states[l], *conv_w, raw_decay, dt_bias, a_log, raw_beta,
                          rec[l], num_heads=h, head_dim=d, eps=1e-6, scale=scale)
 
     qn = torch.randn((1, h, d), device=dev, generator=gen)
@@ -1023,6 +1033,7 @@ def run_kda_decode(plan: Plan, dev, cpu: bool) -> dict:
         kda_decode_step(rec[l], qn, qn, vv, dd, bb, scale=scale)
 
     one = time_steps(one_launch, KDA_LAYERS, stream, plan)
+    blk = time_steps(one_block_per_head, KDA_LAYERS, stream, plan)
     t = time_steps(layer, KDA_LAYERS, stream, plan)
     st = time_steps(step_only, KDA_LAYERS, stream, plan)
     state_bytes = h * d * d * 4
@@ -1030,8 +1041,8 @@ def run_kda_decode(plan: Plan, dev, cpu: bool) -> dict:
     layer_bytes = (2 * state_bytes + 3 * d * h * 2 * (1 + 4 + 4 + 4) + h * d * (2 + 4) + h * 6
                    + h * d * 4)
     step_bytes = 2 * state_bytes + h * (3 * d + d + 1) * 4 + h * d * 4  # state in + out, q k v decay beta, out
-    log(f"[bench] KDA decode: {one['us']:.2f} us/layer in one launch, three-launch chain "
-        f"{t['us']:.2f} us, step kernel {st['us']:.2f} us")
+    log(f"[bench] KDA decode: {one['us']:.2f} us/layer in one launch (one block per head "
+        f"{blk['us']:.2f} us), three-launch chain {t['us']:.2f} us, step kernel {st['us']:.2f} us")
     res = {
         "metric": "KDA decode us/layer (short convs + gates + recurrence step, batch 1)",
         "value": round(one["us"], 3), "unit": "us/layer", "steps": one["steps"],
@@ -1039,9 +1050,11 @@ def run_kda_decode(plan: Plan, dev, cpu: bool) -> dict:
         "dtype": "f32 state, bf16 projections",
         "config": {"workload": "kda_decode_batch1", "heads": h, "head_dim": d,
                    "layers_rotated": KDA_LAYERS, "launches_per_layer": 1},
+        "one_block_per_head_us": round(blk["us"], 3),
         "three_launch_chain_us": round(t["us"], 3),
         "step_kernel_us": round(st["us"], 3),
-        "roofline": {"kernel": "kda_layer_kernel (convs + gates + step, one launch)",
+        "roofline": {"kernel": "kda_layer_split_kernel (convs + gates + step, one launch, "
+                               "8 blocks per head)",
                      "bound": "hbm",
                      "achieved": round(layer_bytes / (one["us"] * 1e3), 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s",

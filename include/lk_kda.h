@@ -83,6 +83,26 @@ LK_API int lk_kda_decode_layer(const void* q_in, const void* k_in, const void* v
                                int64_t head_dim, float eps, float scale, int value_dtype,
                                int weight_dtype, int decay_dtype, int beta_dtype, void* stream);
 
+/* ---- the same layer over several blocks per head (no reference counterpart)
+ * Arguments as lk_kda_decode_layer, except that the convolution states are
+ * read from q/k/v_state and the shifted states written to q/k/v_state_out
+ * (distinct buffers; callers alternate the two from call to call), which lets
+ * a head's value columns be split over blocks of 16 without a block reading a
+ * state another block already shifted. The recurrent state is updated in
+ * place. q, k, v, decay and beta are bit-identical to lk_kda_decode_layer's;
+ * the step sums its rows in another grouping. head_dim a multiple of 4, at
+ * most 128. */
+LK_API int lk_kda_decode_layer_split(const void* q_in, const void* k_in, const void* v_in,
+                                     const void* q_state, const void* k_state,
+                                     const void* v_state, void* q_state_out, void* k_state_out,
+                                     void* v_state_out, const void* q_weight,
+                                     const void* k_weight, const void* v_weight,
+                                     const void* raw_decay, const float* dt_bias,
+                                     const float* a_log, const void* raw_beta, float* state,
+                                     float* out, int64_t batch, int64_t heads, int64_t head_dim,
+                                     float eps, float scale, int value_dtype, int weight_dtype,
+                                     int decay_dtype, int beta_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

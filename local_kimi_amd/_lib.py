@@ -73,6 +73,8 @@ SIGNATURES: dict[str, list] = {
                      _I, _P],
     "lk_kda_decode_layer": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                             _I64, _I64, _I64, _F, _F, _I, _I, _I, _I, _P],
+    "lk_kda_decode_layer_split": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                  _P, _P, _P, _I64, _I64, _I64, _F, _F, _I, _I, _I, _I, _P],
     "lk_rms_norm": [_P, _P, _P, _I64, _I64, _F, _I, _I, _P],
     "lk_add_rms_norm": [_P, _P, _P, _P, _P, _I64, _I64, _F, _I, _I, _P],
     "lk_rms_gated_norm": [_P, _P, _P, _P, _I64, _I64, _F, _I, _I, _I, _I, _P],

@@ -429,6 +429,247 @@ kda_layer_kernel(const LayerArgs a, int heads, int dim, float eps, float scale, 
   if (rg == 0) *reinterpret_cast<float4*>(a.out + bh * dim + c0) = make_float4(o[0], o[1], o[2], o[3]);
 }
 
+// A decode layer over several blocks per head: block (b, h, y) owns value
+// columns [16 y, 16 y + 16) of the head's D x D state (128 threads: column
+// group cg = lane / 16 of 4 columns, row group rg = 16 * wave + lane % 16 of
+// rows rg + 32 p), so 256 blocks cover 32 heads of 128 and every CU streams a
+// slice of the state. Every block of a head needs all of q and k (the norms,
+// and every row's k and q in the step), so each block computes the q and k
+// convolutions itself, and the v convolutions of its own columns. The
+// convolution states are read from one buffer and the shifted states written
+// to another (the caller alternates them from call to call), so no block can
+// read a state that another block already shifted: block y = 0 writes the q
+// and k states, each block the v states of its columns. The arithmetic of
+// every convolution, gate and norm is kda_layer_kernel's, so q, k, v, decay
+// and beta are bit-identical with it; the step's sums run over the rows in
+// another grouping. The blocks of a 128-byte state line (two column
+// blocks) are dispatched to one XCD when the item count allows, so the line
+// is fetched into one L2 once.
+constexpr int kSplitThreads = 128;
+constexpr int kSplitCols = 16;
+constexpr int kSplitRowGroups = 32;
+
+struct SplitArgs {
+  const void* in[3];
+  const void* conv_in[3];
+  void* conv_out[3];
+  const void* conv_weight[3];
+  const void* raw_decay;
+  const float* dt_bias;
+  const float* a_log;
+  const void* raw_beta;
+  float* state;
+  float* out;
+};
+
+// storage of compile-time dtype DT (the split kernel's conv loads go out in
+// one batch only when no run-time dtype branch sits between them)
+template <int DT>
+__device__ inline float load_as(const void* p, int64_t i) {
+  if constexpr (DT == LK_DTYPE_F32) {
+    return static_cast<const float*>(p)[i];
+  } else if constexpr (DT == LK_DTYPE_BF16) {
+    return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  } else {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<const uint16_t*>(p)[i]));
+  }
+}
+
+// One width-4 convolution channel: the loads (window, token, weights) of
+// load(), then apply() (short_conv_kernel's arithmetic) and the shifted
+// window into state_out.
+template <int VDT, int WDT>
+struct ConvChannel {
+  float s1, s2, s3, token, w0, w1, w2, w3;
+  __device__ inline void load(const void* state_in, const void* in, const void* weight,
+                              int64_t si, int64_t xi, int64_t wi) {
+    s1 = load_as<VDT>(state_in, si + 1);
+    s2 = load_as<VDT>(state_in, si + 2);
+    s3 = load_as<VDT>(state_in, si + 3);
+    token = load_as<VDT>(in, xi);
+    w0 = load_as<WDT>(weight, wi + 0);
+    w1 = load_as<WDT>(weight, wi + 1);
+    w2 = load_as<WDT>(weight, wi + 2);
+    w3 = load_as<WDT>(weight, wi + 3);
+  }
+  __device__ inline float apply(void* state_out, int64_t si, bool write) const {
+    float acc = s1 * w0;
+    acc += s2 * w1;
+    acc += s3 * w2;
+    acc += token * w3;
+    float y = acc / (1.0f + expf(-acc));
+    if constexpr (VDT == LK_DTYPE_BF16) y = round_bf16(y);
+    else if constexpr (VDT == LK_DTYPE_F16) y = static_cast<float>(static_cast<_Float16>(y));
+    if (write) {
+      store_value(state_out, si + 0, s1, VDT);
+      store_value(state_out, si + 1, s2, VDT);
+      store_value(state_out, si + 2, s3, VDT);
+      store_value(state_out, si + 3, token, VDT);
+    }
+    return y;
+  }
+};
+
+template <int VDT, int WDT>
+__global__ void __launch_bounds__(kSplitThreads)
+kda_layer_split_kernel(const SplitArgs a, int heads, int dim, int vs, int64_t items, int paired,
+                       float eps, float scale, int ddt, int bdt) {
+  __shared__ float qk[2][kLayerMaxDim];
+  __shared__ float vcol[kSplitCols];
+  __shared__ float gain[kLayerMaxDim];
+  __shared__ float norm[2];
+  __shared__ float beta_s;
+  __shared__ float red[2][kSplitCols];
+  // item = (batch * heads + head) * vs + column block; with `paired`, the
+  // two column blocks of a 128-byte line sit 8 blocks apart (one XCD)
+  const int64_t lin = blockIdx.x;
+  const int64_t item = paired ? 2 * ((lin >> 4) * 8 + (lin & 7)) + ((lin >> 3) & 1) : lin;
+  if (item >= items) return;  // block-uniform
+  const int64_t bh = item / vs;
+  const int y = static_cast<int>(item - bh * vs);
+  const int64_t b = bh / heads;
+  const int h = static_cast<int>(bh - b * heads);
+  const int channels = heads * dim;
+  const int t = threadIdx.x;
+  const int wave = t / kWave, lane = t & (kWave - 1);
+  const int cg = lane >> 4, rg = wave * 16 + (lane & 15);
+  const int c0 = y * kSplitCols + cg * 4;
+  const bool cols = c0 < dim;  // dim % 4 == 0 (host-checked)
+  float* const s_head = a.state + bh * dim * dim;
+
+  // 1. this thread's state rows, before anything else
+  float s[4][4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int i = rg + kSplitRowGroups * p;
+    if (cols && i < dim) {
+      const float4 x = *reinterpret_cast<const float4*>(s_head + static_cast<int64_t>(i) * dim + c0);
+      s[p][0] = x.x;
+      s[p][1] = x.y;
+      s[p][2] = x.z;
+      s[p][3] = x.w;
+    } else {
+      s[p][0] = s[p][1] = s[p][2] = s[p][3] = 0.f;
+    }
+  }
+  // 2. every load of the preparation in one batch: the q and k convolution
+  // channels of the head (thread t takes channels t and t + 128 of the 2 * dim),
+  // the v channel of this block's column t, the gate inputs of row t
+  ConvChannel<VDT, WDT> cc[3];
+  int conv_of[2], j_of[2];
+  bool live[3];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int u = t + kSplitThreads * q;
+    live[q] = u < 2 * dim;
+    const int uc = live[q] ? u : 0;
+    conv_of[q] = uc >= dim ? 1 : 0;
+    j_of[q] = uc - conv_of[q] * dim;
+    const int64_t ch = static_cast<int64_t>(h) * dim + j_of[q];
+    cc[q].load(a.conv_in[conv_of[q]], a.in[conv_of[q]], a.conv_weight[conv_of[q]],
+               (b * channels + ch) * 4, b * channels + ch, ch * 4);
+  }
+  const int vj = y * kSplitCols + t;
+  live[2] = t < kSplitCols && vj < dim;
+  const int64_t vch = static_cast<int64_t>(h) * dim + (live[2] ? vj : 0);
+  cc[2].load(a.conv_in[2], a.in[2], a.conv_weight[2], (b * channels + vch) * 4, b * channels + vch,
+             vch * 4);
+  const bool grow = t < dim;
+  const float raw = load_value(a.raw_decay, bh * dim + (grow ? t : 0), ddt);
+  const float dtb = a.dt_bias[h * dim + (grow ? t : 0)];
+  const float alog = a.a_log[h];
+  const float rbeta = t == 0 ? load_value(a.raw_beta, bh, bdt) : 0.f;
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+    if (live[q])
+      qk[conv_of[q]][j_of[q]] = cc[q].apply(a.conv_out[conv_of[q]],
+                                            (b * channels + static_cast<int64_t>(h) * dim +
+                                             j_of[q]) * 4,
+                                            y == 0);
+  if (live[2]) vcol[t] = cc[2].apply(a.conv_out[2], (b * channels + vch) * 4, true);
+  // 3. exp(decay) of every row, beta
+  if (grow) gain[t] = expf(-expf(alog) * softplus_f32(raw + dtb));
+  if (t == 0) beta_s = 1.0f / (1.0f + expf(-rbeta));
+  __syncthreads();
+  // 4. q and k norms: wave 0 and wave 1, the gates kernel's per-lane order
+  {
+    float acc = 0.f;
+    for (int d = lane; d < dim; d += kWave) acc = fmaf(qk[wave][d], qk[wave][d], acc);
+    acc = wave_sum(acc);
+    if (lane == 0) norm[wave] = 1.0f / sqrtf(acc + eps);
+  }
+  __syncthreads();
+  const float rq = norm[0], rk = norm[1], beta = beta_s;
+
+  // 5. the recurrence step on this block's columns
+  float kr[4], qr[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int i = rg + kSplitRowGroups * p;
+    const bool row_ok = i < dim;
+    const float g = row_ok ? gain[i] : 0.f;
+    kr[p] = row_ok ? qk[1][i] * rk : 0.f;
+    qr[p] = row_ok ? (qk[0][i] * rq) * scale : 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s[p][c] *= g;
+  }
+  // sums over the 32 row groups: the 16 lanes of a DPP row, then the 2 waves
+  auto reduce = [&](float (&v)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float x = v[c];
+      x += dpp_f32<kQuadXor1>(x);
+      x += dpp_f32<kQuadXor2>(x);
+      x += dpp_f32<kRowHalfMirror>(x);
+      x += dpp_f32<kRowMirror>(x);
+      v[c] = x;
+    }
+    __syncthreads();
+    if ((lane & 15) == 0) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) red[wave][cg * 4 + c] = v[c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] = red[0][cg * 4 + c] + red[1][cg * 4 + c];
+  };
+  float delta[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float part = 0.f;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) part = fmaf(s[p][c], kr[p], part);
+    delta[c] = part;
+  }
+  reduce(delta);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) delta[c] = (cols ? vcol[cg * 4 + c] : 0.f) - delta[c];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float bk = beta * kr[p];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s[p][c] = fmaf(bk, delta[c], s[p][c]);
+  }
+  float o[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float part = 0.f;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) part = fmaf(s[p][c], qr[p], part);
+    o[c] = part;
+  }
+  reduce(o);
+  if (!cols) return;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int i = rg + kSplitRowGroups * p;
+    if (i < dim)
+      *reinterpret_cast<float4*>(s_head + static_cast<int64_t>(i) * dim + c0) =
+          make_float4(s[p][0], s[p][1], s[p][2], s[p][3]);
+  }
+  if (rg == 0) *reinterpret_cast<float4*>(a.out + bh * dim + c0) = make_float4(o[0], o[1], o[2], o[3]);
+}
+
 bool valid_dtype(int d) { return d == LK_DTYPE_F32 || d == LK_DTYPE_F16 || d == LK_DTYPE_BF16; }
 
 }  // namespace
@@ -531,6 +772,61 @@ int lk_kda_decode_layer(const void* q_in, const void* k_in, const void* v_in, vo
       a, static_cast<int>(heads), static_cast<int>(head_dim), eps, scale, value_dtype,
       weight_dtype, decay_dtype, beta_dtype);
   return check_launch("lk_kda_decode_layer");
+}
+
+int lk_kda_decode_layer_split(const void* q_in, const void* k_in, const void* v_in,
+                              const void* q_state, const void* k_state, const void* v_state,
+                              void* q_state_out, void* k_state_out, void* v_state_out,
+                              const void* q_weight, const void* k_weight, const void* v_weight,
+                              const void* raw_decay, const float* dt_bias, const float* a_log,
+                              const void* raw_beta, float* state, float* out, int64_t batch,
+                              int64_t heads, int64_t head_dim, float eps, float scale,
+                              int value_dtype, int weight_dtype, int decay_dtype, int beta_dtype,
+                              void* stream) {
+  LK_REQUIRE(batch > 0 && heads > 0, "KDA decode dimensions must be nonzero");
+  LK_REQUIRE(head_dim > 0 && head_dim <= kLayerMaxDim && head_dim % 4 == 0,
+             "one-launch KDA layer takes head_dim a multiple of 4 up to %d, got %lld",
+             kLayerMaxDim, (long long)head_dim);
+  LK_REQUIRE(eps > 0, "eps must be positive");
+  LK_REQUIRE(heads * head_dim < (int64_t{1} << 31), "too many channels");
+  LK_REQUIRE(valid_dtype(value_dtype) && valid_dtype(weight_dtype) && valid_dtype(decay_dtype) &&
+                 valid_dtype(beta_dtype),
+             "unknown dtype code");
+  LK_REQUIRE(q_in && k_in && v_in && q_state && k_state && v_state && q_state_out &&
+                 k_state_out && v_state_out && q_weight && k_weight && v_weight && raw_decay &&
+                 dt_bias && a_log && raw_beta && state && out,
+             "null pointer argument");
+  LK_REQUIRE(q_state_out != q_state && k_state_out != k_state && v_state_out != v_state,
+             "the split KDA layer writes the shifted convolution states to other buffers");
+  LK_REQUIRE(reinterpret_cast<uintptr_t>(state) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
+             "state and out must be 16-byte aligned");
+  const int64_t vs = (head_dim + kSplitCols - 1) / kSplitCols;
+  const int64_t items = batch * heads * vs;
+  LK_REQUIRE(items < (int64_t{1} << 31), "too many heads");
+  const int paired = (vs % 2 == 0 && items % 16 == 0) ? 1 : 0;
+  SplitArgs a{{q_in, k_in, v_in}, {q_state, k_state, v_state},
+              {q_state_out, k_state_out, v_state_out}, {q_weight, k_weight, v_weight},
+              raw_decay, dt_bias, a_log, raw_beta, state, out};
+  const dim3 grid(static_cast<unsigned>(items));
+  const int nh = static_cast<int>(heads), nd = static_cast<int>(head_dim),
+            nvs = static_cast<int>(vs);
+  hipStream_t s = as_stream(stream);
+#define LK_KDA_SPLIT(V, W)                                                                 \
+  kda_layer_split_kernel<V, W><<<grid, kSplitThreads, 0, s>>>(a, nh, nd, nvs, items, paired, \
+                                                              eps, scale, decay_dtype,       \
+                                                              beta_dtype)
+#define LK_KDA_SPLIT_W(V)                                             \
+  do {                                                                \
+    if (weight_dtype == LK_DTYPE_F32) LK_KDA_SPLIT(V, LK_DTYPE_F32);  \
+    else if (weight_dtype == LK_DTYPE_F16) LK_KDA_SPLIT(V, LK_DTYPE_F16); \
+    else LK_KDA_SPLIT(V, LK_DTYPE_BF16);                              \
+  } while (0)
+  if (value_dtype == LK_DTYPE_F32) LK_KDA_SPLIT_W(LK_DTYPE_F32);
+  else if (value_dtype == LK_DTYPE_F16) LK_KDA_SPLIT_W(LK_DTYPE_F16);
+  else LK_KDA_SPLIT_W(LK_DTYPE_BF16);
+#undef LK_KDA_SPLIT_W
+#undef LK_KDA_SPLIT
+  return check_launch("lk_kda_decode_layer_split");
 }
 
 }  // extern "C"

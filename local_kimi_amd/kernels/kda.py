@@ -258,16 +258,24 @@ def kda_decode_layer(q_in: torch.Tensor, k_in: torch.Tensor, v_in: torch.Tensor,
                      q_weight: torch.Tensor, k_weight: torch.Tensor, v_weight: torch.Tensor,
                      raw_decay: torch.Tensor, dt_bias: torch.Tensor, a_log: torch.Tensor,
                      raw_beta: torch.Tensor, state: torch.Tensor, *, num_heads: int,
-                     head_dim: int, eps: float = 1e-6, scale: float | None = None
+                     head_dim: int, eps: float = 1e-6, scale: float | None = None,
+                     conv_states_out: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None
                      ) -> torch.Tensor:
     """One KDA decode token: the short convolutions, the gates and the
     recurrence step in one launch (what engine/klinear/attention.py:193-271
     does with fused_short_conv_triple, fused_kda_gates and kda_decode_step).
 
     Arguments as those three functions take them, with ``state`` the fp32
-    recurrent state [B, H, D, D]; ``scale`` defaults to D ** -0.5. Conv states
-    and ``state`` are updated in place; returns the fp32 output [B, H, D]
-    (``fused_output`` of attention.py:268). head_dim: a multiple of 4 up to 128.
+    recurrent state [B, H, D, D]; ``scale`` defaults to D ** -0.5. ``state``
+    is updated in place; returns the fp32 output [B, H, D] (``fused_output``
+    of attention.py:268). head_dim: a multiple of 4 up to 128.
+
+    Without ``conv_states_out`` the conv states are updated in place and one
+    block works on each head. With ``conv_states_out`` (three dense tensors
+    shaped like the states, none of them a state) the shifted conv states are
+    written there instead and each head's value columns are split over blocks
+    of 16 (a head's blocks all read the old conv states); callers alternate
+    the two state sets from token to token.
     """
     batch, channels = _validate_conv(q_in, k_in, v_in, q_state, k_state, v_state, q_weight,
                                      k_weight, v_weight)
@@ -291,6 +299,10 @@ def kda_decode_layer(q_in: torch.Tensor, k_in: torch.Tensor, v_in: torch.Tensor,
         weights = [w.float() for w in weights]
     wcode = _DTYPE_CODES[weights[0].dtype]
     weights = [_w._c(w) for w in weights]
+    if conv_states_out is not None:
+        return _layer_split(ins, [q_state, k_state, v_state], conv_states_out, weights, raw_decay,
+                            dt_bias, a_log, raw_beta, state, batch, num_heads, head_dim, eps,
+                            scale, vcode, wcode)
     conv_states = [q_state, k_state, v_state]
     conv_work = [s if s.is_contiguous() else s.contiguous() for s in conv_states]
     work = _dense(state)
@@ -308,6 +320,39 @@ def kda_decode_layer(q_in: torch.Tensor, k_in: torch.Tensor, v_in: torch.Tensor,
     for st, w in zip(conv_states, conv_work):
         if w is not st:
             st.copy_(w)
+    if work is not state:
+        state.copy_(work)
+    return out
+
+
+def _layer_split(ins, states, outs, weights, raw_decay, dt_bias, a_log, raw_beta, state, batch,
+                 num_heads, head_dim, eps, scale, vcode, wcode):
+    outs = tuple(outs)
+    if len(outs) != 3:
+        raise ValueError("conv_states_out must hold the q, k and v states")
+    for st, o in zip(states, outs):
+        if o.shape != st.shape or o.dtype != st.dtype or o.device != st.device:
+            raise ValueError("each conv_states_out tensor must match its state's shape, dtype "
+                             "and device")
+        if not o.is_contiguous():
+            raise ValueError("conv_states_out tensors must be contiguous")
+    spans = [(t.data_ptr(), t.data_ptr() + t.numel() * t.element_size()) for t in (*states, *outs)]
+    for i, (lo, hi) in enumerate(spans[3:]):
+        if any(lo < h2 and l2 < hi for l2, h2 in spans[:3]):
+            raise ValueError(f"conv_states_out[{i}] overlaps a state it is computed from")
+    src = [s if s.is_contiguous() else s.contiguous() for s in states]
+    work = _dense(state)
+    bias = dt_bias.float().contiguous()
+    rate = a_log.float().reshape(num_heads).contiguous()
+    out = torch.empty((batch, num_heads, head_dim), dtype=torch.float32, device=state.device)
+    s = head_dim ** -0.5 if scale is None else float(scale)
+    with torch.cuda.device(state.device):
+        _lib.call("lk_kda_decode_layer_split", *(t.data_ptr() for t in ins),
+                  *(t.data_ptr() for t in src), *(t.data_ptr() for t in outs),
+                  *(t.data_ptr() for t in weights), raw_decay.data_ptr(), bias.data_ptr(),
+                  rate.data_ptr(), raw_beta.data_ptr(), work.data_ptr(), out.data_ptr(), batch,
+                  num_heads, head_dim, float(eps), s, vcode, wcode, _code(raw_decay, "raw_decay"),
+                  _code(raw_beta, "raw_beta"), _w._stream(state.device))
     if work is not state:
         state.copy_(work)
     return out

@@ -399,3 +399,118 @@ def test_layer_rejects_wide_heads():
                          torch.zeros(c, device=DEV), torch.zeros((1, 1, h, 1), device=DEV),
                          torch.zeros((1, 1, h), dtype=bf, device=DEV),
                          torch.zeros((1, h, d, d), device=DEV), num_heads=h, head_dim=d)
+
+
+# ---------------------------------------------------------------------------
+# the layer over several blocks per head (conv states double-buffered)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("b,h,d", [(1, 32, 128), (2, 4, 72), (3, 2, 8), (1, 3, 64)])
+def test_split_layer_matches_the_oracle_chain(rng, dtype, b, h, d):
+    """New conv states (written to the other buffer) bit-exact, the old ones
+    untouched, state and output within the step's single-step bound (3e-5).
+    (2, 4, 72): 5 column blocks per head, the last one half empty; (1, 3, 64):
+    an item count that is no multiple of 16 (blocks in plain order)."""
+    from local_kimi_amd.kernels import kda_decode_layer
+
+    name = _STORAGE[dtype]
+    ins, conv_states, conv_w, raw_decay, raw_beta, dt_bias, a_log, rec = _layer_inputs(
+        rng, b, h, d, name)
+    (qo, ko, vo), states_want = K.short_conv_triple(*ins, *conv_states, *conv_w, name)
+    decay, beta, qn, kn = K.gates(raw_decay, dt_bias, a_log, raw_beta, qo, ko, h, d, 1e-6)
+    want_state, want_out = K.decode_step(rec, qn[:, 0], kn[:, 0], vo.reshape(b, h, d),
+                                         decay[:, 0], beta[:, 0], d ** -0.5)
+    old = [_t(s, dtype) for s in conv_states]
+    new = [torch.full_like(s, 7.0) for s in old]
+    st = _t(rec)
+    out = kda_decode_layer(*(_t(x, dtype) for x in ins), *old, *(_t(w, dtype) for w in conv_w),
+                           _t(raw_decay, dtype), _t(dt_bias), _t(a_log), _t(raw_beta, dtype), st,
+                           num_heads=h, head_dim=d, conv_states_out=new)
+    for s, want, before in zip(new, states_want, conv_states):
+        assert np.array_equal(_np(s), want)
+    for s, before in zip(old, conv_states):
+        assert np.array_equal(_np(s), before)
+    _close(_np(st), want_state, 3e-5, 3e-5, f"split layer state {b, h, d}")
+    _close(_np(out), want_out, 3e-5, 3e-5, f"split layer output {b, h, d}")
+
+
+def test_split_layer_tokens_agree_with_the_one_block_layer(rng):
+    """Four decode tokens, the split layer alternating two conv-state sets and
+    the one-block layer updating its states in place: conv states equal after
+    every token; state and output within two summation orders (1e-6 absolute
+    + 1e-5 relative per token)."""
+    from local_kimi_amd.kernels import kda_decode_layer
+
+    b, h, d = 2, 32, 128
+    bf = torch.bfloat16
+    ins, conv_states, conv_w, raw_decay, raw_beta, dt_bias, a_log, rec = _layer_inputs(
+        rng, b, h, d, "bfloat16")
+    fixed = ([_t(w, bf) for w in conv_w], _t(raw_decay, bf), _t(dt_bias), _t(a_log),
+             _t(raw_beta, bf))
+    one = [_t(s, bf) for s in conv_states]
+    sets = [[_t(s, bf) for s in conv_states], [torch.zeros_like(_t(s, bf)) for s in conv_states]]
+    r_one, r_split = _t(rec), _t(rec)
+    for token in range(4):
+        x = [_t(K.round_to(rng.normal(size=(b, 1, h * d)), "bfloat16"), bf) for _ in range(3)]
+        o1 = kda_decode_layer(*x, *one, *fixed[0], *fixed[1:], r_one, num_heads=h, head_dim=d)
+        src, dst = sets[token % 2], sets[(token + 1) % 2]
+        o2 = kda_decode_layer(*x, *src, *fixed[0], *fixed[1:], r_split, num_heads=h, head_dim=d,
+                              conv_states_out=dst)
+        for a, c in zip(one, dst):
+            assert torch.equal(a, c), token
+        _close(_np(r_split), _np(r_one), 1e-6, 1e-5, f"token {token} state")
+        _close(_np(o2), _np(o1), 1e-6, 1e-5, f"token {token} output")
+        r_split.copy_(r_one)  # the next token starts both layers from the same state
+
+
+def test_split_layer_graph_replays_match_eager(rng):
+    from local_kimi_amd.kernels import kda_decode_layer
+
+    b, h, d = 1, 32, 128
+    bf = torch.bfloat16
+    ins, conv_states, conv_w, raw_decay, raw_beta, dt_bias, a_log, rec = _layer_inputs(
+        rng, b, h, d, "bfloat16")
+    fixed = ([_t(x, bf) for x in ins], [_t(w, bf) for w in conv_w], _t(raw_decay, bf),
+             _t(dt_bias), _t(a_log), _t(raw_beta, bf))
+    src = [_t(s, bf) for s in conv_states]
+
+    def run(dst, r):
+        return kda_decode_layer(*fixed[0], *src, *fixed[1], *fixed[2:], r, num_heads=h,
+                                head_dim=d, conv_states_out=dst)
+
+    g_dst, e_dst = [torch.zeros_like(s) for s in src], [torch.zeros_like(s) for s in src]
+    g_rec, e_rec = _t(rec), _t(rec)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        run([torch.zeros_like(s) for s in src], _t(rec))
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        g_out = run(g_dst, g_rec)
+    for rep in range(4):
+        with torch.cuda.stream(stream):
+            graph.replay()
+        e_out = run(e_dst, e_rec)
+        torch.cuda.synchronize()
+        assert torch.equal(g_out, e_out) and torch.equal(g_rec, e_rec), rep
+        for a, c in zip(g_dst, e_dst):
+            assert torch.equal(a, c), rep
+
+
+def test_split_layer_refuses_outputs_that_overlap_the_states(rng):
+    from local_kimi_amd.kernels import kda_decode_layer
+
+    b, h, d = 1, 2, 8
+    bf = torch.bfloat16
+    ins, conv_states, conv_w, raw_decay, raw_beta, dt_bias, a_log, rec = _layer_inputs(
+        rng, b, h, d, "bfloat16")
+    states = [_t(s, bf) for s in conv_states]
+    args = ([_t(x, bf) for x in ins], [_t(w, bf) for w in conv_w])
+    with pytest.raises(ValueError, match="overlaps"):
+        kda_decode_layer(*args[0], *states, *args[1], _t(raw_decay, bf), _t(dt_bias), _t(a_log),
+                         _t(raw_beta, bf), _t(rec), num_heads=h, head_dim=d,
+                         conv_states_out=(states[0], torch.zeros_like(states[1]),
+                                          torch.zeros_like(states[2])))
