@@ -903,6 +903,10 @@ __device__ inline void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Slot swizzle of row m in the direct-load activation layout: (m & 15) with
+// its two 2-bit halves swapped.
+__device__ inline int row_swizzle(int m) { return ((m >> 2) & 3) | ((m & 3) << 2); }
+
 // One tile of <= 16 * MT rows x kBN columns of a streaming block (below).
 // MT = 1: all k-steps of the activations resident; MT = 4 or 5: passes of
 // kStPassSteps (5: 3) k-steps, double buffered. DIRECT: activations come in by
@@ -1064,9 +1068,12 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
   auto pass_steps = [&](int p) { return min(ps, ksteps - p * ps); };
 
   // Direct-load layout: a k-step's activations are [tile row m][slot] of 16
-  // bytes, chunk c (k = 8c..8c+7 of the step) of row m in slot c ^ (m & 15),
-  // so 16 lanes of one load read one row's 256 contiguous bytes and an MFMA
-  // fragment read (16 rows, one chunk each) meets every bank once. One load
+  // bytes, chunk c (k = 8c..8c+7 of the step) of row m in slot c ^ rs(m),
+  // rs(m) = (m & 15) with its two 2-bit halves swapped, so 16 lanes of one
+  // load read one row's 256 contiguous bytes and an MFMA fragment read (16
+  // rows, one chunk each) is free of bank conflicts (measured by the
+  // SQ_LDS_BANK_CONFLICT counter on this access pattern: the plain c ^ (m & 15)
+  // costs 4 conflict cycles per 16-byte read, this one none). One load
   // fills a block of 4 rows of one k-step (lane L: row 4 blk + L / 16, chunk
   // (L & 15) ^ (row & 15)). MT > 1: wave wv fills blocks wv, wv + 8, ... of
   // every k-step of a pass. MT == 1 (one pass over all k-steps): wave wv
@@ -1094,7 +1101,7 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
     for (int h = 0; h < kPw; ++h) {
       const int blk = MT == 1 ? (wv & 3) : min(wv + kStWaves * h, kBlocks - 1);
       const int m = blk * 4 + jq;
-      voff[h] = static_cast<uint32_t>(row_index[m] * K * 2 + ((lane & 15) ^ (m & 15)) * 16);
+      voff[h] = static_cast<uint32_t>(row_index[m] * K * 2 + ((lane & 15) ^ row_swizzle(m)) * 16);
     }
     if constexpr (FMT == kFmtW4A16) {
       rs_n = buffer_rsrc(g.a_neg, g.a_rows * (K / 128) * 4);
@@ -1205,9 +1212,11 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& g, const int expert,
       }
   // LDS slot of this lane's MFMA fragment (subtile ms, sub-step t) of local
   // k-step ls in buffer b: the swizzled fragment blocks of the staged layout,
-  // or the row-major layout of direct loads
+  // or the row-major layout of direct loads (this lane's row within a subtile
+  // is ln, so its swizzle is rs(ln))
+  [[maybe_unused]] const int rsw = row_swizzle(ln);
   auto a_slot = [&](int b, int ls, int ms, int t) -> int {
-    if constexpr (kDirect) return ((b * ps + ls) * kRows + ms * 16 + ln) * 16 + ((4 * jq + t) ^ ln);
+    if constexpr (kDirect) return ((b * ps + ls) * kRows + ms * 16 + ln) * 16 + ((4 * jq + t) ^ rsw);
     else return (((b * ps + ls) * MT + ms) * 4 + t) * kWave + jq * 16 + (ln ^ (4 * t + jq));
   };
   // one k-step: weights wj (a ring slot), activation buffer b, local step ls.
