@@ -27,80 +27,77 @@ namespace {
 constexpr int kNormThreads = 256;
 constexpr int kNormMaxWidth = 8192;
 
-// 8 values of one chunk as loaded from storage of a given dtype code
-// (every dtype is a run-time argument; the branches are uniform per launch)
+// 8 values of one chunk as loaded from storage of a given dtype code. The
+// dtype only picks the addresses (no branch between loads, so a lane's loads
+// all go out before the first is used): fp32 takes two 16-byte words, the
+// 16-bit types one, whose second load repeats the first (an L1 hit).
 struct Chunk {
   uint4 lo, hi;  // hi holds values 4..7 only for fp32 storage
 };
 
 __device__ inline Chunk load_chunk(const void* base, int64_t chunk, int dt) {
+  const uint4* p = static_cast<const uint4*>(base);
+  const bool wide = dt == LK_DTYPE_F32;
   Chunk c;
-  if (dt == LK_DTYPE_F32) {
-    const uint4* p = static_cast<const uint4*>(base) + 2 * chunk;
-    c.lo = p[0];
-    c.hi = p[1];
-  } else {
-    c.lo = static_cast<const uint4*>(base)[chunk];
-    c.hi = make_uint4(0, 0, 0, 0);
-  }
+  c.lo = p[wide ? 2 * chunk : chunk];
+  c.hi = p[wide ? 2 * chunk + 1 : chunk];
   return c;
 }
 
+// The dtype conversions below select between the candidate results with the
+// (launch-uniform) dtype code instead of branching on it: the kernels stay
+// straight-line code a few KB long, which a cold instruction cache fetches in
+// far less time than a branch tree over every dtype (a one-row decode launch
+// is one wave walking that code once).
+__device__ inline float half_bits_to_f32(uint32_t h, bool bf16) {
+  const float as_bf16 = __uint_as_float(h << 16);
+  const float as_f16 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+  return bf16 ? as_bf16 : as_f16;
+}
+
 __device__ inline void unpack_chunk(const Chunk& c, int dt, float (&v)[8]) {
-  if (dt == LK_DTYPE_F32) {
-    v[0] = __uint_as_float(c.lo.x); v[1] = __uint_as_float(c.lo.y);
-    v[2] = __uint_as_float(c.lo.z); v[3] = __uint_as_float(c.lo.w);
-    v[4] = __uint_as_float(c.hi.x); v[5] = __uint_as_float(c.hi.y);
-    v[6] = __uint_as_float(c.hi.z); v[7] = __uint_as_float(c.hi.w);
-    return;
-  }
-  const uint32_t w[4] = {c.lo.x, c.lo.y, c.lo.z, c.lo.w};
+  const bool wide = dt == LK_DTYPE_F32, bf16 = dt == LK_DTYPE_BF16;
+  const uint32_t w[8] = {c.lo.x, c.lo.y, c.lo.z, c.lo.w, c.hi.x, c.hi.y, c.hi.z, c.hi.w};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint16_t a = static_cast<uint16_t>(w[j] & 0xFFFFu), b = static_cast<uint16_t>(w[j] >> 16);
-    if (dt == LK_DTYPE_BF16) {
-      v[2 * j] = bf16_to_f32(a);
-      v[2 * j + 1] = bf16_to_f32(b);
-    } else {
-      v[2 * j] = static_cast<float>(__builtin_bit_cast(_Float16, a));
-      v[2 * j + 1] = static_cast<float>(__builtin_bit_cast(_Float16, b));
-    }
+    const float a = half_bits_to_f32(w[j] & 0xFFFFu, bf16);
+    const float b = half_bits_to_f32(w[j] >> 16, bf16);
+    v[2 * j] = wide ? __uint_as_float(w[2 * j]) : a;
+    v[2 * j + 1] = wide ? __uint_as_float(w[2 * j + 1]) : b;
   }
 }
 
-// x rounded to storage dtype dt, as fp32
+__device__ inline uint32_t f32_to_half_bits(float x, bool bf16) {
+  const uint32_t as_f16 = __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+  return bf16 ? static_cast<uint32_t>(f32_to_bf16(x)) : as_f16;
+}
+
 __device__ inline float round_to(float x, int dt) {
-  if (dt == LK_DTYPE_BF16) return round_bf16(x);
-  if (dt == LK_DTYPE_F16) return static_cast<float>(static_cast<_Float16>(x));
-  return x;
+  const float as_bf16 = round_bf16(x);
+  const float as_f16 = static_cast<float>(static_cast<_Float16>(x));
+  return dt == LK_DTYPE_BF16 ? as_bf16 : (dt == LK_DTYPE_F16 ? as_f16 : x);
 }
 
 __device__ inline void store_chunk(void* base, int64_t chunk, int dt, const float (&v)[8]) {
-  if (dt == LK_DTYPE_F32) {
-    uint4* p = static_cast<uint4*>(base) + 2 * chunk;
-    p[0] = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
-                      __float_as_uint(v[3]));
-    p[1] = make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
-                      __float_as_uint(v[7]));
-    return;
-  }
-  uint32_t w[4];
+  const bool wide = dt == LK_DTYPE_F32, bf16 = dt == LK_DTYPE_BF16;
+  uint32_t h[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint16_t a, b;
-    if (dt == LK_DTYPE_BF16) {
-      a = f32_to_bf16(v[2 * j]);
-      b = f32_to_bf16(v[2 * j + 1]);
-    } else {
-      a = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[2 * j]));
-      b = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[2 * j + 1]));
-    }
-    w[j] = static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
-  }
-  static_cast<uint4*>(base)[chunk] = make_uint4(w[0], w[1], w[2], w[3]);
+  for (int j = 0; j < 4; ++j)
+    h[j] = f32_to_half_bits(v[2 * j], bf16) | (f32_to_half_bits(v[2 * j + 1], bf16) << 16);
+  // fp32 writes two 16-byte words; the 16-bit types write their one word
+  // twice (the same bytes to the same address), so no store is conditional
+  uint4* p = static_cast<uint4*>(base);
+  const uint4 narrow = make_uint4(h[0], h[1], h[2], h[3]);
+  p[wide ? 2 * chunk : chunk] =
+      wide ? make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                        __float_as_uint(v[3]))
+           : narrow;
+  p[wide ? 2 * chunk + 1 : chunk] =
+      wide ? make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                        __float_as_uint(v[7]))
+           : narrow;
 }
 
-// Sum over the LPR lanes of each row group (every lane gets the total).
 template <int LPR>
 __device__ inline float row_sum(float v) {
   v += dpp_f32<kQuadXor1>(v);
@@ -134,9 +131,20 @@ struct NormArgs {
   int weight_dt, gate_dt, out_dt;
 };
 
-template <NormKind KIND, int LPR, int IT>
+// XDT is the storage dtype of the input rows (and delta / sum), ODT the one
+// dtype of weight, gate, rounding and output, when the launch has one; a
+// negative value takes each dtype from the arguments at run time instead.
+// The fixed forms fold every dtype decision at compile time.
+constexpr int kRuntimeDtype = -1;
+
+template <NormKind KIND, int LPR, int IT, int XDT, int ODT>
 __global__ void __launch_bounds__(kNormThreads) norm_kernel(NormArgs a) {
   constexpr int kRowsPerBlock = kNormThreads / LPR;
+  const int xdt = XDT >= 0 ? XDT : a.in_dt;
+  const int wdt = ODT >= 0 ? ODT : a.weight_dt;
+  const int gdt = ODT >= 0 ? ODT : a.gate_dt;
+  const int rdt = ODT >= 0 ? ODT : a.round_dt;
+  const int odt = ODT >= 0 ? ODT : a.out_dt;
   const int lane = static_cast<int>(threadIdx.x) % LPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / LPR;
   if (row >= a.rows) return;  // uniform per row group; the butterfly stays within it
@@ -144,19 +152,24 @@ __global__ void __launch_bounds__(kNormThreads) norm_kernel(NormArgs a) {
   const int64_t first = row * chunks;
 
   // every load of the row first: input (and delta / gate), then the weight
-  Chunk cx[IT], cd[IT], cw[IT];
+  // (wide rows load the weight after the reduction, which keeps them in
+  // registers)
+  constexpr bool kEarlyWeight = IT <= 8;
+  Chunk cx[IT], cd[IT], cw[kEarlyWeight ? IT : 1];
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int64_t c = lane + static_cast<int64_t>(LPR) * i;
     const int64_t cc = c < chunks ? c : 0;
-    cx[i] = load_chunk(a.x, first + cc, a.in_dt);
-    if constexpr (KIND == NormKind::Add) cd[i] = load_chunk(a.delta, first + cc, a.in_dt);
-    if constexpr (KIND == NormKind::Gated) cd[i] = load_chunk(a.gate, first + cc, a.gate_dt);
+    cx[i] = load_chunk(a.x, first + cc, xdt);
+    if constexpr (KIND == NormKind::Add) cd[i] = load_chunk(a.delta, first + cc, xdt);
+    if constexpr (KIND == NormKind::Gated) cd[i] = load_chunk(a.gate, first + cc, gdt);
   }
+  if constexpr (kEarlyWeight) {
 #pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    const int64_t c = lane + static_cast<int64_t>(LPR) * i;
-    cw[i] = load_chunk(a.weight, c < chunks ? c : 0, a.weight_dt);
+    for (int i = 0; i < IT; ++i) {
+      const int64_t c = lane + static_cast<int64_t>(LPR) * i;
+      cw[i] = load_chunk(a.weight, c < chunks ? c : 0, wdt);
+    }
   }
 
   float v[IT][8];
@@ -164,17 +177,17 @@ __global__ void __launch_bounds__(kNormThreads) norm_kernel(NormArgs a) {
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const bool ok = lane + static_cast<int64_t>(LPR) * i < chunks;
-    unpack_chunk(cx[i], a.in_dt, v[i]);
+    unpack_chunk(cx[i], xdt, v[i]);
     if constexpr (KIND == NormKind::Add) {
       float d[8];
-      unpack_chunk(cd[i], a.in_dt, d);
+      unpack_chunk(cd[i], xdt, d);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[i][j] = round_to(v[i][j] + d[j], a.in_dt);
-      if (ok) store_chunk(a.sum_out, first + lane + static_cast<int64_t>(LPR) * i, a.in_dt, v[i]);
+      for (int j = 0; j < 8; ++j) v[i][j] = round_to(v[i][j] + d[j], xdt);
+      if (ok) store_chunk(a.sum_out, first + lane + static_cast<int64_t>(LPR) * i, xdt, v[i]);
     }
     if constexpr (KIND == NormKind::Gated) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[i][j] = round_to(v[i][j], a.round_dt);
+      for (int j = 0; j < 8; ++j) v[i][j] = round_to(v[i][j], rdt);
     }
     float part = sq;
 #pragma unroll
@@ -188,10 +201,14 @@ __global__ void __launch_bounds__(kNormThreads) norm_kernel(NormArgs a) {
     const int64_t c = lane + static_cast<int64_t>(LPR) * i;
     if (c >= chunks) continue;
     float w[8], out[8];
-    unpack_chunk(cw[i], a.weight_dt, w);
+    if constexpr (kEarlyWeight) {
+      unpack_chunk(cw[i], wdt, w);
+    } else {
+      unpack_chunk(load_chunk(a.weight, c, wdt), wdt, w);
+    }
     if constexpr (KIND == NormKind::Gated) {
       float g[8];
-      unpack_chunk(cd[i], a.gate_dt, g);
+      unpack_chunk(cd[i], gdt, g);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float sig = 1.0f / (1.0f + expf(-g[j]));
@@ -199,20 +216,28 @@ __global__ void __launch_bounds__(kNormThreads) norm_kernel(NormArgs a) {
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) out[j] = w[j] * round_to(v[i][j] * r, a.round_dt);
+      for (int j = 0; j < 8; ++j) out[j] = w[j] * round_to(v[i][j] * r, rdt);
     }
-    store_chunk(a.y, first + c, a.out_dt, out);
+    store_chunk(a.y, first + c, odt, out);
   }
 }
 
-template <NormKind KIND, int LPR>
-int launch_it(const NormArgs& a, int64_t its, hipStream_t s) {
-  constexpr int kRowsPerBlock = kNormThreads / LPR;
-  const dim3 grid(static_cast<unsigned>((a.rows + kRowsPerBlock - 1) / kRowsPerBlock));
-#define LK_NORM_CASE(N)                                              \
-  if (its <= N) {                                                    \
-    norm_kernel<KIND, LPR, N><<<grid, kNormThreads, 0, s>>>(a);      \
-    return check_launch("norm_kernel");                              \
+// rows of up to 16 chunks take 16 lanes each (4 rows per wave); wider rows a
+// whole wave, IT chunks per lane
+template <NormKind KIND, int XDT, int ODT>
+int launch_width(const NormArgs& a, hipStream_t s) {
+  const int64_t chunks = a.width / 8;
+  if (chunks <= 16) {
+    const dim3 grid(static_cast<unsigned>((a.rows + kNormThreads / 16 - 1) / (kNormThreads / 16)));
+    norm_kernel<KIND, 16, 1, XDT, ODT><<<grid, kNormThreads, 0, s>>>(a);
+    return check_launch("norm_kernel");
+  }
+  const int64_t its = (chunks + 63) / 64;
+  const dim3 grid(static_cast<unsigned>((a.rows + kNormThreads / 64 - 1) / (kNormThreads / 64)));
+#define LK_NORM_CASE(N)                                               \
+  if (its <= N) {                                                     \
+    norm_kernel<KIND, 64, N, XDT, ODT><<<grid, kNormThreads, 0, s>>>(a); \
+    return check_launch("norm_kernel");                               \
   }
   LK_NORM_CASE(1)
   LK_NORM_CASE(2)
@@ -229,9 +254,19 @@ int launch_it(const NormArgs& a, int64_t its, hipStream_t s) {
 
 template <NormKind KIND>
 int launch_norm(const NormArgs& a, hipStream_t s) {
-  const int64_t chunks = a.width / 8;
-  if (chunks <= 16) return launch_it<KIND, 16>(a, 1, s);
-  return launch_it<KIND, 64>(a, (chunks + 63) / 64, s);
+  const bool one_out = a.weight_dt == a.round_dt && a.out_dt == a.round_dt &&
+                       (KIND != NormKind::Gated || a.gate_dt == a.round_dt);
+  if (one_out && a.in_dt == a.round_dt) {
+    if (a.in_dt == LK_DTYPE_BF16) return launch_width<KIND, LK_DTYPE_BF16, LK_DTYPE_BF16>(a, s);
+    if (a.in_dt == LK_DTYPE_F16) return launch_width<KIND, LK_DTYPE_F16, LK_DTYPE_F16>(a, s);
+    if (a.in_dt == LK_DTYPE_F32) return launch_width<KIND, LK_DTYPE_F32, LK_DTYPE_F32>(a, s);
+  }
+  if constexpr (KIND == NormKind::Gated) {
+    // fp32 values rounded to bf16 before the norm (the KDA output projection's input)
+    if (one_out && a.in_dt == LK_DTYPE_F32 && a.round_dt == LK_DTYPE_BF16)
+      return launch_width<KIND, LK_DTYPE_F32, LK_DTYPE_BF16>(a, s);
+  }
+  return launch_width<KIND, kRuntimeDtype, kRuntimeDtype>(a, s);
 }
 
 bool norm_dtype(int d) { return d == LK_DTYPE_F32 || d == LK_DTYPE_F16 || d == LK_DTYPE_BF16; }
