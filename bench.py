@@ -341,6 +341,7 @@ def run_moe_decode(plan: Plan, dev, banks, cpu: bool) -> dict:
     step_bytes = (TOP_K + 1) * EXPERT_BYTES + TOKEN_IO_BYTES
     gu_bytes = (TOP_K + 1) * GATEUP_EXPERT_BYTES + H * 2 + E_ROUTED * 4 + (TOP_K + 1) * INTER * 2
     traffic = measured_traffic("moe_gateup_ksplit_kernel")
+    prof_us = rocprof_avg_us("moe_decode", "moe_gateup_ksplit_kernel")
     log(f"[bench] config 2: block {blk['us']:.2f} us/token, gate/up kernel {gu['us']:.2f} us")
     res = {
         "value": round(blk["us"], 3), "unit": "us/token", "steps": blk["steps"],
@@ -354,7 +355,11 @@ def run_moe_decode(plan: Plan, dev, banks, cpu: bool) -> dict:
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gu_bytes / (gu["us"] * 1e3) / HBM_PEAK_GBPS, 4),
                      "traffic": traffic, "bytes_per_launch": gu_bytes,
-                     "avg_launch_us": round(gu["us"], 3)},
+                     "avg_launch_us": round(gu["us"], 3),
+                     # the same kernel's average dispatch in the committed rocprofv3 trace
+                     "rocprof_avg_launch_us": prof_us,
+                     "frac_at_rocprof_avg": (round(gu_bytes / (prof_us * 1e3) / HBM_PEAK_GBPS, 4)
+                                             if prof_us else None)},
     }
     if cpu:
         log("[bench] config 2: CPU baseline")
@@ -433,7 +438,10 @@ def run_moe_batched(plan: Plan, dev, banks, m: int, weights: str, cpu: bool) -> 
                    "mean_distinct_routed_experts": round(float(np.mean(unions)), 2)},
         "roofline": {"kernel": "whole block (router, schedule, expert GEMMs, combine)",
                      "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": measured_traffic(
+                         f"whole block (moe_batched_decode_m{m}"
+                         f"{', mxfp4' if weights == 'mxfp4' else ''})"),
                      "bytes_per_step": int(step_bytes)},
     }
     if cpu:
@@ -475,8 +483,10 @@ def run_moe_prefill(plan: Plan, dev, banks, weights: str, cpu: bool) -> dict:
         "pct_hbm_peak": round(100 * nbytes / (t["us"] * 1e3) / HBM_PEAK_GBPS, 2),
         "roofline": {"kernel": "whole block (router, schedule, gate/up GEMM, down GEMM, combine)",
                      "bound": "mfma", "achieved": round(tflops, 1), "peak": peak,
-                     "unit": "TFLOP/s", "frac": round(tflops / peak, 4), "traffic": None,
-                     "flops_per_step": flops,
+                     "unit": "TFLOP/s", "frac": round(tflops / peak, 4),
+                     "traffic": measured_traffic(
+                         f"whole block (moe_prefill_{m}{', mxfp4' if weights == 'mxfp4' else ''})"),
+                     "algorithmic_bytes_per_step": nbytes, "flops_per_step": flops,
                      "frac_of_fp4_peak": round(tflops / FP4_PEAK_TFLOPS, 4)},
     }
     if cpu:
@@ -514,7 +524,9 @@ def run_qkv_prefill(plan: Plan, dev, cpu: bool) -> dict:
         "roofline": {"kernel": "w4a16_stream_kernel (dense, three outputs in one launch)",
                      "bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None, "flops_per_launch": flops, "avg_launch_us": round(t["us"], 2)},
+                     "traffic": measured_traffic(f"w4a16_stream_kernel (qkv_prefill_{m})"),
+                     "algorithmic_bytes_per_launch": 3 * w4a16_bytes(n, H) + m * H * 2 + 3 * m * n * 2,
+                     "flops_per_launch": flops, "avg_launch_us": round(t["us"], 2)},
     }
     if cpu:
         threads = cpu_threads()
@@ -693,7 +705,9 @@ def run_norm_decode(plan: Plan, dev, cpu: bool) -> dict:
         "prefill_add_rms_norm_us": round(t_pre["us"], 3),
         "roofline": {"kernel": "norm_kernel (add + RMSNorm, 2048 x 2304 prefill rows)",
                      "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": measured_traffic(
+                         "norm_kernel (add + RMSNorm, 2048 x 2304 prefill rows)"),
                      "bytes_per_launch": pre_bytes, "avg_launch_us": round(t_pre["us"], 3)},
     }
     if cpu:
@@ -776,12 +790,25 @@ def run_floor(plan: Plan, dev, banks) -> dict:
 
 
 def measured_traffic(kernel: str):
-    """HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (profiles/traffic.json)."""
+    """HBM bytes per launch (or per step, for a whole block) from rocprofv3
+    FETCH_SIZE + WRITE_SIZE, copy-calibrated (profiles/traffic.json)."""
     try:
         with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
             return int(json.load(f)["kernels"][kernel]["traffic_bytes"])
     except (OSError, KeyError, ValueError):
         return None
+
+
+def rocprof_avg_us(run: str, kernel: str, grid: str | None = None):
+    """Average dispatch duration of a kernel in the committed rocprofv3 trace
+    of a bench run (profiles/kernel_times.json), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "kernel_times.json")) as f:
+            rows = json.load(f)["runs"][run]["kernels"]
+    except (OSError, KeyError, ValueError):
+        return None
+    hits = [r for r in rows if kernel in r["kernel"] and (grid is None or r["grid"] == grid)]
+    return hits[0]["avg_us"] if len(hits) == 1 else None
 
 
 def run_copy(dev) -> dict:
@@ -909,6 +936,7 @@ def main() -> int:
                              lambda: run_moe_prefill(plan, dev, mx, "mxfp4", False))):
                 configs[key] = fn()
                 configs[key]["config"]["mfma_form"] = "fp4 (scaled f8f6f4, fp8 hi/lo activations)"
+                configs[key]["roofline"]["traffic"] = None  # counted for the default form only
         res["configs"] = configs
         floor = res["floor"]
         res["roofline"]["frac_of_measured_floor"] = round(
@@ -1059,7 +1087,8 @@ def run_kda_decode(plan: Plan, dev, cpu: bool) -> dict:
                      "achieved": round(layer_bytes / (one["us"] * 1e3), 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s",
                      "frac": round(layer_bytes / (one["us"] * 1e3) / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "bytes_per_launch": layer_bytes,
+                     "traffic": measured_traffic("kda_layer_split_kernel"),
+                     "bytes_per_launch": layer_bytes,
                      "avg_launch_us": round(one["us"], 3),
                      "step_kernel_gbps": round(step_bytes / (st["us"] * 1e3), 1)},
     }
