@@ -1528,10 +1528,24 @@ w4a16_stream_kernel(const GemmArgs g) {
 
   const int per_tile = g.col_blocks * g.outputs;
   const int id = blockIdx.x;
-  const int grp = id / (8 * per_tile);
-  const int rem = id - grp * 8 * per_tile;
-  const int tile = grp * 8 + (rem & 7);
-  const int cb_all = rem >> 3;
+  int tile, cb_all;
+  if (DENSE && per_tile % 8 == 0) {
+    // dense products: XCD x (block ids are dealt round robin to the 8 XCDs)
+    // takes the band of per_tile / 8 column blocks from x * band and walks the
+    // row tiles with it, so the band's weights stay in that XCD's L2 while
+    // each row tile is read once per XCD (tile-major within the band keeps
+    // the blocks in flight on a few row tiles)
+    const int band = per_tile >> 3;
+    const int j = id >> 3;
+    tile = j / band;
+    cb_all = (id & 7) * band + (j - tile * band);
+  } else {
+    // a tile's column blocks sit on one XCD
+    const int grp = id / (8 * per_tile);
+    const int rem = id - grp * 8 * per_tile;
+    tile = grp * 8 + (rem & 7);
+    cb_all = rem >> 3;
+  }
   const int osel = cb_all / g.col_blocks;
   const int cb = cb_all - osel * g.col_blocks;
   int expert, row0, rows;

@@ -163,7 +163,8 @@ def test_decode_fused_qkv_is_one_launch_at_the_kda_shape(rng, m):
 
 
 @pytest.mark.parametrize("m,n,k", [(16, 256, 512), (100, 384, 1024), (130, 256, 2304),
-                                   (2048, 512, 2304)])
+                                   (2048, 512, 2304),
+                                   (200, 2048, 512)])  # column blocks a multiple of 8: XCD bands
 def test_direct_load_dense_forms_match_the_staged_forms(rng, m, n, k):
     """The workspace entry points (rows paired by a pre-pass, loaded straight
     into LDS) against the entry points without a workspace (rows staged through
