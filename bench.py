@@ -734,19 +734,21 @@ def run_floor(plan: Plan, dev, banks) -> dict:
     the gate/up weights the batched-decode expert GEMMs read at 16 and 64
     tokens (the mean distinct experts of the Zipf routing, plus the shared
     expert; one contiguous region, four copies rotated)."""
-    from local_kimi_amd import _lib
-
-    lib = _lib.load()
+    lib = load_probe_library()
     stream = torch.cuda.Stream(device=dev)
     sink = torch.zeros(256, dtype=torch.int32, device=dev)
     s_ptr = stream.cuda_stream
 
+    def checked(rc):
+        if rc != 0:
+            raise RuntimeError(f"probe failed ({rc}): {lib.lk_probe_last_error().decode()}")
+
     def probe(regions):
         ptrs = (ctypes.c_void_p * len(regions))(*[r.data_ptr() for r in regions])
         sizes = (ctypes.c_int64 * len(regions))(*[r.numel() * r.element_size() for r in regions])
-        _lib.call("lk_probe_stream_read", ptrs, sizes, len(regions), sink.data_ptr(), s_ptr)
+        checked(lib.lk_probe_stream_read(ptrs, sizes, len(regions), sink.data_ptr(), s_ptr))
 
-    empty = time_steps(lambda i: lib.lk_probe_empty(s_ptr), 100, stream, plan)
+    empty = time_steps(lambda i: checked(lib.lk_probe_empty(s_ptr)), 100, stream, plan)
     # one MoE layer's matrices: 9 experts x (gate, up, down) packed weights + scales, per layer
     rng = np.random.default_rng(5)
     layer_sets = []
@@ -787,6 +789,23 @@ def run_floor(plan: Plan, dev, banks) -> dict:
             "read_moe_layer_us": round(moe["us"], 3), "read_moe_layer_bytes": layer_bytes,
             "read_moe_layer_gbps": round(layer_bytes / (moe["us"] * 1e3), 1),
             "kernel": "stream_read_kernel (16-byte non-temporal loads, one launch per step)"}
+
+
+def load_probe_library() -> ctypes.CDLL:
+    """The measurement probes (local_kimi_amd/liblkprobe.so, include/lk_probe.h),
+    built beside the product library but not part of it."""
+    path = os.path.join(ROOT, "local_kimi_amd", "liblkprobe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run python -m local_kimi_amd._build")
+    lib = ctypes.CDLL(path)
+    P = ctypes.c_void_p
+    lib.lk_probe_stream_read.argtypes = [P, P, ctypes.c_int, P, P]
+    lib.lk_probe_stream_read.restype = ctypes.c_int
+    lib.lk_probe_empty.argtypes = [P]
+    lib.lk_probe_empty.restype = ctypes.c_int
+    lib.lk_probe_last_error.argtypes = []
+    lib.lk_probe_last_error.restype = ctypes.c_char_p
+    return lib
 
 
 def measured_traffic(kernel: str):

@@ -409,19 +409,6 @@ LK_API int lk_mxfp4_expert_mlp(const uint16_t* x, const uint8_t* w1_packed,
                                int64_t m, int64_t h, int64_t i, float situ_beta,
                                float situ_linear_beta, void* stream);
 
-/* ---- measurement probes (no reference counterpart): the floors the decode
- * kernels are measured against (bench.py --workload stream_floor).
- * lk_probe_stream_read reads `count` (1..32) device regions once with 16-byte
- * non-temporal loads, one launch; regions and bytes are HOST arrays of device
- * pointers and byte counts (each region 16-byte aligned, a positive multiple
- * of 16 bytes); sink is device memory of 256 uint32 words, written only in the
- * practically impossible case that a thread's folded words equal a fixed
- * value (it keeps the loads live). lk_probe_empty launches an empty kernel
- * (one wave). */
-LK_API int lk_probe_stream_read(const void* const* regions, const int64_t* bytes, int count,
-                                uint32_t* sink, void* stream);
-LK_API int lk_probe_empty(void* stream);
-
 #ifdef __cplusplus
 }
 #endif

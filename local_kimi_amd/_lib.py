@@ -78,8 +78,6 @@ SIGNATURES: dict[str, list] = {
     "lk_rms_norm": [_P, _P, _P, _I64, _I64, _F, _I, _I, _P],
     "lk_add_rms_norm": [_P, _P, _P, _P, _P, _I64, _I64, _F, _I, _I, _P],
     "lk_rms_gated_norm": [_P, _P, _P, _P, _I64, _I64, _F, _I, _I, _I, _I, _P],
-    "lk_probe_stream_read": [_P, _P, _I, _P, _P],
-    "lk_probe_empty": [_P],
 }
 
 # name -> argument types of the size queries (they return int64, -1 on bad input)

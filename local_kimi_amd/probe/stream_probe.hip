@@ -10,10 +10,44 @@
 // The read kernel folds what it loads into one word per thread and stores it
 // only if it equals a value no input produces in practice, so the loads stay
 // live without adding write traffic.
+//
+// This file builds into its own library (liblkprobe.so), apart from the
+// product library, so it keeps its own error state.
+
+#include <stdarg.h>
+#include <stdio.h>
 
 #include "lk_common.hpp"
+#include "lk_probe.h"
 
 namespace lk {
+
+static thread_local char g_probe_error[256] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_probe_error, sizeof(g_probe_error), fmt, ap);
+  va_end(ap);
+}
+
+int fail_arg(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_probe_error, sizeof(g_probe_error), fmt, ap);
+  va_end(ap);
+  return LK_ERR_ARGUMENT;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: kernel launch failed: %s", what, hipGetErrorString(e));
+    return LK_ERR_HIP;
+  }
+  return LK_OK;
+}
+
 namespace {
 
 constexpr int kProbeRegions = 32;
@@ -86,5 +120,7 @@ int lk_probe_empty(void* stream) {
   empty_kernel<<<1, kWave, 0, as_stream(stream)>>>();
   return check_launch("lk_probe_empty");
 }
+
+const char* lk_probe_last_error(void) { return lk::g_probe_error; }
 
 }  // extern "C"

@@ -14,10 +14,13 @@ from local_kimi_amd import _lib
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def _declared() -> list[str]:
+PROBE_HEADER = "lk_probe.h"  # the benchmark's probe library, not the product library
+
+
+def _declared(probe: bool = False) -> list[str]:
     names = []
     for header in os.listdir(os.path.join(ROOT, "include")):
-        if header.endswith(".h"):
+        if header.endswith(".h") and (header == PROBE_HEADER) == probe:
             text = open(os.path.join(ROOT, "include", header)).read()
             names += re.findall(r"LK_API\s+[\w\s\*]+?\b(lk_\w+)\s*\(", text)
     return sorted(set(names))
@@ -39,6 +42,24 @@ def test_header_declares_the_entry_points_the_binding_uses():
 def test_library_exports_every_declared_symbol(lib):
     for name in _declared():
         assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
+
+
+def test_probe_library_is_separate_and_exports_its_symbols(lib):
+    path = os.path.join(ROOT, "local_kimi_amd", "liblkprobe.so")
+    if not os.path.exists(path):
+        pytest.skip("probe library not built")
+    probe = ctypes.CDLL(path)
+    names = _declared(probe=True)
+    assert names == ["lk_probe_empty", "lk_probe_last_error", "lk_probe_stream_read"]
+    for name in names:
+        assert isinstance(getattr(probe, name), ctypes._CFuncPtr), name
+        with pytest.raises(AttributeError):
+            getattr(lib, name)  # the product library does not carry the probes
+    probe.lk_probe_stream_read.restype = ctypes.c_int
+    probe.lk_probe_last_error.restype = ctypes.c_char_p
+    # argument errors are reported on the host, before any launch
+    assert probe.lk_probe_stream_read(None, None, 0, None, None) == 1
+    assert b"null pointer" in probe.lk_probe_last_error()
 
 
 def test_abi_version_and_error_string(lib):

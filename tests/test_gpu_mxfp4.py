@@ -233,7 +233,10 @@ def test_moe_block_full_size(rng, kimi_mx_banks, tokens, zipf):
     x = random_bf16_bits(rng, (tokens, 2304))
     logits = (zipf_router_logits if zipf else normal_router_logits)(rng, tokens, 256)
     y, idx, _ = mxfp4_moe_block(_dev(x), _dev(logits), None, *kimi_mx_banks, 8, 2.446)
-    sel = np.unique(rng.choice(tokens, size=6, replace=False))
+    # 64 tokens: every token against the oracle; 2048 tokens: 6 sampled (the
+    # designed-bank prefill tests check every token)
+    sel = (np.arange(tokens) if tokens <= 64
+           else np.unique(rng.choice(tokens, size=6, replace=False)))
     eidx, ew = OM.route(logits[sel], None, 8, routed_scaling_factor=2.446)
     assert np.array_equal(idx.cpu().numpy()[sel], eidx)
     e_total = 257
@@ -246,6 +249,7 @@ def test_moe_block_full_size(rng, kimi_mx_banks, tokens, zipf):
                    sub[5]).reshape(len(sel), 9, -1)
     cw = np.concatenate((ew, np.ones((len(sel), 1), np.float32)), 1)
     worst = assert_close_bf16(to_bits(y)[sel], OM.combine(eo, cw), what=f"mxfp4 block T={tokens}")
+    print(f"mxfp4 block T={tokens}: {sel.size} tokens checked, worst {worst:.3f} of the tolerance")
     assert worst < 0.75
 
 
