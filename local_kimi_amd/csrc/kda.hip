@@ -155,6 +155,14 @@ __device__ inline float load_value(const void* p, int64_t i, int dtype) {
   return static_cast<float>(__builtin_bit_cast(_Float16, b));
 }
 
+// one of the first two pointers of an argument triple, without indexing the
+// kernel arguments by a per-thread value (which would load the pointer from
+// memory before the data it points to)
+template <typename T>
+__device__ inline T pick2(const T (&v)[3], int i) {
+  return i ? v[1] : v[0];
+}
+
 __device__ inline void store_value(void* p, int64_t i, float x, int dtype) {
   if (dtype == LK_DTYPE_F32) {
     static_cast<float*>(p)[i] = x;
@@ -492,7 +500,7 @@ struct ConvChannel {
     w2 = load_as<WDT>(weight, wi + 2);
     w3 = load_as<WDT>(weight, wi + 3);
   }
-  __device__ inline float apply(void* state_out, int64_t si, bool write) const {
+  __device__ inline float apply() const {
     float acc = s1 * w0;
     acc += s2 * w1;
     acc += s3 * w2;
@@ -500,20 +508,27 @@ struct ConvChannel {
     float y = acc / (1.0f + expf(-acc));
     if constexpr (VDT == LK_DTYPE_BF16) y = round_bf16(y);
     else if constexpr (VDT == LK_DTYPE_F16) y = static_cast<float>(static_cast<_Float16>(y));
-    if (write) {
-      store_value(state_out, si + 0, s1, VDT);
-      store_value(state_out, si + 1, s2, VDT);
-      store_value(state_out, si + 2, s3, VDT);
-      store_value(state_out, si + 3, token, VDT);
-    }
     return y;
+  }
+  // the shifted window, issued at the end of the kernel: a store among the
+  // preparation's loads would make every later wait on those loads count it
+  __device__ inline void store_shifted(void* state_out, int64_t si) const {
+    store_value(state_out, si + 0, s1, VDT);
+    store_value(state_out, si + 1, s2, VDT);
+    store_value(state_out, si + 2, s3, VDT);
+    store_value(state_out, si + 3, token, VDT);
   }
 };
 
-template <int VDT, int WDT>
+// GATES_AS_VALUES: the raw decay and beta are stored in the value dtype (the
+// common case), fixed at compile time so that no dtype branch splits the
+// preparation's loads; otherwise ddt and bdt are taken at run time.
+template <int VDT, int WDT, bool GATES_AS_VALUES>
 __global__ void __launch_bounds__(kSplitThreads)
 kda_layer_split_kernel(const SplitArgs a, int heads, int dim, int vs, int64_t items, int paired,
-                       float eps, float scale, int ddt, int bdt) {
+                       float eps, float scale, int ddt_arg, int bdt_arg) {
+  const int ddt = GATES_AS_VALUES ? VDT : ddt_arg;
+  const int bdt = GATES_AS_VALUES ? VDT : bdt_arg;
   __shared__ float qk[2][kLayerMaxDim];
   __shared__ float vcol[kSplitCols];
   __shared__ float gain[kLayerMaxDim];
@@ -537,24 +552,12 @@ kda_layer_split_kernel(const SplitArgs a, int heads, int dim, int vs, int64_t it
   const bool cols = c0 < dim;  // dim % 4 == 0 (host-checked)
   float* const s_head = a.state + bh * dim * dim;
 
-  // 1. this thread's state rows, before anything else
-  float s[4][4];
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int i = rg + kSplitRowGroups * p;
-    if (cols && i < dim) {
-      const float4 x = *reinterpret_cast<const float4*>(s_head + static_cast<int64_t>(i) * dim + c0);
-      s[p][0] = x.x;
-      s[p][1] = x.y;
-      s[p][2] = x.z;
-      s[p][3] = x.w;
-    } else {
-      s[p][0] = s[p][1] = s[p][2] = s[p][3] = 0.f;
-    }
-  }
-  // 2. every load of the preparation in one batch: the q and k convolution
+  // 1. every load of the preparation in one batch: the q and k convolution
   // channels of the head (thread t takes channels t and t + 128 of the 2 * dim),
-  // the v channel of this block's column t, the gate inputs of row t
+  // the v channel of this block's column t, the gate inputs of row t. They go
+  // out before the state rows: loads retire in issue order, so the
+  // preparation below waits only for its own inputs and runs while the
+  // state (the bulk of the bytes, from HBM) is still arriving.
   ConvChannel<VDT, WDT> cc[3];
   int conv_of[2], j_of[2];
   bool live[3];
@@ -566,7 +569,8 @@ kda_layer_split_kernel(const SplitArgs a, int heads, int dim, int vs, int64_t it
     conv_of[q] = uc >= dim ? 1 : 0;
     j_of[q] = uc - conv_of[q] * dim;
     const int64_t ch = static_cast<int64_t>(h) * dim + j_of[q];
-    cc[q].load(a.conv_in[conv_of[q]], a.in[conv_of[q]], a.conv_weight[conv_of[q]],
+    cc[q].load(pick2(a.conv_in, conv_of[q]), pick2(a.in, conv_of[q]),
+               pick2(a.conv_weight, conv_of[q]),
                (b * channels + ch) * 4, b * channels + ch, ch * 4);
   }
   const int vj = y * kSplitCols + t;
@@ -578,15 +582,27 @@ kda_layer_split_kernel(const SplitArgs a, int heads, int dim, int vs, int64_t it
   const float raw = load_value(a.raw_decay, bh * dim + (grow ? t : 0), ddt);
   const float dtb = a.dt_bias[h * dim + (grow ? t : 0)];
   const float alog = a.a_log[h];
-  const float rbeta = t == 0 ? load_value(a.raw_beta, bh, bdt) : 0.f;
+  const float rbeta_all = load_value(a.raw_beta, bh, bdt);  // every thread: no branch
+  const float rbeta = t == 0 ? rbeta_all : 0.f;
+  // 2. this thread's state rows, every load unconditional (rows or columns
+  // past the head read its first four values and are zeroed): the wait for
+  // a preparation input then counts only the loads issued after it
+  float s[4][4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int i = rg + kSplitRowGroups * p;
+    const bool ok = cols && i < dim;
+    const float4 x = *reinterpret_cast<const float4*>(
+        s_head + (ok ? static_cast<int64_t>(i) * dim + c0 : 0));
+    s[p][0] = ok ? x.x : 0.f;
+    s[p][1] = ok ? x.y : 0.f;
+    s[p][2] = ok ? x.z : 0.f;
+    s[p][3] = ok ? x.w : 0.f;
+  }
 #pragma unroll
   for (int q = 0; q < 2; ++q)
-    if (live[q])
-      qk[conv_of[q]][j_of[q]] = cc[q].apply(a.conv_out[conv_of[q]],
-                                            (b * channels + static_cast<int64_t>(h) * dim +
-                                             j_of[q]) * 4,
-                                            y == 0);
-  if (live[2]) vcol[t] = cc[2].apply(a.conv_out[2], (b * channels + vch) * 4, true);
+    if (live[q]) qk[conv_of[q]][j_of[q]] = cc[q].apply();
+  if (live[2]) vcol[t] = cc[2].apply();
   // 3. exp(decay) of every row, beta
   if (grow) gain[t] = expf(-expf(alog) * softplus_f32(raw + dtb));
   if (t == 0) beta_s = 1.0f / (1.0f + expf(-rbeta));
@@ -659,15 +675,27 @@ kda_layer_split_kernel(const SplitArgs a, int heads, int dim, int vs, int64_t it
     o[c] = part;
   }
   reduce(o);
-  if (!cols) return;
+  if (cols) {
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int i = rg + kSplitRowGroups * p;
-    if (i < dim)
-      *reinterpret_cast<float4*>(s_head + static_cast<int64_t>(i) * dim + c0) =
-          make_float4(s[p][0], s[p][1], s[p][2], s[p][3]);
+    for (int p = 0; p < 4; ++p) {
+      const int i = rg + kSplitRowGroups * p;
+      if (i < dim)
+        *reinterpret_cast<float4*>(s_head + static_cast<int64_t>(i) * dim + c0) =
+            make_float4(s[p][0], s[p][1], s[p][2], s[p][3]);
+    }
+    if (rg == 0)
+      *reinterpret_cast<float4*>(a.out + bh * dim + c0) = make_float4(o[0], o[1], o[2], o[3]);
   }
-  if (rg == 0) *reinterpret_cast<float4*>(a.out + bh * dim + c0) = make_float4(o[0], o[1], o[2], o[3]);
+  // the shifted conv windows into the second state set: q and k channels
+  // from column block 0 of a head, each block its own v columns
+  if (y == 0) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      if (live[q])
+        cc[q].store_shifted(pick2(a.conv_out, conv_of[q]),
+                            (b * channels + static_cast<int64_t>(h) * dim + j_of[q]) * 4);
+  }
+  if (live[2]) cc[2].store_shifted(a.conv_out[2], (b * channels + vch) * 4);
 }
 
 bool valid_dtype(int d) { return d == LK_DTYPE_F32 || d == LK_DTYPE_F16 || d == LK_DTYPE_BF16; }
@@ -811,10 +839,16 @@ int lk_kda_decode_layer_split(const void* q_in, const void* k_in, const void* v_
   const int nh = static_cast<int>(heads), nd = static_cast<int>(head_dim),
             nvs = static_cast<int>(vs);
   hipStream_t s = as_stream(stream);
-#define LK_KDA_SPLIT(V, W)                                                                 \
-  kda_layer_split_kernel<V, W><<<grid, kSplitThreads, 0, s>>>(a, nh, nd, nvs, items, paired, \
-                                                              eps, scale, decay_dtype,       \
-                                                              beta_dtype)
+  const bool gates_as_values = decay_dtype == value_dtype && beta_dtype == value_dtype;
+#define LK_KDA_SPLIT(V, W)                                                                   \
+  do {                                                                                       \
+    if (gates_as_values)                                                                     \
+      kda_layer_split_kernel<V, W, true><<<grid, kSplitThreads, 0, s>>>(                     \
+          a, nh, nd, nvs, items, paired, eps, scale, decay_dtype, beta_dtype);               \
+    else                                                                                     \
+      kda_layer_split_kernel<V, W, false><<<grid, kSplitThreads, 0, s>>>(                    \
+          a, nh, nd, nvs, items, paired, eps, scale, decay_dtype, beta_dtype);               \
+  } while (0)
 #define LK_KDA_SPLIT_W(V)                                             \
   do {                                                                \
     if (weight_dtype == LK_DTYPE_F32) LK_KDA_SPLIT(V, LK_DTYPE_F32);  \
