@@ -163,6 +163,11 @@ __device__ inline T pick2(const T (&v)[3], int i) {
   return i ? v[1] : v[0];
 }
 
+template <typename T>
+__device__ inline T pick3(const T (&v)[3], int i) {
+  return i == 0 ? v[0] : (i == 1 ? v[1] : v[2]);
+}
+
 __device__ inline void store_value(void* p, int64_t i, float x, int dtype) {
   if (dtype == LK_DTYPE_F32) {
     static_cast<float*>(p)[i] = x;
@@ -290,9 +295,62 @@ struct LayerArgs {
   float* out;
 };
 
+// storage of compile-time dtype DT (the split kernel's conv loads go out in
+// one batch only when no run-time dtype branch sits between them)
+template <int DT>
+__device__ inline float load_as(const void* p, int64_t i) {
+  if constexpr (DT == LK_DTYPE_F32) {
+    return static_cast<const float*>(p)[i];
+  } else if constexpr (DT == LK_DTYPE_BF16) {
+    return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  } else {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<const uint16_t*>(p)[i]));
+  }
+}
+
+// One width-4 convolution channel: the loads (window, token, weights) of
+// load(), then apply() (short_conv_kernel's arithmetic) and the shifted
+// window into state_out.
+template <int VDT, int WDT>
+struct ConvChannel {
+  float s1, s2, s3, token, w0, w1, w2, w3;
+  __device__ inline void load(const void* state_in, const void* in, const void* weight,
+                              int64_t si, int64_t xi, int64_t wi) {
+    s1 = load_as<VDT>(state_in, si + 1);
+    s2 = load_as<VDT>(state_in, si + 2);
+    s3 = load_as<VDT>(state_in, si + 3);
+    token = load_as<VDT>(in, xi);
+    w0 = load_as<WDT>(weight, wi + 0);
+    w1 = load_as<WDT>(weight, wi + 1);
+    w2 = load_as<WDT>(weight, wi + 2);
+    w3 = load_as<WDT>(weight, wi + 3);
+  }
+  __device__ inline float apply() const {
+    float acc = s1 * w0;
+    acc += s2 * w1;
+    acc += s3 * w2;
+    acc += token * w3;
+    float y = acc / (1.0f + expf(-acc));
+    if constexpr (VDT == LK_DTYPE_BF16) y = round_bf16(y);
+    else if constexpr (VDT == LK_DTYPE_F16) y = static_cast<float>(static_cast<_Float16>(y));
+    return y;
+  }
+  // the shifted window, issued at the end of the kernel: a store among the
+  // preparation's loads would make every later wait on those loads count it
+  __device__ inline void store_shifted(void* state_out, int64_t si) const {
+    store_value(state_out, si + 0, s1, VDT);
+    store_value(state_out, si + 1, s2, VDT);
+    store_value(state_out, si + 2, s3, VDT);
+    store_value(state_out, si + 3, token, VDT);
+  }
+};
+
+template <int VDT, int WDT, bool GATES_AS_VALUES>
 __global__ void __launch_bounds__(kLayerThreads)
-kda_layer_kernel(const LayerArgs a, int heads, int dim, float eps, float scale, int vdt,
-                 int wdt, int ddt, int bdt) {
+kda_layer_kernel(const LayerArgs a, int heads, int dim, float eps, float scale, int ddt_arg,
+                 int bdt_arg) {
+  const int ddt = GATES_AS_VALUES ? VDT : ddt_arg;
+  const int bdt = GATES_AS_VALUES ? VDT : bdt_arg;
   __shared__ float qkv[3][kLayerMaxDim];
   __shared__ float gain[kLayerMaxDim];  // exp(decay)
   __shared__ float norm[2];
@@ -308,57 +366,46 @@ kda_layer_kernel(const LayerArgs a, int heads, int dim, float eps, float scale, 
   const bool cols = c0 < dim;  // dim % 4 == 0 (host-checked)
   float* const s_head = a.state + bh * dim * dim;
 
-  // 1. the state rows of this thread (rows rg + 32 p), before anything else
+  // 1. every load of the preparation, before the state rows (loads retire in
+  // issue order, so the convolutions and gates wait only for their own
+  // inputs): thread t < 3 dim one convolution channel, t < dim the gate
+  // inputs of row t, every thread the beta input (no branch around a load)
+  const bool conv_live = t < 3 * dim;
+  const int tc = conv_live ? t : 0;
+  const int conv = tc / dim, j = tc - conv * dim;
+  const int64_t ch = static_cast<int64_t>(h) * dim + j;
+  const int64_t si = (b * channels + ch) * 4;
+  ConvChannel<VDT, WDT> cc;
+  cc.load(pick3(a.conv_state, conv), pick3(a.in, conv), pick3(a.conv_weight, conv), si,
+          b * channels + ch, ch * 4);
+  const bool grow = t < dim;
+  const float raw = load_value(a.raw_decay, bh * dim + (grow ? t : 0), ddt);
+  const float dtb = a.dt_bias[h * dim + (grow ? t : 0)];
+  const float alog = a.a_log[h];
+  const float rbeta = load_value(a.raw_beta, bh, bdt);
+
+  // 2. the state rows of this thread (rows rg + 32 p), every load
+  // unconditional (rows or columns past the head read its first values and
+  // are zeroed)
   float s[4][4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
     const int i = rg + kLayerRowGroups * p;
-    if (cols && i < dim) {
-      const float4 x = *reinterpret_cast<const float4*>(s_head + static_cast<int64_t>(i) * dim + c0);
-      s[p][0] = x.x;
-      s[p][1] = x.y;
-      s[p][2] = x.z;
-      s[p][3] = x.w;
-    } else {
-      s[p][0] = s[p][1] = s[p][2] = s[p][3] = 0.f;
-    }
+    const bool ok = cols && i < dim;
+    const float4 x = *reinterpret_cast<const float4*>(
+        s_head + (ok ? static_cast<int64_t>(i) * dim + c0 : 0));
+    s[p][0] = ok ? x.x : 0.f;
+    s[p][1] = ok ? x.y : 0.f;
+    s[p][2] = ok ? x.z : 0.f;
+    s[p][3] = ok ? x.w : 0.f;
   }
 
-  // 2. the three convolutions of this head's channels (as short_conv_kernel)
-  if (t < 3 * dim) {
-    const int conv = t / dim, j = t - conv * dim;
-    const int64_t ch = static_cast<int64_t>(h) * dim + j;
-    const int64_t si = (b * channels + ch) * 4;
-    const float s1 = load_value(a.conv_state[conv], si + 1, vdt);
-    const float s2 = load_value(a.conv_state[conv], si + 2, vdt);
-    const float s3 = load_value(a.conv_state[conv], si + 3, vdt);
-    const float token = load_value(a.in[conv], b * channels + ch, vdt);
-    const float w0 = load_value(a.conv_weight[conv], ch * 4 + 0, wdt);
-    const float w1 = load_value(a.conv_weight[conv], ch * 4 + 1, wdt);
-    const float w2 = load_value(a.conv_weight[conv], ch * 4 + 2, wdt);
-    const float w3 = load_value(a.conv_weight[conv], ch * 4 + 3, wdt);
-    float acc = s1 * w0;
-    acc += s2 * w1;
-    acc += s3 * w2;
-    acc += token * w3;
-    // the conv output rounded to the value dtype, then widened (as the
-    // reference's gates read their bf16 / fp16 inputs)
-    float y = acc / (1.0f + expf(-acc));
-    if (vdt == LK_DTYPE_BF16) y = round_bf16(y);
-    else if (vdt == LK_DTYPE_F16) y = static_cast<float>(static_cast<_Float16>(y));
-    qkv[conv][j] = y;
-    store_value(a.conv_state[conv], si + 0, s1, vdt);
-    store_value(a.conv_state[conv], si + 1, s2, vdt);
-    store_value(a.conv_state[conv], si + 2, s3, vdt);
-    store_value(a.conv_state[conv], si + 3, token, vdt);
-  }
-  // 3. decay (as kda_gates_kernel), kept as exp(decay) for the step
-  if (t < dim) {
-    const float rate = expf(a.a_log[h]);
-    const float biased = load_value(a.raw_decay, bh * dim + t, ddt) + a.dt_bias[h * dim + t];
-    gain[t] = expf(-rate * softplus_f32(biased));
-  }
-  if (t == 0) beta_s = 1.0f / (1.0f + expf(-load_value(a.raw_beta, bh, bdt)));
+  // 3. the three convolutions (as short_conv_kernel; the output rounded to the
+  // value dtype, as the reference's gates read their bf16 / fp16 inputs), the
+  // decay (as kda_gates_kernel) kept as exp(decay) for the step, and beta
+  if (conv_live) qkv[conv][j] = cc.apply();
+  if (grow) gain[t] = expf(-expf(alog) * softplus_f32(raw + dtb));
+  if (t == 0) beta_s = 1.0f / (1.0f + expf(-rbeta));
   __syncthreads();
   // 4. q and k norms: waves 0 and 1, the gates kernel's per-lane order
   if (t < 2 * kWave) {
@@ -426,15 +473,20 @@ kda_layer_kernel(const LayerArgs a, int heads, int dim, float eps, float scale, 
     o[c] = part;
   }
   reduce(o);
-  if (!cols) return;
+  if (cols) {
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int i = rg + kLayerRowGroups * p;
-    if (i < dim)
-      *reinterpret_cast<float4*>(s_head + static_cast<int64_t>(i) * dim + c0) =
-          make_float4(s[p][0], s[p][1], s[p][2], s[p][3]);
+    for (int p = 0; p < 4; ++p) {
+      const int i = rg + kLayerRowGroups * p;
+      if (i < dim)
+        *reinterpret_cast<float4*>(s_head + static_cast<int64_t>(i) * dim + c0) =
+            make_float4(s[p][0], s[p][1], s[p][2], s[p][3]);
+    }
+    if (rg == 0)
+      *reinterpret_cast<float4*>(a.out + bh * dim + c0) = make_float4(o[0], o[1], o[2], o[3]);
   }
-  if (rg == 0) *reinterpret_cast<float4*>(a.out + bh * dim + c0) = make_float4(o[0], o[1], o[2], o[3]);
+  // the shifted windows, in place: each channel is read and written by one
+  // thread of this block only
+  if (conv_live) cc.store_shifted(pick3(a.conv_state, conv), si);
 }
 
 // A decode layer over several blocks per head: block (b, h, y) owns value
@@ -470,55 +522,6 @@ struct SplitArgs {
   float* out;
 };
 
-// storage of compile-time dtype DT (the split kernel's conv loads go out in
-// one batch only when no run-time dtype branch sits between them)
-template <int DT>
-__device__ inline float load_as(const void* p, int64_t i) {
-  if constexpr (DT == LK_DTYPE_F32) {
-    return static_cast<const float*>(p)[i];
-  } else if constexpr (DT == LK_DTYPE_BF16) {
-    return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
-  } else {
-    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<const uint16_t*>(p)[i]));
-  }
-}
-
-// One width-4 convolution channel: the loads (window, token, weights) of
-// load(), then apply() (short_conv_kernel's arithmetic) and the shifted
-// window into state_out.
-template <int VDT, int WDT>
-struct ConvChannel {
-  float s1, s2, s3, token, w0, w1, w2, w3;
-  __device__ inline void load(const void* state_in, const void* in, const void* weight,
-                              int64_t si, int64_t xi, int64_t wi) {
-    s1 = load_as<VDT>(state_in, si + 1);
-    s2 = load_as<VDT>(state_in, si + 2);
-    s3 = load_as<VDT>(state_in, si + 3);
-    token = load_as<VDT>(in, xi);
-    w0 = load_as<WDT>(weight, wi + 0);
-    w1 = load_as<WDT>(weight, wi + 1);
-    w2 = load_as<WDT>(weight, wi + 2);
-    w3 = load_as<WDT>(weight, wi + 3);
-  }
-  __device__ inline float apply() const {
-    float acc = s1 * w0;
-    acc += s2 * w1;
-    acc += s3 * w2;
-    acc += token * w3;
-    float y = acc / (1.0f + expf(-acc));
-    if constexpr (VDT == LK_DTYPE_BF16) y = round_bf16(y);
-    else if constexpr (VDT == LK_DTYPE_F16) y = static_cast<float>(static_cast<_Float16>(y));
-    return y;
-  }
-  // the shifted window, issued at the end of the kernel: a store among the
-  // preparation's loads would make every later wait on those loads count it
-  __device__ inline void store_shifted(void* state_out, int64_t si) const {
-    store_value(state_out, si + 0, s1, VDT);
-    store_value(state_out, si + 1, s2, VDT);
-    store_value(state_out, si + 2, s3, VDT);
-    store_value(state_out, si + 3, token, VDT);
-  }
-};
 
 // GATES_AS_VALUES: the raw decay and beta are stored in the value dtype (the
 // common case), fixed at compile time so that no dtype branch splits the
@@ -796,9 +799,30 @@ int lk_kda_decode_layer(const void* q_in, const void* k_in, const void* v_in, vo
              "state and out must be 16-byte aligned");
   LayerArgs a{{q_in, k_in, v_in}, {q_state, k_state, v_state}, {q_weight, k_weight, v_weight},
               raw_decay, dt_bias, a_log, raw_beta, state, out};
-  kda_layer_kernel<<<static_cast<unsigned>(batch * heads), kLayerThreads, 0, as_stream(stream)>>>(
-      a, static_cast<int>(heads), static_cast<int>(head_dim), eps, scale, value_dtype,
-      weight_dtype, decay_dtype, beta_dtype);
+  const dim3 grid(static_cast<unsigned>(batch * heads));
+  const int nh = static_cast<int>(heads), nd = static_cast<int>(head_dim);
+  hipStream_t s = as_stream(stream);
+  const bool gates_as_values = decay_dtype == value_dtype && beta_dtype == value_dtype;
+#define LK_KDA_LAYER(V, W)                                                                  \
+  do {                                                                                      \
+    if (gates_as_values)                                                                    \
+      kda_layer_kernel<V, W, true><<<grid, kLayerThreads, 0, s>>>(a, nh, nd, eps, scale,    \
+                                                                  decay_dtype, beta_dtype); \
+    else                                                                                    \
+      kda_layer_kernel<V, W, false><<<grid, kLayerThreads, 0, s>>>(a, nh, nd, eps, scale,   \
+                                                                   decay_dtype, beta_dtype); \
+  } while (0)
+#define LK_KDA_LAYER_W(V)                                                  \
+  do {                                                                     \
+    if (weight_dtype == LK_DTYPE_F32) LK_KDA_LAYER(V, LK_DTYPE_F32);       \
+    else if (weight_dtype == LK_DTYPE_F16) LK_KDA_LAYER(V, LK_DTYPE_F16);  \
+    else LK_KDA_LAYER(V, LK_DTYPE_BF16);                                   \
+  } while (0)
+  if (value_dtype == LK_DTYPE_F32) LK_KDA_LAYER_W(LK_DTYPE_F32);
+  else if (value_dtype == LK_DTYPE_F16) LK_KDA_LAYER_W(LK_DTYPE_F16);
+  else LK_KDA_LAYER_W(LK_DTYPE_BF16);
+#undef LK_KDA_LAYER_W
+#undef LK_KDA_LAYER
   return check_launch("lk_kda_decode_layer");
 }
 
