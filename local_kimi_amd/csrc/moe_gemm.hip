@@ -355,6 +355,15 @@ struct GemmArgs {
   int act;                   // two-matrix epilogue (kActSwiglu / kActSitu)
   int tail16;                // 64-row launches: tiles of <= 16 rows take the 16-row path
   float situ_beta, situ_linear_beta;  // SiTU parameters; linear_beta <= 0: none
+  // persistent gate/up launches of small batches that route and schedule the
+  // batch themselves (no router or schedule launch before them): the
+  // router's inputs, the outputs block 0 writes, and the batch
+  const float* rt_logits;
+  const float* rt_bias;
+  int64_t* rt_idx;
+  float* rt_w;
+  int rt_tokens, rt_routed, rt_top_k, rt_renorm;
+  float rt_scaling;
 };
 
 template <typename T>
@@ -1726,11 +1735,75 @@ struct PsPair {
 // the tail of the gate/up launch, where the last units of each block stream
 // alone; the SwiGLU is applied to the same bf16-rounded values as in the
 // fused epilogue, so the block's output is the same bits.
+// Routing and schedule of a small batch inside each block of the persistent
+// gate/up GEMM (ROUTED): waves 0 .. tokens - 1 route one token each
+// (engine/klinear/router.py:47-85; block 0 writes the selections and weights
+// for the W2 launch that follows), then wave 0 builds the 16-row schedule of
+// the at most kRoutedEntries token-routes (shared expert as route top_k) in
+// LDS: entry e's sorted position counts the entries of lower buckets and the
+// entries of its bucket before it (stable, row-major, as the schedule
+// kernels), and an expert's tiles start after the tiles of every lower
+// bucket. Bucket routed + 1 collects invalid selections (expert -1: zeros).
+// Replaces the router + schedule launch: no tables go through memory.
+constexpr int kRoutedEntries = 64;
+
+__device__ void route_schedule_block(const GemmArgs& g, int32_t* r_sel, int4* r_tiles,
+                                     int32_t* r_perm, int32_t* r_count) {
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, lane = tid & (kWave - 1);
+  const int ne = g.rt_routed, top_k = g.rt_top_k, tokens = g.rt_tokens;
+  if (wave < tokens) {
+    const bool writer = blockIdx.x == 0;
+    route_token<4>(g.rt_logits + static_cast<int64_t>(wave) * ne, g.rt_bias, ne, top_k, -1,
+                   g.rt_scaling, g.rt_renorm,
+                   writer ? g.rt_idx + static_cast<int64_t>(wave) * top_k : nullptr,
+                   writer ? g.rt_w + static_cast<int64_t>(wave) * top_k : nullptr,
+                   r_sel + wave * top_k);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int routes = top_k + 1;
+    const int n = tokens * routes;  // <= kRoutedEntries (host-checked)
+    const bool live = lane < n;
+    int b = 0x7FFFFFFF;  // lanes past the batch sort after every bucket
+    if (live) {
+      const int t = lane / routes, r = lane - t * routes;
+      const int x = r == top_k ? ne : r_sel[t * top_k + r];
+      b = (x >= 0 && x <= ne) ? x : ne + 1;
+    }
+    int less = 0, before = 0, same = 0;
+    for (int j = 0; j < n; ++j) {  // uniform trip count
+      const int bj = __builtin_amdgcn_readlane(b, j);
+      less += bj < b ? 1 : 0;
+      same += bj == b ? 1 : 0;
+      before += (bj == b && j < lane) ? 1 : 0;
+    }
+    // the first entry of each bucket carries its tile count
+    const int tiles_here = (live && before == 0) ? (same + 15) >> 4 : 0;
+    int tbase = 0, tcount = 0;
+    for (int j = 0; j < n; ++j) {
+      const int bj = __builtin_amdgcn_readlane(b, j);
+      const int cj = __builtin_amdgcn_readlane(tiles_here, j);
+      tbase += bj < b ? cj : 0;
+      tcount += cj;
+    }
+    if (live) {
+      const int pos = less + before;
+      r_perm[pos] = lane;
+      if ((before & 15) == 0)
+        r_tiles[tbase + (before >> 4)] = make_int4(b <= ne ? b : -1, pos, min(16, same - before), 0);
+    }
+    if (lane == 0) *r_count = tcount;
+  }
+  __syncthreads();
+}
+
 template <int FMT, int MATS, int DEPTH, bool GATHER, bool SCATTER, bool SPLIT = false,
-          bool SWI = false>
+          bool SWI = false, bool ROUTED = false>
 __global__ void __launch_bounds__(kStWaves * kWave)
 w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   static_assert(FMT == kFmtW4A16 || FMT == kFmtMxBf16, "bf16 activations, 16-byte weight loads");
+  static_assert(!ROUTED || (GATHER && SCATTER && !SPLIT && !SWI), "routing feeds the gate/up GEMM");
   static_assert(DEPTH % 2 == 0, "the ring holds pairs of k-steps");
   static_assert(!SPLIT || MATS == 1, "split units hold one matrix");
   static_assert(!SWI || (MATS == 1 && !SPLIT), "SwiGLU staging feeds the down GEMM");
@@ -1753,7 +1826,14 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   const int rounds = ksteps / DEPTH;  // DEPTH divides ksteps (host-checked)
   const int cgs1 = static_cast<int>((N + NT * 16 - 1) / (NT * 16));  // column groups per matrix
   const int cgs = SPLIT ? 2 * cgs1 : cgs1;
-  const int total = *g.tile_count * cgs;
+  // ROUTED: the batch's selections and schedule, computed by every block in
+  // the activation LDS before any staging (at most kRoutedEntries routes)
+  int32_t* const r_sel = reinterpret_cast<int32_t*>(smem);  // [tokens][top_k]
+  int4* const r_tiles = reinterpret_cast<int4*>(smem) + kRoutedEntries / 4;
+  int32_t* const r_perm = reinterpret_cast<int32_t*>(r_tiles + kRoutedEntries);
+  int32_t* const r_count = r_perm + kRoutedEntries;
+  if constexpr (ROUTED) route_schedule_block(g, r_sel, r_tiles, r_perm, r_count);
+  const int total = (ROUTED ? *r_count : *g.tile_count) * cgs;
   const int per = (total + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
   // ranges go to XCDs in contiguous runs (block b runs on XCD b % 8): the
   // blocks on one XCD take consecutive ranges, so an expert's consecutive
@@ -1783,13 +1863,13 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   if (tid == 0) next_unit = ub;
   if (tid < nseg * 16) {
     const int s = tid >> 4, m = tid & 15;
-    const int4 d = reinterpret_cast<const int4*>(g.tiles)[t_first + s];
+    const int4 d = ROUTED ? r_tiles[t_first + s] : reinterpret_cast<const int4*>(g.tiles)[t_first + s];
     if (m == 0) {
       seg_exp[s] = d.x;
       seg_rows[s] = d.z;
     }
     if (m < d.z) {
-      const int32_t p = (GATHER || SCATTER) ? g.perm[d.y + m] : d.y + m;
+      const int32_t p = ROUTED ? r_perm[d.y + m] : (GATHER || SCATTER) ? g.perm[d.y + m] : d.y + m;
       seg_row[s][m] = GATHER ? p / g.routes : static_cast<int64_t>(d.y) + m;
       seg_out[s][m] = SCATTER ? p : d.y + m;
     }
@@ -2573,10 +2653,11 @@ bool stream_fits(int64_t k, int mt, int64_t group, bool mx) {
 
 constexpr int kPsMaxLds = 160 * 1024 - 2048;  // dynamic LDS of one persistent block
 
-template <int FMT, int MATS, int DEPTH, bool GATHER, bool SCATTER, bool SPLIT, bool SWI>
+template <int FMT, int MATS, int DEPTH, bool GATHER, bool SCATTER, bool SPLIT, bool SWI,
+          bool ROUTED = false>
 int persist_one(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hipStream_t s,
                 bool launch) {
-  auto* fn = &w4a16_persist_kernel<FMT, MATS, DEPTH, GATHER, SCATTER, SPLIT, SWI>;
+  auto* fn = &w4a16_persist_kernel<FMT, MATS, DEPTH, GATHER, SCATTER, SPLIT, SWI, ROUTED>;
   struct Cfg {
     int device = -1, blocks_per_cu = 0, cus = 0;
     size_t lds = 0;
@@ -2623,20 +2704,21 @@ int persist_one(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hi
   return 0;
 }
 
-template <int FMT, int MATS, bool GATHER, bool SCATTER, bool SPLIT, bool SWI>
+template <int FMT, int MATS, bool GATHER, bool SCATTER, bool SPLIT, bool SWI,
+          bool ROUTED = false>
 int persist_depth(const GemmArgs& g, int nbuf, size_t lds, int64_t tiles_bound, hipStream_t s,
                   bool launch) {
   // the ring depth divides the k-steps (at least one whole round per unit)
   const int64_t ksteps = g.k / 128;
   if (ksteps >= 6 && ksteps % 6 == 0)
-    return persist_one<FMT, MATS, 6, GATHER, SCATTER, SPLIT, SWI>(g, nbuf, lds, tiles_bound, s,
-                                                                  launch);
+    return persist_one<FMT, MATS, 6, GATHER, SCATTER, SPLIT, SWI, ROUTED>(g, nbuf, lds,
+                                                                          tiles_bound, s, launch);
   if (ksteps >= 8 && ksteps % 8 == 0)
-    return persist_one<FMT, MATS, 8, GATHER, SCATTER, SPLIT, SWI>(g, nbuf, lds, tiles_bound, s,
-                                                                  launch);
+    return persist_one<FMT, MATS, 8, GATHER, SCATTER, SPLIT, SWI, ROUTED>(g, nbuf, lds,
+                                                                          tiles_bound, s, launch);
   if (ksteps >= 4 && ksteps % 4 == 0)
-    return persist_one<FMT, MATS, 4, GATHER, SCATTER, SPLIT, SWI>(g, nbuf, lds, tiles_bound, s,
-                                                                  launch);
+    return persist_one<FMT, MATS, 4, GATHER, SCATTER, SPLIT, SWI, ROUTED>(g, nbuf, lds,
+                                                                          tiles_bound, s, launch);
   return -1;
 }
 
@@ -2688,6 +2770,13 @@ int persist_launch(const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_
           rc = persist_depth<FMT, MATS, false, true, false, false>(g, nbuf, lds, tiles_bound, s, launch);
           break;
         case Mode::GatherScatter:
+          if constexpr (FMT == kFmtW4A16 && MATS == 2) {
+            if (g.rt_logits != nullptr) {  // the block routes and schedules the batch itself
+              rc = persist_depth<FMT, MATS, true, true, false, false, true>(g, nbuf, lds,
+                                                                            tiles_bound, s, launch);
+              break;
+            }
+          }
           rc = persist_depth<FMT, MATS, true, true, false, false>(g, nbuf, lds, tiles_bound, s, launch);
           break;
         default: break;
@@ -3293,7 +3382,32 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   const int tr = mt == 1 ? kSmallTileRows : kTileRows;
   // W4A16 G = 128 on 64-row tiles: x and the activations go in paired
   const bool paired = !mx && mt == 4 && group == 128;
-  if (route_schedule_fits(tokens, experts - 1, top_k)) {
+  const int64_t tb = max_tiles_for(entries, experts, tr);
+  // Few tokens (W4A16): the activations go to (token, route) rows and one
+  // token-major launch does W2, the combine and the shared expert, instead of
+  // the down GEMM and the combine kernel; it reads an expert's W2 once per
+  // route that uses it rather than once per call.
+  const bool w2_rows = !mx && tokens <= kW2RowsMaxTokens && w2_rows_fits(routes, i);
+  // ...and their persistent gate/up GEMM routes and schedules the batch in
+  // every block (route_schedule_block), where that launch applies: no router
+  // or schedule launch, no tables through memory (the same path knob as the
+  // one-launch router + schedule turns it off)
+  bool gemm_routes = false;
+  if (w2_rows && mt == 1 && entries <= kRoutedEntries && tokens <= kStWaves &&
+      route_schedule_fits(tokens, experts - 1, top_k)) {
+    GemmArgs probe{};
+    probe.k = h;
+    probe.n = i;
+    probe.group = group;
+    probe.outputs = 1;
+    probe.act = kActSwiglu;
+    probe.rt_logits = logits;
+    gemm_routes =
+        persist_fmt<2>(false, probe, Mode::GatherScatter, tb, s, "", PsForm::Plain, false) == 0;
+  }
+  if (gemm_routes) {
+    // routed by the gate/up GEMM below
+  } else if (route_schedule_fits(tokens, experts - 1, top_k)) {
     if (int rc = route_schedule_launch(logits, bias, expert_indices, weights, tokens, experts - 1,
                                        top_k, routed_scaling_factor, renormalize, offsets, perm,
                                        tiles, count, tr, mtiles, mcount, s))
@@ -3352,12 +3466,6 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   g.k = h;
   g.wstride = i * h / 2;
   g.sstride = i * (h / group);
-  const int64_t tb = max_tiles_for(entries, experts, tr);
-  // Few tokens (W4A16): the activations go to (token, route) rows and one
-  // token-major launch does W2, the combine and the shared expert, instead of
-  // the down GEMM and the combine kernel; it reads an expert's W2 once per
-  // route that uses it rather than once per call.
-  const bool w2_rows = !mx && tokens <= kW2RowsMaxTokens && w2_rows_fits(routes, i);
   const Mode gu_mode = w2_rows ? Mode::GatherScatter : Mode::Gather;
   // down projection: sorted activation rows, outputs scattered to (token, route) rows
   auto down_args = [&](GemmArgs d) {
@@ -3394,7 +3502,20 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
       path_choice(kKnobMoeSplitSwiglu) != 1 &&
       persist_fmt<1>(mx, g, Mode::Gather, tb, s, "", PsForm::SplitGateUp, false) == 0 &&
       persist_fmt<1>(mx, down_args(g), Mode::Scatter, tb, s, "", PsForm::SwiDown, false) == 0;
-  if (int rc = f8 ? stream_launch<kFmtMxF8, 2>(g, Mode::Gather, tb, mt, s, "moe gate/up gemm")
+  if (gemm_routes) {
+    g.rt_logits = logits;
+    g.rt_bias = bias;
+    g.rt_idx = expert_indices;
+    g.rt_w = weights;
+    g.rt_tokens = static_cast<int>(tokens);
+    g.rt_routed = static_cast<int>(experts - 1);
+    g.rt_top_k = static_cast<int>(top_k);
+    g.rt_renorm = renormalize;
+    g.rt_scaling = routed_scaling_factor;
+  }
+  if (int rc = gemm_routes ? persist_fmt<2>(false, g, Mode::GatherScatter, tb, s,
+                                            "moe gate/up gemm (routing)", PsForm::Plain, true)
+               : f8 ? stream_launch<kFmtMxF8, 2>(g, Mode::Gather, tb, mt, s, "moe gate/up gemm")
                : split ? persist_fmt<1>(mx, g, Mode::Gather, tb, s, "moe gate/up gemm",
                                         PsForm::SplitGateUp, true)
                : mt    ? stream_fmt<2>(mx, g, gu_mode, tb, mt, s, "moe gate/up gemm")

@@ -118,3 +118,73 @@ def test_fused_router_schedule_matches_separate_launches(rng, monkeypatch, weigh
         ey, _, _ = OM.moe_block(x[sel], logits[sel], b, *banks, top_k=top_k,
                                 routed_scaling_factor=2.446, group_size=128)
     assert_close_bf16(to_bits(y)[sel], ey, what=f"{weights} block T={tokens} k={top_k}")
+
+
+@pytest.mark.parametrize("tokens,top_k,routed,bias,ties", [
+    (1, 8, 256, False, False),
+    (2, 8, 256, True, True),
+    (3, 8, 256, False, True),
+    (4, 8, 256, True, False),
+    (4, 2, 64, False, False),
+    (4, 6, 32, True, True),   # few experts: routes of one token land on few tiles
+])
+def test_gate_up_gemm_that_routes_matches_separate_launches(rng, monkeypatch, tokens, top_k,
+                                                            routed, bias, ties):
+    """Batches of at most 4 tokens at K >= 512: the persistent gate/up GEMM
+    routes and schedules the batch in every block (no router or schedule
+    launch). Selections, weights and outputs bit-identical to the router and
+    chunked schedule launches (path knob off), and the block against the
+    oracle on every token."""
+    from local_kimi_amd.kernels import w4a16_moe_forward
+
+    h, inter = 512, 256
+    banks = (*_w4_bank(rng, routed + 1, inter, h), *_w4_bank(rng, routed + 1, inter, h),
+             *_w4_bank(rng, routed + 1, h, inter))
+    x = random_bf16_bits(rng, (tokens, h))
+    logits = rng.normal(0, 1, (tokens, routed)).astype(np.float32)
+    if ties:
+        logits[:, 4:12] = logits[:, 4:5]
+    b = rng.normal(0, 0.05, routed).astype(np.float32) if bias else None
+    args = (_dev(x), _dev(logits), None if b is None else _dev(b), *(_dev(v) for v in banks),
+            top_k, 2.446)
+    (y, idx, w), (y0, idx0, w0) = _fused_and_split(monkeypatch, w4a16_moe_forward, *args)
+    assert torch.equal(idx, idx0)
+    assert torch.equal(w, w0)
+    assert torch.equal(y, y0), "the routing gate/up GEMM and the separate launches differ"
+    eidx, ew = OM.route(logits, b, top_k, routed_scaling_factor=2.446)
+    assert np.array_equal(idx.cpu().numpy(), eidx)
+    np.testing.assert_allclose(w.cpu().numpy(), ew, rtol=2e-6)
+    ey, _, _ = OM.moe_block(x, logits, b, *banks, top_k=top_k, routed_scaling_factor=2.446,
+                            group_size=128)
+    assert_close_bf16(to_bits(y), ey, what=f"routing gate/up T={tokens} k={top_k} E={routed}")
+
+
+def test_gate_up_gemm_that_routes_under_graph_replay(rng):
+    """The same launch captured in a HIP graph and replayed with new logits
+    copied in between: every replay matches an eager call on those logits."""
+    from local_kimi_amd.kernels import w4a16_moe_forward
+
+    tokens, top_k, routed, h, inter = 4, 8, 256, 512, 256
+    banks = [_dev(v) for v in (*_w4_bank(rng, routed + 1, inter, h),
+                               *_w4_bank(rng, routed + 1, inter, h),
+                               *_w4_bank(rng, routed + 1, h, inter))]
+    x = _dev(random_bf16_bits(rng, (tokens, h)))
+    logits = _dev(rng.normal(0, 1, (tokens, routed)).astype(np.float32))
+    w4a16_moe_forward(x, logits, None, *banks, top_k, 2.446)  # allocations outside the graph
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out = w4a16_moe_forward(x, logits, None, *banks, top_k, 2.446)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        fresh = _dev(rng.normal(0, 1, (tokens, routed)).astype(np.float32))
+        logits.copy_(fresh)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = w4a16_moe_forward(x, fresh, None, *banks, top_k, 2.446)
+        torch.cuda.synchronize()
+        for a, e in zip(out, want):
+            assert torch.equal(a, e)
