@@ -1740,11 +1740,11 @@ struct PsPair {
 // (engine/klinear/router.py:47-85; block 0 writes the selections and weights
 // for the W2 launch that follows), then wave 0 builds the 16-row schedule of
 // the at most kRoutedEntries token-routes (shared expert as route top_k) in
-// LDS: entry e's sorted position counts the entries of lower buckets and the
-// entries of its bucket before it (stable, row-major, as the schedule
-// kernels), and an expert's tiles start after the tiles of every lower
-// bucket. Bucket routed + 1 collects invalid selections (expert -1: zeros).
-// Replaces the router + schedule launch: no tables go through memory.
+// LDS with the schedule kernels' ranking: a bitmap of the entries of each
+// bucket, the buckets' entry and tile counts scanned in bucket order, and an
+// entry's rank the popcount of the lower entries of its bucket (stable,
+// row-major). Bucket routed + 1 collects invalid selections (expert -1:
+// zeros). Replaces the router + schedule launch: no tables go through memory.
 constexpr int kRoutedEntries = 64;
 
 __device__ void route_schedule_block(const GemmArgs& g, int32_t* r_sel, int4* r_tiles,
@@ -1764,36 +1764,52 @@ __device__ void route_schedule_block(const GemmArgs& g, int32_t* r_sel, int4* r_
   if (wave == 0) {
     const int routes = top_k + 1;
     const int n = tokens * routes;  // <= kRoutedEntries (host-checked)
+    const int nb = ne + 2;          // experts 0 .. ne (ne: shared), invalid
+    uint32_t* const mask = reinterpret_cast<uint32_t*>(r_count + 1);  // [nb][2]
+    int* const bstart = reinterpret_cast<int*>(mask + 2 * nb);        // [nb]
+    int* const btile = bstart + nb;                                   // [nb]
     const bool live = lane < n;
-    int b = 0x7FFFFFFF;  // lanes past the batch sort after every bucket
+    int b = 0;
     if (live) {
       const int t = lane / routes, r = lane - t * routes;
       const int x = r == top_k ? ne : r_sel[t * top_k + r];
       b = (x >= 0 && x <= ne) ? x : ne + 1;
     }
-    int less = 0, before = 0, same = 0;
-    for (int j = 0; j < n; ++j) {  // uniform trip count
-      const int bj = __builtin_amdgcn_readlane(b, j);
-      less += bj < b ? 1 : 0;
-      same += bj == b ? 1 : 0;
-      before += (bj == b && j < lane) ? 1 : 0;
+    for (int i = lane; i < 2 * nb; i += kWave) mask[i] = 0u;
+    __builtin_amdgcn_s_waitcnt(0);  // one wave: its LDS operations in order
+    if (live) atomicOr(&mask[2 * b + (lane >> 5)], 1u << (lane & 31));
+    __builtin_amdgcn_s_waitcnt(0);
+    // bucket entry and tile counts, scanned in bucket order (lane: a run of buckets)
+    const int per = (nb + kWave - 1) / kWave;
+    const int b0 = min(nb, lane * per), b1 = min(nb, b0 + per);
+    int se = 0, st = 0;
+    for (int i = b0; i < b1; ++i) {
+      const int c = __popc(mask[2 * i]) + __popc(mask[2 * i + 1]);
+      se += c;
+      st += (c + 15) >> 4;
     }
-    // the first entry of each bucket carries its tile count
-    const int tiles_here = (live && before == 0) ? (same + 15) >> 4 : 0;
-    int tbase = 0, tcount = 0;
-    for (int j = 0; j < n; ++j) {
-      const int bj = __builtin_amdgcn_readlane(b, j);
-      const int cj = __builtin_amdgcn_readlane(tiles_here, j);
-      tbase += bj < b ? cj : 0;
-      tcount += cj;
+    const int ie = wave_inclusive_scan(se);
+    const int it = wave_inclusive_scan(st);
+    int re = ie - se, rt = it - st;
+    for (int i = b0; i < b1; ++i) {
+      const int c = __popc(mask[2 * i]) + __popc(mask[2 * i + 1]);
+      bstart[i] = re;
+      btile[i] = rt;
+      re += c;
+      rt += (c + 15) >> 4;
     }
+    if (lane == kWave - 1) *r_count = it;
+    __builtin_amdgcn_s_waitcnt(0);
     if (live) {
-      const int pos = less + before;
+      const uint32_t lo = mask[2 * b], hi = mask[2 * b + 1];
+      const int before = lane < 32 ? __popc(lo & ((1u << lane) - 1u))
+                                   : __popc(lo) + __popc(hi & ((1u << (lane - 32)) - 1u));
+      const int same = __popc(lo) + __popc(hi);
+      const int pos = bstart[b] + before;
       r_perm[pos] = lane;
       if ((before & 15) == 0)
-        r_tiles[tbase + (before >> 4)] = make_int4(b <= ne ? b : -1, pos, min(16, same - before), 0);
+        r_tiles[btile[b] + (before >> 4)] = make_int4(b <= ne ? b : -1, pos, min(16, same - before), 0);
     }
-    if (lane == 0) *r_count = tcount;
   }
   __syncthreads();
 }
@@ -1831,7 +1847,7 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   int32_t* const r_sel = reinterpret_cast<int32_t*>(smem);  // [tokens][top_k]
   int4* const r_tiles = reinterpret_cast<int4*>(smem) + kRoutedEntries / 4;
   int32_t* const r_perm = reinterpret_cast<int32_t*>(r_tiles + kRoutedEntries);
-  int32_t* const r_count = r_perm + kRoutedEntries;
+  int32_t* const r_count = r_perm + kRoutedEntries;  // then the ranking scratch (<= 1,033 words)
   if constexpr (ROUTED) route_schedule_block(g, r_sel, r_tiles, r_perm, r_count);
   const int total = (ROUTED ? *r_count : *g.tile_count) * cgs;
   const int per = (total + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
