@@ -364,6 +364,11 @@ struct GemmArgs {
   float* rt_w;
   int rt_tokens, rt_routed, rt_top_k, rt_renorm;
   float rt_scaling;
+  // where block 0 also writes the schedule (perm, tiles, count) for a later
+  // launch of the same block (the split SwiGLU's down GEMM); null: not needed
+  int32_t* rt_perm_out;
+  int32_t* rt_tiles_out;
+  int32_t* rt_count_out;
 };
 
 template <typename T>
@@ -1736,82 +1741,155 @@ struct PsPair {
 // alone; the SwiGLU is applied to the same bf16-rounded values as in the
 // fused epilogue, so the block's output is the same bits.
 // Routing and schedule of a small batch inside each block of the persistent
-// gate/up GEMM (ROUTED): waves 0 .. tokens - 1 route one token each
-// (engine/klinear/router.py:47-85; block 0 writes the selections and weights
-// for the W2 launch that follows), then wave 0 builds the 16-row schedule of
-// the at most kRoutedEntries token-routes (shared expert as route top_k) in
-// LDS with the schedule kernels' ranking: a bitmap of the entries of each
-// bucket, the buckets' entry and tile counts scanned in bucket order, and an
-// entry's rank the popcount of the lower entries of its bucket (stable,
-// row-major). Bucket routed + 1 collects invalid selections (expert -1:
-// zeros). Replaces the router + schedule launch: no tables go through memory.
-constexpr int kRoutedEntries = 64;
+// gate/up GEMM (ROUTED): the block's waves route the tokens, wave w tokens
+// w, w + 8, ... (engine/klinear/router.py:47-85; block 0 writes the
+// selections and weights for the launches that follow), then the block ranks
+// the at most kRoutedEntries token-routes (shared expert as route top_k) into
+// the 16-row schedule in LDS, as the schedule kernels do: a bitmap of each
+// bucket's entries per wave of entries, the buckets' entry and tile counts
+// scanned in bucket order by one wave, and an entry's rank the entries of its
+// bucket in earlier waves plus the popcount of the lower lanes of its own
+// (stable, row-major). Bucket routed + 1 collects invalid selections (expert
+// -1: zeros). No router or schedule launch; block 0 also writes the tables
+// where a later launch reads them (rt_tiles_out).
+constexpr int kRoutedEntries = kStWaves * kWave;  // 512
+constexpr int kRoutedSelWords = 256;               // tokens x top_k selections
+
+// LDS words of the routing scratch for n token-routes over nb buckets
+__host__ __device__ inline int routed_scratch_words(int n, int nb) {
+  const int nw = (n + kWave - 1) / kWave;
+  return kRoutedSelWords + 4 * kRoutedEntries + kRoutedEntries + 1 + 3 * nw * nb + 3 * nb;
+}
+
+// Bucket entry and tile counts of the nb buckets (cnt(i)), scanned in bucket
+// order by one wave (a lane takes a run of buckets): bucket starts, first
+// tiles and the tile count.
+template <typename Count>
+__device__ void routed_bucket_scan(int nb, int lane, Count cnt, int* bstart, int* btile,
+                                   int32_t* r_count) {
+  const int per = (nb + kWave - 1) / kWave;
+  const int b0 = min(nb, lane * per), b1 = min(nb, b0 + per);
+  int se = 0, st = 0;
+  for (int i = b0; i < b1; ++i) {
+    const int c = cnt(i);
+    se += c;
+    st += (c + 15) >> 4;
+  }
+  const int ie = wave_inclusive_scan(se);
+  const int it = wave_inclusive_scan(st);
+  int re = ie - se, rt = it - st;
+  for (int i = b0; i < b1; ++i) {
+    const int c = cnt(i);
+    bstart[i] = re;
+    btile[i] = rt;
+    re += c;
+    rt += (c + 15) >> 4;
+  }
+  if (lane == kWave - 1) *r_count = it;
+}
 
 __device__ void route_schedule_block(const GemmArgs& g, int32_t* r_sel, int4* r_tiles,
                                      int32_t* r_perm, int32_t* r_count) {
+  constexpr int kThreads = kStWaves * kWave;
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid & (kWave - 1);
   const int ne = g.rt_routed, top_k = g.rt_top_k, tokens = g.rt_tokens;
-  if (wave < tokens) {
-    const bool writer = blockIdx.x == 0;
-    route_token<4>(g.rt_logits + static_cast<int64_t>(wave) * ne, g.rt_bias, ne, top_k, -1,
+  const int routes = top_k + 1;
+  const int n = tokens * routes;  // <= kRoutedEntries (host-checked)
+  const int nb = ne + 2;          // experts 0 .. ne (ne: shared), invalid
+  const bool writer = blockIdx.x == 0;
+  const int nw = (n + kWave - 1) / kWave;
+  uint32_t* const mask = reinterpret_cast<uint32_t*>(r_count + 1);  // [nw][nb][2]
+  if (nw > 1)  // the several waves' bitmaps, cleared while the logits arrive
+    for (int i = tid; i < 2 * nw * nb; i += kThreads) mask[i] = 0u;
+  for (int t = wave; t < tokens; t += kStWaves)
+    route_token<4>(g.rt_logits + static_cast<int64_t>(t) * ne, g.rt_bias, ne, top_k, -1,
                    g.rt_scaling, g.rt_renorm,
-                   writer ? g.rt_idx + static_cast<int64_t>(wave) * top_k : nullptr,
-                   writer ? g.rt_w + static_cast<int64_t>(wave) * top_k : nullptr,
-                   r_sel + wave * top_k);
-  }
+                   writer ? g.rt_idx + static_cast<int64_t>(t) * top_k : nullptr,
+                   writer ? g.rt_w + static_cast<int64_t>(t) * top_k : nullptr,
+                   r_sel + t * top_k);
   __syncthreads();
-  if (wave == 0) {
-    const int routes = top_k + 1;
-    const int n = tokens * routes;  // <= kRoutedEntries (host-checked)
-    const int nb = ne + 2;          // experts 0 .. ne (ne: shared), invalid
-    uint32_t* const mask = reinterpret_cast<uint32_t*>(r_count + 1);  // [nb][2]
-    int* const bstart = reinterpret_cast<int*>(mask + 2 * nb);        // [nb]
-    int* const btile = bstart + nb;                                   // [nb]
-    const bool live = lane < n;
+  if (nw == 1) {  // block-uniform: wave 0 ranks the entries alone
+    if (wave == 0) {
+      int* const bstart = reinterpret_cast<int*>(mask + 2 * nb);        // [nb]
+      int* const btile = bstart + nb;                                   // [nb]
+      const bool live = lane < n;
+      int b = 0;
+      if (live) {
+        const int t = lane / routes, r = lane - t * routes;
+        const int x = r == top_k ? ne : r_sel[t * top_k + r];
+        b = (x >= 0 && x <= ne) ? x : ne + 1;
+      }
+      for (int i = lane; i < 2 * nb; i += kWave) mask[i] = 0u;
+      __builtin_amdgcn_s_waitcnt(0);  // one wave: its LDS operations in order
+      if (live) atomicOr(&mask[2 * b + (lane >> 5)], 1u << (lane & 31));
+      __builtin_amdgcn_s_waitcnt(0);
+      routed_bucket_scan(nb, lane,
+                         [&](int i) { return __popc(mask[2 * i]) + __popc(mask[2 * i + 1]); },
+                         bstart, btile, r_count);
+      __builtin_amdgcn_s_waitcnt(0);
+      if (live) {
+        const uint32_t lo = mask[2 * b], hi = mask[2 * b + 1];
+        const int before = lane < 32 ? __popc(lo & ((1u << lane) - 1u))
+                                     : __popc(lo) + __popc(hi & ((1u << (lane - 32)) - 1u));
+        const int same = __popc(lo) + __popc(hi);
+        const int pos = bstart[b] + before;
+        r_perm[pos] = lane;
+        if ((before & 15) == 0)
+          r_tiles[btile[b] + (before >> 4)] =
+              make_int4(b <= ne ? b : -1, pos, min(16, same - before), 0);
+      }
+    }
+  } else {
+    int* const pre = reinterpret_cast<int*>(mask + 2 * nw * nb);  // [nw][nb]
+    int* const tot = pre + nw * nb;                               // [nb]
+    int* const bstart = tot + nb;                                 // [nb]
+    int* const btile = bstart + nb;                               // [nb]
+    const bool live = tid < n;
     int b = 0;
     if (live) {
-      const int t = lane / routes, r = lane - t * routes;
+      const int t = tid / routes, r = tid - t * routes;
       const int x = r == top_k ? ne : r_sel[t * top_k + r];
       b = (x >= 0 && x <= ne) ? x : ne + 1;
+      atomicOr(&mask[(wave * nb + b) * 2 + (lane >> 5)], 1u << (lane & 31));
     }
-    for (int i = lane; i < 2 * nb; i += kWave) mask[i] = 0u;
-    __builtin_amdgcn_s_waitcnt(0);  // one wave: its LDS operations in order
-    if (live) atomicOr(&mask[2 * b + (lane >> 5)], 1u << (lane & 31));
-    __builtin_amdgcn_s_waitcnt(0);
-    // bucket entry and tile counts, scanned in bucket order (lane: a run of buckets)
-    const int per = (nb + kWave - 1) / kWave;
-    const int b0 = min(nb, lane * per), b1 = min(nb, b0 + per);
-    int se = 0, st = 0;
-    for (int i = b0; i < b1; ++i) {
-      const int c = __popc(mask[2 * i]) + __popc(mask[2 * i + 1]);
-      se += c;
-      st += (c + 15) >> 4;
+    __syncthreads();
+    // each bucket's entries in the waves before each wave, and in all
+    for (int bb = tid; bb < nb; bb += kThreads) {
+      int run = 0;
+#pragma unroll
+      for (int w = 0; w < kStWaves; ++w) {
+        if (w < nw) {
+          pre[w * nb + bb] = run;
+          run += __popc(mask[(w * nb + bb) * 2]) + __popc(mask[(w * nb + bb) * 2 + 1]);
+        }
+      }
+      tot[bb] = run;
     }
-    const int ie = wave_inclusive_scan(se);
-    const int it = wave_inclusive_scan(st);
-    int re = ie - se, rt = it - st;
-    for (int i = b0; i < b1; ++i) {
-      const int c = __popc(mask[2 * i]) + __popc(mask[2 * i + 1]);
-      bstart[i] = re;
-      btile[i] = rt;
-      re += c;
-      rt += (c + 15) >> 4;
-    }
-    if (lane == kWave - 1) *r_count = it;
-    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (wave == 0)
+      routed_bucket_scan(nb, lane, [&](int i) { return tot[i]; }, bstart, btile, r_count);
+    __syncthreads();
     if (live) {
-      const uint32_t lo = mask[2 * b], hi = mask[2 * b + 1];
-      const int before = lane < 32 ? __popc(lo & ((1u << lane) - 1u))
-                                   : __popc(lo) + __popc(hi & ((1u << (lane - 32)) - 1u));
-      const int same = __popc(lo) + __popc(hi);
-      const int pos = bstart[b] + before;
-      r_perm[pos] = lane;
-      if ((before & 15) == 0)
-        r_tiles[btile[b] + (before >> 4)] = make_int4(b <= ne ? b : -1, pos, min(16, same - before), 0);
+      const uint32_t lo = mask[(wave * nb + b) * 2], hi = mask[(wave * nb + b) * 2 + 1];
+      const int below = lane < 32 ? __popc(lo & ((1u << lane) - 1u))
+                                  : __popc(lo) + __popc(hi & ((1u << (lane - 32)) - 1u));
+      const int rank = pre[wave * nb + b] + below;
+      const int pos = bstart[b] + rank;
+      r_perm[pos] = tid;
+      if ((rank & 15) == 0)
+        r_tiles[btile[b] + (rank >> 4)] =
+            make_int4(b <= ne ? b : -1, pos, min(16, tot[b] - rank), 0);
     }
   }
   __syncthreads();
+  if (writer && g.rt_tiles_out != nullptr) {
+    const int count = *r_count;
+    for (int i = tid; i < n; i += kThreads) g.rt_perm_out[i] = r_perm[i];
+    for (int i = tid; i < count; i += kThreads)
+      reinterpret_cast<int4*>(g.rt_tiles_out)[i] = r_tiles[i];
+    if (tid == 0) *g.rt_count_out = count;
+  }
 }
 
 template <int FMT, int MATS, int DEPTH, bool GATHER, bool SCATTER, bool SPLIT = false,
@@ -1819,7 +1897,7 @@ template <int FMT, int MATS, int DEPTH, bool GATHER, bool SCATTER, bool SPLIT = 
 __global__ void __launch_bounds__(kStWaves * kWave)
 w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   static_assert(FMT == kFmtW4A16 || FMT == kFmtMxBf16, "bf16 activations, 16-byte weight loads");
-  static_assert(!ROUTED || (GATHER && SCATTER && !SPLIT && !SWI), "routing feeds the gate/up GEMM");
+  static_assert(!ROUTED || (GATHER && !SWI), "routing feeds the gate/up GEMM");
   static_assert(DEPTH % 2 == 0, "the ring holds pairs of k-steps");
   static_assert(!SPLIT || MATS == 1, "split units hold one matrix");
   static_assert(!SWI || (MATS == 1 && !SPLIT), "SwiGLU staging feeds the down GEMM");
@@ -1845,9 +1923,9 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   // ROUTED: the batch's selections and schedule, computed by every block in
   // the activation LDS before any staging (at most kRoutedEntries routes)
   int32_t* const r_sel = reinterpret_cast<int32_t*>(smem);  // [tokens][top_k]
-  int4* const r_tiles = reinterpret_cast<int4*>(smem) + kRoutedEntries / 4;
+  int4* const r_tiles = reinterpret_cast<int4*>(smem) + kRoutedSelWords / 4;
   int32_t* const r_perm = reinterpret_cast<int32_t*>(r_tiles + kRoutedEntries);
-  int32_t* const r_count = r_perm + kRoutedEntries;  // then the ranking scratch (<= 1,033 words)
+  int32_t* const r_count = r_perm + kRoutedEntries;  // then the ranking scratch
   if constexpr (ROUTED) route_schedule_block(g, r_sel, r_tiles, r_perm, r_count);
   const int total = (ROUTED ? *r_count : *g.tile_count) * cgs;
   const int per = (total + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
@@ -2764,6 +2842,13 @@ int persist_launch(const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_
     const int nbuf = 2 * one <= static_cast<size_t>(kPsMaxLds) ? 2 : (one <= static_cast<size_t>(kPsMaxLds) ? 1 : 0);
     if (nbuf == 0) return kPsNotApplicable;
     const size_t lds = nbuf * one;
+    // a launch that routes keeps its routing scratch in the activation LDS
+    if (g.rt_logits != nullptr) {
+      const int n = g.rt_tokens * (g.rt_top_k + 1);
+      if (FMT == kFmtMxF16 || n > kRoutedEntries || g.rt_tokens * g.rt_top_k > kRoutedSelWords ||
+          g.rt_routed > 256 || static_cast<size_t>(routed_scratch_words(n, g.rt_routed + 2)) * 4 > lds)
+        return kPsNotApplicable;
+    }
     // a phase's activations are staged from one batch of registers per thread
     const int half_cap = form == PsForm::SwiDown ? kPsSwiHalfMax : kPsHalfMax;
     if (g.k / 128 > 2 * half_cap) return kPsNotApplicable;
@@ -2771,7 +2856,11 @@ int persist_launch(const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_
     if constexpr (MATS == 1) {
       if (form == PsForm::SplitGateUp) {
         if (mode != Mode::Gather || g.act != kActSwiglu) return kPsNotApplicable;
-        rc = persist_depth<FMT, 1, true, false, true, false>(g, nbuf, lds, tiles_bound, s, launch);
+        if (g.rt_logits != nullptr)  // the block routes and schedules the batch itself
+          rc = persist_depth<FMT, 1, true, false, true, false, true>(g, nbuf, lds, tiles_bound, s,
+                                                                     launch);
+        else
+          rc = persist_depth<FMT, 1, true, false, true, false>(g, nbuf, lds, tiles_bound, s, launch);
       } else if (form == PsForm::SwiDown) {
         if (mode != Mode::Scatter || g.act != kActSwiglu) return kPsNotApplicable;
         rc = persist_depth<FMT, 1, false, true, false, true>(g, nbuf, lds, tiles_bound, s, launch);
@@ -2786,7 +2875,7 @@ int persist_launch(const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_
           rc = persist_depth<FMT, MATS, false, true, false, false>(g, nbuf, lds, tiles_bound, s, launch);
           break;
         case Mode::GatherScatter:
-          if constexpr (FMT == kFmtW4A16 && MATS == 2) {
+          if constexpr (MATS == 2) {
             if (g.rt_logits != nullptr) {  // the block routes and schedules the batch itself
               rc = persist_depth<FMT, MATS, true, true, false, false, true>(g, nbuf, lds,
                                                                             tiles_bound, s, launch);
@@ -3404,40 +3493,6 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   // the down GEMM and the combine kernel; it reads an expert's W2 once per
   // route that uses it rather than once per call.
   const bool w2_rows = !mx && tokens <= kW2RowsMaxTokens && w2_rows_fits(routes, i);
-  // ...and their persistent gate/up GEMM routes and schedules the batch in
-  // every block (route_schedule_block), where that launch applies: no router
-  // or schedule launch, no tables through memory (the same path knob as the
-  // one-launch router + schedule turns it off)
-  bool gemm_routes = false;
-  if (w2_rows && mt == 1 && entries <= kRoutedEntries && tokens <= kStWaves &&
-      route_schedule_fits(tokens, experts - 1, top_k)) {
-    GemmArgs probe{};
-    probe.k = h;
-    probe.n = i;
-    probe.group = group;
-    probe.outputs = 1;
-    probe.act = kActSwiglu;
-    probe.rt_logits = logits;
-    gemm_routes =
-        persist_fmt<2>(false, probe, Mode::GatherScatter, tb, s, "", PsForm::Plain, false) == 0;
-  }
-  if (gemm_routes) {
-    // routed by the gate/up GEMM below
-  } else if (route_schedule_fits(tokens, experts - 1, top_k)) {
-    if (int rc = route_schedule_launch(logits, bias, expert_indices, weights, tokens, experts - 1,
-                                       top_k, routed_scaling_factor, renormalize, offsets, perm,
-                                       tiles, count, tr, mtiles, mcount, s))
-      return rc;
-  } else {
-    if (int rc = lk_moe_router(logits, bias, expert_indices, weights, tokens, experts - 1, top_k,
-                               routed_scaling_factor, renormalize, stream))
-      return rc;
-    const RouteTable rt{expert_indices, top_k, routes, experts, experts - 1};
-    if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, tr, s,
-                                 mtiles, mcount))
-      return rc;
-  }
-
   // MXFP4 on the scaled fp4 MFMA: x and the activations go in as fp8 hi + lo
   const bool f8 = mx && mt != 0 && h % 128 == 0 && i % 128 == 0 && mxfp4_scaled_mfma();
   SplitBufs xs{}, as{};
@@ -3518,6 +3573,24 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
       path_choice(kKnobMoeSplitSwiglu) != 1 &&
       persist_fmt<1>(mx, g, Mode::Gather, tb, s, "", PsForm::SplitGateUp, false) == 0 &&
       persist_fmt<1>(mx, down_args(g), Mode::Scatter, tb, s, "", PsForm::SwiDown, false) == 0;
+  // Batches of at most 16 tokens on the persistent 16-row GEMMs: the gate/up
+  // GEMM routes and schedules the batch in every block (route_schedule_block)
+  // where that launch applies, with no router or schedule launch before it;
+  // for the split SwiGLU its block 0 also writes the schedule for the down
+  // GEMM. The path knob of the one-launch router + schedule turns it off.
+  bool gemm_routes = false;
+  if ((w2_rows || split) && mt == 1 && entries <= kRoutedEntries &&
+      route_schedule_fits(tokens, experts - 1, top_k)) {
+    GemmArgs probe = g;
+    probe.rt_logits = logits;
+    probe.rt_tokens = static_cast<int>(tokens);
+    probe.rt_routed = static_cast<int>(experts - 1);
+    probe.rt_top_k = static_cast<int>(top_k);
+    gemm_routes = (w2_rows ? persist_fmt<2>(mx, probe, Mode::GatherScatter, tb, s, "",
+                                            PsForm::Plain, false)
+                           : persist_fmt<1>(mx, probe, Mode::Gather, tb, s, "",
+                                            PsForm::SplitGateUp, false)) == 0;
+  }
   if (gemm_routes) {
     g.rt_logits = logits;
     g.rt_bias = bias;
@@ -3528,9 +3601,28 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
     g.rt_top_k = static_cast<int>(top_k);
     g.rt_renorm = renormalize;
     g.rt_scaling = routed_scaling_factor;
+    if (split) {
+      g.rt_perm_out = perm;
+      g.rt_tiles_out = tiles;
+      g.rt_count_out = count;
+    }
+  } else if (route_schedule_fits(tokens, experts - 1, top_k)) {
+    if (int rc = route_schedule_launch(logits, bias, expert_indices, weights, tokens, experts - 1,
+                                       top_k, routed_scaling_factor, renormalize, offsets, perm,
+                                       tiles, count, tr, mtiles, mcount, s))
+      return rc;
+  } else {
+    if (int rc = lk_moe_router(logits, bias, expert_indices, weights, tokens, experts - 1, top_k,
+                               routed_scaling_factor, renormalize, stream))
+      return rc;
+    const RouteTable rt{expert_indices, top_k, routes, experts, experts - 1};
+    if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, tr, s,
+                                 mtiles, mcount))
+      return rc;
   }
-  if (int rc = gemm_routes ? persist_fmt<2>(false, g, Mode::GatherScatter, tb, s,
-                                            "moe gate/up gemm (routing)", PsForm::Plain, true)
+  if (int rc = gemm_routes && w2_rows
+                   ? persist_fmt<2>(mx, g, Mode::GatherScatter, tb, s, "moe gate/up gemm (routing)",
+                                    PsForm::Plain, true)
                : f8 ? stream_launch<kFmtMxF8, 2>(g, Mode::Gather, tb, mt, s, "moe gate/up gemm")
                : split ? persist_fmt<1>(mx, g, Mode::Gather, tb, s, "moe gate/up gemm",
                                         PsForm::SplitGateUp, true)

@@ -1,10 +1,12 @@
 """GPU parity of the one-block schedule forms of the expert-major block.
 
-With at most 256 routed experts, batches of at most 8 tokens route and
-schedule in one launch (schedule_one_kernel with routing); batches of at most
-1024 token-routes route on a grid and schedule in one launch; larger batches,
-or the path knob moe_fused_schedule=off for any batch, take the router launch and the
-chunked schedule launches. All run the same selection code and the same stable
+With at most 256 routed experts, batches of at most 16 tokens route and
+schedule in one launch (schedule_one_kernel with routing), or, on the
+persistent 16-row GEMMs (K >= 512), inside every block of the gate/up GEMM
+with no launch before it; batches of at most 1024 token-routes route on a
+grid and schedule in one launch; larger batches, or the path knob
+moe_fused_schedule=off for any batch, take the router launch and the chunked
+schedule launches. All run the same selection code and the same stable
 ranking, so the selections, combine weights and block outputs must be
 bit-identical; the results are also checked against the oracle within the
 quantized-matmul tolerance (1e-2 relative / 2e-2 absolute in bf16), with the
@@ -120,26 +122,36 @@ def test_fused_router_schedule_matches_separate_launches(rng, monkeypatch, weigh
     assert_close_bf16(to_bits(y)[sel], ey, what=f"{weights} block T={tokens} k={top_k}")
 
 
+@pytest.mark.parametrize("weights", ["w4a16", "mxfp4"])
 @pytest.mark.parametrize("tokens,top_k,routed,bias,ties", [
     (1, 8, 256, False, False),
     (2, 8, 256, True, True),
     (3, 8, 256, False, True),
     (4, 8, 256, True, False),
     (4, 2, 64, False, False),
-    (4, 6, 32, True, True),   # few experts: routes of one token land on few tiles
+    (4, 6, 32, True, True),     # few experts: routes of one token land on few tiles
+    (5, 8, 256, False, False),  # split SwiGLU: the down GEMM reads block 0's tables
+    (8, 8, 256, True, True),
+    (9, 8, 256, False, True),   # waves route two tokens each
+    (12, 4, 32, True, False),
+    (16, 8, 256, True, True),   # 144 token-routes over three waves' bitmaps
+    (16, 16, 64, False, False),  # 272 token-routes, 256 selections: the limits
 ])
-def test_gate_up_gemm_that_routes_matches_separate_launches(rng, monkeypatch, tokens, top_k,
-                                                            routed, bias, ties):
-    """Batches of at most 4 tokens at K >= 512: the persistent gate/up GEMM
+def test_gate_up_gemm_that_routes_matches_separate_launches(rng, monkeypatch, weights, tokens,
+                                                            top_k, routed, bias, ties):
+    """Batches of at most 16 tokens at K >= 512: the persistent gate/up GEMM
     routes and schedules the batch in every block (no router or schedule
-    launch). Selections, weights and outputs bit-identical to the router and
-    chunked schedule launches (path knob off), and the block against the
-    oracle on every token."""
-    from local_kimi_amd.kernels import w4a16_moe_forward
+    launch); on the split SwiGLU (5 to 16 tokens, and MXFP4 at any of these
+    sizes) its block 0 also writes the schedule the down GEMM reads.
+    Selections, weights and outputs bit-identical to the router and chunked
+    schedule launches (path knob off), and the block against the oracle on
+    every token."""
+    from local_kimi_amd.kernels import mxfp4_moe_block, w4a16_moe_forward
 
     h, inter = 512, 256
-    banks = (*_w4_bank(rng, routed + 1, inter, h), *_w4_bank(rng, routed + 1, inter, h),
-             *_w4_bank(rng, routed + 1, h, inter))
+    bank = _mx_bank if weights == "mxfp4" else _w4_bank
+    banks = (*bank(rng, routed + 1, inter, h), *bank(rng, routed + 1, inter, h),
+             *bank(rng, routed + 1, h, inter))
     x = random_bf16_bits(rng, (tokens, h))
     logits = rng.normal(0, 1, (tokens, routed)).astype(np.float32)
     if ties:
@@ -147,24 +159,32 @@ def test_gate_up_gemm_that_routes_matches_separate_launches(rng, monkeypatch, to
     b = rng.normal(0, 0.05, routed).astype(np.float32) if bias else None
     args = (_dev(x), _dev(logits), None if b is None else _dev(b), *(_dev(v) for v in banks),
             top_k, 2.446)
-    (y, idx, w), (y0, idx0, w0) = _fused_and_split(monkeypatch, w4a16_moe_forward, *args)
+    block = mxfp4_moe_block if weights == "mxfp4" else w4a16_moe_forward
+    (y, idx, w), (y0, idx0, w0) = _fused_and_split(monkeypatch, block, *args)
     assert torch.equal(idx, idx0)
     assert torch.equal(w, w0)
     assert torch.equal(y, y0), "the routing gate/up GEMM and the separate launches differ"
     eidx, ew = OM.route(logits, b, top_k, routed_scaling_factor=2.446)
     assert np.array_equal(idx.cpu().numpy(), eidx)
     np.testing.assert_allclose(w.cpu().numpy(), ew, rtol=2e-6)
-    ey, _, _ = OM.moe_block(x, logits, b, *banks, top_k=top_k, routed_scaling_factor=2.446,
-                            group_size=128)
-    assert_close_bf16(to_bits(y), ey, what=f"routing gate/up T={tokens} k={top_k} E={routed}")
+    if weights == "mxfp4":
+        ey, _, _ = X.moe_block(x, logits, b, *banks, top_k=top_k, routed_scaling_factor=2.446)
+    else:
+        ey, _, _ = OM.moe_block(x, logits, b, *banks, top_k=top_k, routed_scaling_factor=2.446,
+                                group_size=128)
+    assert_close_bf16(to_bits(y), ey,
+                      what=f"{weights} routing gate/up T={tokens} k={top_k} E={routed}")
 
 
-def test_gate_up_gemm_that_routes_under_graph_replay(rng):
+@pytest.mark.parametrize("tokens", [4, 12])
+def test_gate_up_gemm_that_routes_under_graph_replay(rng, tokens):
     """The same launch captured in a HIP graph and replayed with new logits
-    copied in between: every replay matches an eager call on those logits."""
+    copied in between: every replay matches an eager call on those logits
+    (4 tokens: the token-major W2 launch follows; 12: the split SwiGLU's down
+    GEMM reads the schedule that the gate/up launch wrote)."""
     from local_kimi_amd.kernels import w4a16_moe_forward
 
-    tokens, top_k, routed, h, inter = 4, 8, 256, 512, 256
+    top_k, routed, h, inter = 8, 256, 512, 256
     banks = [_dev(v) for v in (*_w4_bank(rng, routed + 1, inter, h),
                                *_w4_bank(rng, routed + 1, inter, h),
                                *_w4_bank(rng, routed + 1, h, inter))]
