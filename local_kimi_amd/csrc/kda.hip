@@ -502,7 +502,8 @@ kda_layer_kernel(const LayerArgs a, int heads, int dim, float eps, float scale, 
 // and k states, each block the v states of its columns. The arithmetic of
 // every convolution, gate and norm is kda_layer_kernel's, so q, k, v, decay
 // and beta are bit-identical with it; the step's sums run over the rows in
-// another grouping. The blocks of a 128-byte state line (two column
+// another grouping, and the output is S^T q + beta (k . q) delta of the
+// decayed state S (one reduction pass instead of two). The blocks of a 128-byte state line (two column
 // blocks) are dispatched to one XCD when the item count allows, so the line
 // is fetched into one L2 once.
 constexpr int kSplitThreads = 128;
@@ -537,7 +538,7 @@ kda_layer_split_kernel(const SplitArgs a, int heads, int dim, int vs, int64_t it
   __shared__ float gain[kLayerMaxDim];
   __shared__ float norm[2];
   __shared__ float beta_s;
-  __shared__ float red[2][kSplitCols];
+  __shared__ float red[2][4][9];
   // item = (batch * heads + head) * vs + column block; with `paired`, the
   // two column blocks of a 128-byte line sit 8 blocks apart (one XCD)
   const int64_t lin = blockIdx.x;
@@ -632,52 +633,54 @@ kda_layer_split_kernel(const SplitArgs a, int heads, int dim, int vs, int64_t it
 #pragma unroll
     for (int c = 0; c < 4; ++c) s[p][c] *= g;
   }
-  // sums over the 32 row groups: the 16 lanes of a DPP row, then the 2 waves
-  auto reduce = [&](float (&v)[4]) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float x = v[c];
-      x += dpp_f32<kQuadXor1>(x);
-      x += dpp_f32<kQuadXor2>(x);
-      x += dpp_f32<kRowHalfMirror>(x);
-      x += dpp_f32<kRowMirror>(x);
-      v[c] = x;
-    }
-    __syncthreads();
-    if ((lane & 15) == 0) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) red[wave][cg * 4 + c] = v[c];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int c = 0; c < 4; ++c) v[c] = red[0][cg * 4 + c] + red[1][cg * 4 + c];
-  };
-  float delta[4];
+  // One pass of sums over the 32 row groups (the 16 lanes of a DPP row, then
+  // the 2 waves) gives S^T k and S^T q of the decayed state S and k . q; the
+  // output needs no second pass over the updated state:
+  //   o = (S + beta k delta^T)^T q = S^T q + beta (k . q) delta.
+  float sum[9];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    float part = 0.f;
+    float pk = 0.f, pq = 0.f;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) part = fmaf(s[p][c], kr[p], part);
-    delta[c] = part;
+    for (int p = 0; p < 4; ++p) {
+      pk = fmaf(s[p][c], kr[p], pk);
+      pq = fmaf(s[p][c], qr[p], pq);
+    }
+    sum[c] = pk;
+    sum[4 + c] = pq;
   }
-  reduce(delta);
+  sum[8] = 0.f;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) delta[c] = (cols ? vcol[cg * 4 + c] : 0.f) - delta[c];
+  for (int p = 0; p < 4; ++p) sum[8] = fmaf(kr[p], qr[p], sum[8]);
+#pragma unroll
+  for (int c = 0; c < 9; ++c) {
+    float x = sum[c];
+    x += dpp_f32<kQuadXor1>(x);
+    x += dpp_f32<kQuadXor2>(x);
+    x += dpp_f32<kRowHalfMirror>(x);
+    x += dpp_f32<kRowMirror>(x);
+    sum[c] = x;
+  }
+  if ((lane & 15) == 0) {
+#pragma unroll
+    for (int c = 0; c < 9; ++c) red[wave][cg][c] = sum[c];
+  }
+  __syncthreads();
+  float delta[4], o[4];
+  const float bkq = beta * (red[0][cg][8] + red[1][cg][8]);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const float sk = red[0][cg][c] + red[1][cg][c];
+    const float sq = red[0][cg][4 + c] + red[1][cg][4 + c];
+    delta[c] = (cols ? vcol[cg * 4 + c] : 0.f) - sk;
+    o[c] = fmaf(bkq, delta[c], sq);
+  }
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
     const float bk = beta * kr[p];
 #pragma unroll
     for (int c = 0; c < 4; ++c) s[p][c] = fmaf(bk, delta[c], s[p][c]);
   }
-  float o[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    float part = 0.f;
-#pragma unroll
-    for (int p = 0; p < 4; ++p) part = fmaf(s[p][c], qr[p], part);
-    o[c] = part;
-  }
-  reduce(o);
   if (cols) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
