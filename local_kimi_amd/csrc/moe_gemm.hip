@@ -1742,7 +1742,7 @@ struct PsPair {
 // fused epilogue, so the block's output is the same bits.
 // Routing and schedule of a small batch inside each block of the persistent
 // gate/up GEMM (ROUTED): the block's waves route the tokens, wave w tokens
-// w, w + 8, ... (engine/klinear/router.py:47-85; block 0 writes the
+// w and w + 8 (engine/klinear/router.py:47-85; block 0 writes the
 // selections and weights for the launches that follow), then the block ranks
 // the at most kRoutedEntries token-routes (shared expert as route top_k) into
 // the 16-row schedule in LDS, as the schedule kernels do: a bitmap of each
@@ -1802,12 +1802,28 @@ __device__ void route_schedule_block(const GemmArgs& g, int32_t* r_sel, int4* r_
   uint32_t* const mask = reinterpret_cast<uint32_t*>(r_count + 1);  // [nw][nb][2]
   if (nw > 1)  // the several waves' bitmaps, cleared while the logits arrive
     for (int i = tid; i < 2 * nw * nb; i += kThreads) mask[i] = 0u;
-  for (int t = wave; t < tokens; t += kStWaves)
-    route_token<4>(g.rt_logits + static_cast<int64_t>(t) * ne, g.rt_bias, ne, top_k, -1,
-                   g.rt_scaling, g.rt_renorm,
-                   writer ? g.rt_idx + static_cast<int64_t>(t) * top_k : nullptr,
-                   writer ? g.rt_w + static_cast<int64_t>(t) * top_k : nullptr,
-                   r_sel + t * top_k);
+  auto select = [&](int t, const float (&lg)[4], const float (&bs)[4]) {
+    route_select<4>(lg, bs, ne, top_k, -1, g.rt_scaling, g.rt_renorm,
+                    writer ? g.rt_idx + static_cast<int64_t>(t) * top_k : nullptr,
+                    writer ? g.rt_w + static_cast<int64_t>(t) * top_k : nullptr,
+                    r_sel + t * top_k);
+  };
+  if (tokens <= kStWaves) {  // block-uniform: one token per wave
+    if (wave < tokens)
+      route_token<4>(g.rt_logits + static_cast<int64_t>(wave) * ne, g.rt_bias, ne, top_k, -1,
+                     g.rt_scaling, g.rt_renorm,
+                     writer ? g.rt_idx + static_cast<int64_t>(wave) * top_k : nullptr,
+                     writer ? g.rt_w + static_cast<int64_t>(wave) * top_k : nullptr,
+                     r_sel + wave * top_k);
+  } else {  // two tokens per wave (at most 2 kStWaves, host-checked): both
+            // tokens' logits are requested before either selection
+    const int t1 = min(wave + kStWaves, tokens - 1);
+    float lg0[4], lg1[4], bs[4];
+    route_load_all<4>(g.rt_logits + static_cast<int64_t>(wave) * ne, g.rt_bias, ne, lg0, bs);
+    route_load<4>(g.rt_logits + static_cast<int64_t>(t1) * ne, ne, lg1);
+    select(wave, lg0, bs);
+    if (wave + kStWaves < tokens) select(wave + kStWaves, lg1, bs);
+  }
   __syncthreads();
   if (nw == 1) {  // block-uniform: wave 0 ranks the entries alone
     if (wave == 0) {
@@ -2845,7 +2861,8 @@ int persist_launch(const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_
     // a launch that routes keeps its routing scratch in the activation LDS
     if (g.rt_logits != nullptr) {
       const int n = g.rt_tokens * (g.rt_top_k + 1);
-      if (FMT == kFmtMxF16 || n > kRoutedEntries || g.rt_tokens * g.rt_top_k > kRoutedSelWords ||
+      if (FMT == kFmtMxF16 || n > kRoutedEntries || g.rt_tokens > 2 * kStWaves ||
+          g.rt_tokens * g.rt_top_k > kRoutedSelWords ||
           g.rt_routed > 256 || static_cast<size_t>(routed_scratch_words(n, g.rt_routed + 2)) * 4 > lds)
         return kPsNotApplicable;
     }
