@@ -1802,19 +1802,20 @@ __device__ void route_schedule_block(const GemmArgs& g, int32_t* r_sel, int4* r_
   uint32_t* const mask = reinterpret_cast<uint32_t*>(r_count + 1);  // [nw][nb][2]
   if (nw > 1)  // the several waves' bitmaps, cleared while the logits arrive
     for (int i = tid; i < 2 * nw * nb; i += kThreads) mask[i] = 0u;
+  // the selection rounds (compact code, run once per block from a cold
+  // instruction cache) rather than the merge network: the same choices
   auto select = [&](int t, const float (&lg)[4], const float (&bs)[4]) {
-    route_select<4>(lg, bs, ne, top_k, -1, g.rt_scaling, g.rt_renorm,
+    route_select_rounds<4>(lg, bs, ne, top_k, -1, g.rt_scaling, g.rt_renorm,
                     writer ? g.rt_idx + static_cast<int64_t>(t) * top_k : nullptr,
                     writer ? g.rt_w + static_cast<int64_t>(t) * top_k : nullptr,
                     r_sel + t * top_k);
   };
   if (tokens <= kStWaves) {  // block-uniform: one token per wave
-    if (wave < tokens)
-      route_token<4>(g.rt_logits + static_cast<int64_t>(wave) * ne, g.rt_bias, ne, top_k, -1,
-                     g.rt_scaling, g.rt_renorm,
-                     writer ? g.rt_idx + static_cast<int64_t>(wave) * top_k : nullptr,
-                     writer ? g.rt_w + static_cast<int64_t>(wave) * top_k : nullptr,
-                     r_sel + wave * top_k);
+    if (wave < tokens) {
+      float lg0[4], bs[4];
+      route_load_all<4>(g.rt_logits + static_cast<int64_t>(wave) * ne, g.rt_bias, ne, lg0, bs);
+      select(wave, lg0, bs);
+    }
   } else {  // two tokens per wave (at most 2 kStWaves, host-checked): both
             // tokens' logits are requested before either selection
     const int t1 = min(wave + kStWaves, tokens - 1);
