@@ -1806,9 +1806,9 @@ __device__ void route_schedule_block(const GemmArgs& g, int32_t* r_sel, int4* r_
   // instruction cache) rather than the merge network: the same choices
   auto select = [&](int t, const float (&lg)[4], const float (&bs)[4]) {
     route_select_rounds<4>(lg, bs, ne, top_k, -1, g.rt_scaling, g.rt_renorm,
-                    writer ? g.rt_idx + static_cast<int64_t>(t) * top_k : nullptr,
-                    writer ? g.rt_w + static_cast<int64_t>(t) * top_k : nullptr,
-                    r_sel + t * top_k);
+                           writer ? g.rt_idx + static_cast<int64_t>(t) * top_k : nullptr,
+                           writer ? g.rt_w + static_cast<int64_t>(t) * top_k : nullptr,
+                           r_sel + t * top_k);
   };
   if (tokens <= kStWaves) {  // block-uniform: one token per wave
     if (wave < tokens) {
