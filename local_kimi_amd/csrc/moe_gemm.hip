@@ -364,6 +364,9 @@ struct GemmArgs {
   float* rt_w;
   int rt_tokens, rt_routed, rt_top_k, rt_renorm;
   float rt_scaling;
+  // nonzero: the selections come from rt_idx (written by the router launch)
+  // and the block only ranks them
+  int rt_from_idx;
   // where block 0 also writes the schedule (perm, tiles, count) for a later
   // launch of the same block (the split SwiGLU's down GEMM); null: not needed
   int32_t* rt_perm_out;
@@ -1751,14 +1754,23 @@ struct PsPair {
 // bucket in earlier waves plus the popcount of the lower lanes of its own
 // (stable, row-major). Bucket routed + 1 collects invalid selections (expert
 // -1: zeros). No router or schedule launch; block 0 also writes the tables
-// where a later launch reads them (rt_tiles_out).
-constexpr int kRoutedEntries = kStWaves * kWave;  // 512
-constexpr int kRoutedSelWords = 256;               // tokens x top_k selections
+// where a later launch reads them (rt_tiles_out). With rt_from_idx the
+// selections come from the router launch's table and the block ranks up to
+// kRoutedEntries token-routes (two per thread): no schedule launch.
+constexpr int kRoutedEntries = 2 * kStWaves * kWave;  // 1024
 
-// LDS words of the routing scratch for n token-routes over nb buckets
-__host__ __device__ inline int routed_scratch_words(int n, int nb) {
+// LDS words of the selections (tokens x top_k, padded to 16 bytes)
+__host__ __device__ inline int routed_sel_words(int tokens, int top_k) {
+  return (tokens * top_k + 3) & ~3;
+}
+
+// LDS words of the routing scratch for n token-routes over nb buckets:
+// selections, the tile list (at most n tiles), the permutation, the tile
+// count, then the ranking's bitmaps, counts and starts
+__host__ __device__ inline int routed_scratch_words(int tokens, int top_k, int nb) {
+  const int n = tokens * (top_k + 1);
   const int nw = (n + kWave - 1) / kWave;
-  return kRoutedSelWords + 4 * kRoutedEntries + kRoutedEntries + 1 + 3 * nw * nb + 3 * nb;
+  return routed_sel_words(tokens, top_k) + 4 * n + n + 1 + 3 * nw * nb + 3 * nb;
 }
 
 // Bucket entry and tile counts of the nb buckets (cnt(i)), scanned in bucket
@@ -1810,7 +1822,10 @@ __device__ void route_schedule_block(const GemmArgs& g, int32_t* r_sel, int4* r_
                            writer ? g.rt_w + static_cast<int64_t>(t) * top_k : nullptr,
                            r_sel + t * top_k);
   };
-  if (tokens <= kStWaves) {  // block-uniform: one token per wave
+  if (g.rt_from_idx) {  // block-uniform: the router launch's selections
+    for (int i = tid; i < tokens * top_k; i += kThreads)
+      r_sel[i] = static_cast<int32_t>(g.rt_idx[i]);
+  } else if (tokens <= kStWaves) {  // block-uniform: one token per wave
     if (wave < tokens) {
       float lg0[4], bs[4];
       route_load_all<4>(g.rt_logits + static_cast<int64_t>(wave) * ne, g.rt_bias, ne, lg0, bs);
@@ -1857,29 +1872,33 @@ __device__ void route_schedule_block(const GemmArgs& g, int32_t* r_sel, int4* r_
               make_int4(b <= ne ? b : -1, pos, min(16, same - before), 0);
       }
     }
-  } else {
+  } else {  // entries tid and tid + 512: 64-entry group e / 64 keeps its bitmaps
     int* const pre = reinterpret_cast<int*>(mask + 2 * nw * nb);  // [nw][nb]
     int* const tot = pre + nw * nb;                               // [nb]
     int* const bstart = tot + nb;                                 // [nb]
     int* const btile = bstart + nb;                               // [nb]
-    const bool live = tid < n;
-    int b = 0;
-    if (live) {
-      const int t = tid / routes, r = tid - t * routes;
+    const bool two = n > kThreads;  // block-uniform: a second entry per thread
+    auto bucket_of = [&](int e) {
+      const int t = e / routes, r = e - t * routes;
       const int x = r == top_k ? ne : r_sel[t * top_k + r];
-      b = (x >= 0 && x <= ne) ? x : ne + 1;
-      atomicOr(&mask[(wave * nb + b) * 2 + (lane >> 5)], 1u << (lane & 31));
+      return (x >= 0 && x <= ne) ? x : ne + 1;
+    };
+    int bk[2] = {0, 0};
+    if (tid < n) {
+      bk[0] = bucket_of(tid);
+      atomicOr(&mask[(wave * nb + bk[0]) * 2 + (lane >> 5)], 1u << (lane & 31));
+    }
+    if (two && tid + kThreads < n) {
+      bk[1] = bucket_of(tid + kThreads);
+      atomicOr(&mask[((wave + kStWaves) * nb + bk[1]) * 2 + (lane >> 5)], 1u << (lane & 31));
     }
     __syncthreads();
-    // each bucket's entries in the waves before each wave, and in all
+    // each bucket's entries in the groups before each group, and in all
     for (int bb = tid; bb < nb; bb += kThreads) {
       int run = 0;
-#pragma unroll
-      for (int w = 0; w < kStWaves; ++w) {
-        if (w < nw) {
-          pre[w * nb + bb] = run;
-          run += __popc(mask[(w * nb + bb) * 2]) + __popc(mask[(w * nb + bb) * 2 + 1]);
-        }
+      for (int w = 0; w < nw; ++w) {
+        pre[w * nb + bb] = run;
+        run += __popc(mask[(w * nb + bb) * 2]) + __popc(mask[(w * nb + bb) * 2 + 1]);
       }
       tot[bb] = run;
     }
@@ -1887,16 +1906,21 @@ __device__ void route_schedule_block(const GemmArgs& g, int32_t* r_sel, int4* r_
     if (wave == 0)
       routed_bucket_scan(nb, lane, [&](int i) { return tot[i]; }, bstart, btile, r_count);
     __syncthreads();
-    if (live) {
-      const uint32_t lo = mask[(wave * nb + b) * 2], hi = mask[(wave * nb + b) * 2 + 1];
-      const int below = lane < 32 ? __popc(lo & ((1u << lane) - 1u))
-                                  : __popc(lo) + __popc(hi & ((1u << (lane - 32)) - 1u));
-      const int rank = pre[wave * nb + b] + below;
-      const int pos = bstart[b] + rank;
-      r_perm[pos] = tid;
-      if ((rank & 15) == 0)
-        r_tiles[btile[b] + (rank >> 4)] =
-            make_int4(b <= ne ? b : -1, pos, min(16, tot[b] - rank), 0);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int e = tid + kThreads * k;
+      if ((k == 0 || two) && e < n) {
+        const int grp = e / kWave, b = bk[k];
+        const uint32_t lo = mask[(grp * nb + b) * 2], hi = mask[(grp * nb + b) * 2 + 1];
+        const int below = lane < 32 ? __popc(lo & ((1u << lane) - 1u))
+                                    : __popc(lo) + __popc(hi & ((1u << (lane - 32)) - 1u));
+        const int rank = pre[grp * nb + b] + below;
+        const int pos = bstart[b] + rank;
+        r_perm[pos] = e;
+        if ((rank & 15) == 0)
+          r_tiles[btile[b] + (rank >> 4)] =
+              make_int4(b <= ne ? b : -1, pos, min(16, tot[b] - rank), 0);
+      }
     }
   }
   __syncthreads();
@@ -1938,11 +1962,14 @@ w4a16_persist_kernel(const GemmArgs g, int nbuf) {
   const int cgs1 = static_cast<int>((N + NT * 16 - 1) / (NT * 16));  // column groups per matrix
   const int cgs = SPLIT ? 2 * cgs1 : cgs1;
   // ROUTED: the batch's selections and schedule, computed by every block in
-  // the activation LDS before any staging (at most kRoutedEntries routes)
+  // the activation LDS before any staging (at most kRoutedEntries routes;
+  // the layout of routed_scratch_words)
+  const int r_n = ROUTED ? g.rt_tokens * (g.rt_top_k + 1) : 0;
   int32_t* const r_sel = reinterpret_cast<int32_t*>(smem);  // [tokens][top_k]
-  int4* const r_tiles = reinterpret_cast<int4*>(smem) + kRoutedSelWords / 4;
-  int32_t* const r_perm = reinterpret_cast<int32_t*>(r_tiles + kRoutedEntries);
-  int32_t* const r_count = r_perm + kRoutedEntries;  // then the ranking scratch
+  int4* const r_tiles =
+      reinterpret_cast<int4*>(smem) + (ROUTED ? routed_sel_words(g.rt_tokens, g.rt_top_k) / 4 : 0);
+  int32_t* const r_perm = reinterpret_cast<int32_t*>(r_tiles + r_n);  // at most n tiles
+  int32_t* const r_count = r_perm + r_n;  // then the ranking scratch
   if constexpr (ROUTED) route_schedule_block(g, r_sel, r_tiles, r_perm, r_count);
   const int total = (ROUTED ? *r_count : *g.tile_count) * cgs;
   const int per = (total + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
@@ -2860,11 +2887,14 @@ int persist_launch(const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_
     if (nbuf == 0) return kPsNotApplicable;
     const size_t lds = nbuf * one;
     // a launch that routes keeps its routing scratch in the activation LDS
-    if (g.rt_logits != nullptr) {
+    const bool routed = g.rt_logits != nullptr || g.rt_from_idx;
+    if (routed) {
       const int n = g.rt_tokens * (g.rt_top_k + 1);
-      if (FMT == kFmtMxF16 || n > kRoutedEntries || g.rt_tokens > 2 * kStWaves ||
-          g.rt_tokens * g.rt_top_k > kRoutedSelWords ||
-          g.rt_routed > 256 || static_cast<size_t>(routed_scratch_words(n, g.rt_routed + 2)) * 4 > lds)
+      if (FMT == kFmtMxF16 || n > kRoutedEntries || g.rt_tokens < 1 ||
+          (!g.rt_from_idx && g.rt_tokens > 2 * kStWaves) ||
+          g.rt_routed > 256 ||
+          static_cast<size_t>(routed_scratch_words(g.rt_tokens, g.rt_top_k, g.rt_routed + 2)) * 4 >
+              lds)
         return kPsNotApplicable;
     }
     // a phase's activations are staged from one batch of registers per thread
@@ -2874,7 +2904,7 @@ int persist_launch(const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_
     if constexpr (MATS == 1) {
       if (form == PsForm::SplitGateUp) {
         if (mode != Mode::Gather || g.act != kActSwiglu) return kPsNotApplicable;
-        if (g.rt_logits != nullptr)  // the block routes and schedules the batch itself
+        if (routed)  // the block routes (or ranks) and schedules the batch itself
           rc = persist_depth<FMT, 1, true, false, true, false, true>(g, nbuf, lds, tiles_bound, s,
                                                                      launch);
         else
@@ -2894,7 +2924,7 @@ int persist_launch(const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_
           break;
         case Mode::GatherScatter:
           if constexpr (MATS == 2) {
-            if (g.rt_logits != nullptr) {  // the block routes and schedules the batch itself
+            if (routed) {  // the block routes (or ranks) and schedules the batch itself
               rc = persist_depth<FMT, MATS, true, true, false, false, true>(g, nbuf, lds,
                                                                             tiles_bound, s, launch);
               break;
@@ -3609,6 +3639,21 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
                            : persist_fmt<1>(mx, probe, Mode::Gather, tb, s, "",
                                             PsForm::SplitGateUp, false)) == 0;
   }
+  // Larger batches on the split SwiGLU (up to kRoutedEntries token-routes):
+  // the router launch, then every block of the gate/up GEMM ranks the
+  // router's selections itself and block 0 writes the schedule for the down
+  // GEMM: no schedule launch. The same path knob turns it off.
+  bool gemm_ranks = false;
+  if (!gemm_routes && split && mt == 1 && entries <= kRoutedEntries &&
+      path_choice(kKnobMoeFusedSchedule) != 1) {
+    GemmArgs probe = g;
+    probe.rt_from_idx = 1;
+    probe.rt_tokens = static_cast<int>(tokens);
+    probe.rt_routed = static_cast<int>(experts - 1);
+    probe.rt_top_k = static_cast<int>(top_k);
+    gemm_ranks =
+        persist_fmt<1>(mx, probe, Mode::Gather, tb, s, "", PsForm::SplitGateUp, false) == 0;
+  }
   if (gemm_routes) {
     g.rt_logits = logits;
     g.rt_bias = bias;
@@ -3624,6 +3669,18 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
       g.rt_tiles_out = tiles;
       g.rt_count_out = count;
     }
+  } else if (gemm_ranks) {
+    if (int rc = lk_moe_router(logits, bias, expert_indices, weights, tokens, experts - 1, top_k,
+                               routed_scaling_factor, renormalize, stream))
+      return rc;
+    g.rt_from_idx = 1;
+    g.rt_idx = expert_indices;
+    g.rt_tokens = static_cast<int>(tokens);
+    g.rt_routed = static_cast<int>(experts - 1);
+    g.rt_top_k = static_cast<int>(top_k);
+    g.rt_perm_out = perm;
+    g.rt_tiles_out = tiles;
+    g.rt_count_out = count;
   } else if (route_schedule_fits(tokens, experts - 1, top_k)) {
     if (int rc = route_schedule_launch(logits, bias, expert_indices, weights, tokens, experts - 1,
                                        top_k, routed_scaling_factor, renormalize, offsets, perm,

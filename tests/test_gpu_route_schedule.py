@@ -176,6 +176,53 @@ def test_gate_up_gemm_that_routes_matches_separate_launches(rng, monkeypatch, we
                       what=f"{weights} routing gate/up T={tokens} k={top_k} E={routed}")
 
 
+@pytest.mark.parametrize("weights", ["w4a16", "mxfp4"])
+@pytest.mark.parametrize("tokens,top_k,routed,h,bias", [
+    (17, 8, 256, 1024, True),   # one token past the in-GEMM routing
+    (24, 8, 64, 512, False),
+    (40, 6, 256, 1024, True),
+    (64, 8, 256, 1024, False),  # 576 token-routes: two entries per thread
+    (113, 8, 32, 512, True),    # 1017 token-routes, the most that rank in the GEMM
+    (100, 1, 256, 1024, False),  # 200 token-routes at top-1
+])
+def test_gate_up_gemm_that_ranks_the_router_selections(rng, monkeypatch, weights, tokens, top_k,
+                                                       routed, h, bias):
+    """Batches above 16 tokens on the split SwiGLU with at most 1024
+    token-routes: the router launch, then every block of the gate/up GEMM
+    ranks its selections and block 0 writes the schedule for the down GEMM
+    (no schedule launch). Selections, weights and outputs bit-identical to
+    the router and chunked schedule launches (path knob off), and the block
+    against the oracle on a third of the tokens."""
+    from local_kimi_amd.kernels import mxfp4_moe_block, w4a16_moe_forward
+
+    inter = 256
+    bank = _mx_bank if weights == "mxfp4" else _w4_bank
+    banks = (*bank(rng, routed + 1, inter, h), *bank(rng, routed + 1, inter, h),
+             *bank(rng, routed + 1, h, inter))
+    x = random_bf16_bits(rng, (tokens, h))
+    logits = rng.normal(0, 1, (tokens, routed)).astype(np.float32)
+    logits[::5, 3:9] = logits[::5, 3:4]  # tied choices
+    b = rng.normal(0, 0.05, routed).astype(np.float32) if bias else None
+    args = (_dev(x), _dev(logits), None if b is None else _dev(b), *(_dev(v) for v in banks),
+            top_k, 2.446)
+    block = mxfp4_moe_block if weights == "mxfp4" else w4a16_moe_forward
+    (y, idx, w), (y0, idx0, w0) = _fused_and_split(monkeypatch, block, *args)
+    assert torch.equal(idx, idx0)
+    assert torch.equal(w, w0)
+    assert torch.equal(y, y0), "the ranking gate/up GEMM and the separate launches differ"
+    eidx, ew = OM.route(logits, b, top_k, routed_scaling_factor=2.446)
+    assert np.array_equal(idx.cpu().numpy(), eidx)
+    sel = np.arange(0, tokens, 3)
+    if weights == "mxfp4":
+        ey, _, _ = X.moe_block(x[sel], logits[sel], b, *banks, top_k=top_k,
+                               routed_scaling_factor=2.446)
+    else:
+        ey, _, _ = OM.moe_block(x[sel], logits[sel], b, *banks, top_k=top_k,
+                                routed_scaling_factor=2.446, group_size=128)
+    assert_close_bf16(to_bits(y)[sel], ey,
+                      what=f"{weights} ranking gate/up T={tokens} k={top_k} E={routed}")
+
+
 @pytest.mark.parametrize("tokens", [4, 12])
 def test_gate_up_gemm_that_routes_under_graph_replay(rng, tokens):
     """The same launch captured in a HIP graph and replayed with new logits
