@@ -1744,19 +1744,18 @@ struct PsPair {
 // alone; the SwiGLU is applied to the same bf16-rounded values as in the
 // fused epilogue, so the block's output is the same bits.
 // Routing and schedule of a small batch inside each block of the persistent
-// gate/up GEMM (ROUTED): the block's waves route the tokens, wave w tokens
-// w and w + 8 (engine/klinear/router.py:47-85; block 0 writes the
-// selections and weights for the launches that follow), then the block ranks
-// the at most kRoutedEntries token-routes (shared expert as route top_k) into
-// the 16-row schedule in LDS, as the schedule kernels do: a bitmap of each
-// bucket's entries per wave of entries, the buckets' entry and tile counts
-// scanned in bucket order by one wave, and an entry's rank the entries of its
-// bucket in earlier waves plus the popcount of the lower lanes of its own
-// (stable, row-major). Bucket routed + 1 collects invalid selections (expert
-// -1: zeros). No router or schedule launch; block 0 also writes the tables
-// where a later launch reads them (rt_tiles_out). With rt_from_idx the
-// selections come from the router launch's table and the block ranks up to
-// kRoutedEntries token-routes (two per thread): no schedule launch.
+// gate/up GEMM (ROUTED): wave w routes token w (at most kStWaves tokens;
+// engine/klinear/router.py:47-85; block 0 writes the selections and weights
+// for the launches that follow), or, with rt_from_idx, the block reads the
+// router launch's selections. Then the block ranks the at most kRoutedEntries
+// token-routes (shared expert as route top_k; two per thread) into the 16-row
+// schedule in LDS, as the schedule kernels do: a bitmap of each bucket's
+// entries per 64-entry group, the buckets' entry and tile counts scanned in
+// bucket order by one wave, and an entry's rank the entries of its bucket in
+// earlier groups plus the popcount of the lower lanes of its own (stable,
+// row-major). Bucket routed + 1 collects invalid selections (expert -1:
+// zeros). No schedule launch; block 0 also writes the tables where a later
+// launch reads them (rt_tiles_out).
 constexpr int kRoutedEntries = 2 * kStWaves * kWave;  // 1024
 
 // LDS words of the selections (tokens x top_k, padded to 16 bytes)
@@ -1825,20 +1824,10 @@ __device__ void route_schedule_block(const GemmArgs& g, int32_t* r_sel, int4* r_
   if (g.rt_from_idx) {  // block-uniform: the router launch's selections
     for (int i = tid; i < tokens * top_k; i += kThreads)
       r_sel[i] = static_cast<int32_t>(g.rt_idx[i]);
-  } else if (tokens <= kStWaves) {  // block-uniform: one token per wave
-    if (wave < tokens) {
-      float lg0[4], bs[4];
-      route_load_all<4>(g.rt_logits + static_cast<int64_t>(wave) * ne, g.rt_bias, ne, lg0, bs);
-      select(wave, lg0, bs);
-    }
-  } else {  // two tokens per wave (at most 2 kStWaves, host-checked): both
-            // tokens' logits are requested before either selection
-    const int t1 = min(wave + kStWaves, tokens - 1);
-    float lg0[4], lg1[4], bs[4];
+  } else if (wave < tokens) {  // one token per wave (at most kStWaves, host-checked)
+    float lg0[4], bs[4];
     route_load_all<4>(g.rt_logits + static_cast<int64_t>(wave) * ne, g.rt_bias, ne, lg0, bs);
-    route_load<4>(g.rt_logits + static_cast<int64_t>(t1) * ne, ne, lg1);
     select(wave, lg0, bs);
-    if (wave + kStWaves < tokens) select(wave + kStWaves, lg1, bs);
   }
   __syncthreads();
   if (nw == 1) {  // block-uniform: wave 0 ranks the entries alone
@@ -2891,7 +2880,7 @@ int persist_launch(const GemmArgs& g, Mode mode, int64_t tiles_bound, hipStream_
     if (routed) {
       const int n = g.rt_tokens * (g.rt_top_k + 1);
       if (FMT == kFmtMxF16 || n > kRoutedEntries || g.rt_tokens < 1 ||
-          (!g.rt_from_idx && g.rt_tokens > 2 * kStWaves) ||
+          (!g.rt_from_idx && g.rt_tokens > kStWaves) ||
           g.rt_routed > 256 ||
           static_cast<size_t>(routed_scratch_words(g.rt_tokens, g.rt_top_k, g.rt_routed + 2)) * 4 >
               lds)
@@ -3621,13 +3610,16 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
       path_choice(kKnobMoeSplitSwiglu) != 1 &&
       persist_fmt<1>(mx, g, Mode::Gather, tb, s, "", PsForm::SplitGateUp, false) == 0 &&
       persist_fmt<1>(mx, down_args(g), Mode::Scatter, tb, s, "", PsForm::SwiDown, false) == 0;
-  // Batches of at most 16 tokens on the persistent 16-row GEMMs: the gate/up
-  // GEMM routes and schedules the batch in every block (route_schedule_block)
-  // where that launch applies, with no router or schedule launch before it;
-  // for the split SwiGLU its block 0 also writes the schedule for the down
-  // GEMM. The path knob of the one-launch router + schedule turns it off.
+  // Batches of at most 8 tokens (one per wave) on the persistent 16-row
+  // GEMMs: the gate/up GEMM routes and schedules the batch in every block
+  // (route_schedule_block) where that launch applies, with no router or
+  // schedule launch before it; for the split SwiGLU its block 0 also writes
+  // the schedule for the down GEMM. (Two tokens per wave made the prologue of
+  // every block longer than the router launch: at 16 tokens 68.0 against
+  // 66.3 us per step with the router launch and the ranking below.) The
+  // path knob of the one-launch router + schedule turns it off.
   bool gemm_routes = false;
-  if ((w2_rows || split) && mt == 1 && entries <= kRoutedEntries &&
+  if ((w2_rows || split) && mt == 1 && tokens <= kStWaves && entries <= kRoutedEntries &&
       route_schedule_fits(tokens, experts - 1, top_k)) {
     GemmArgs probe = g;
     probe.rt_logits = logits;

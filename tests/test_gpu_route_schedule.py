@@ -2,9 +2,11 @@
 
 With at most 256 routed experts, batches of at most 16 tokens route and
 schedule in one launch (schedule_one_kernel with routing), or, on the
-persistent 16-row GEMMs (K >= 512), inside every block of the gate/up GEMM
-with no launch before it; batches of at most 1024 token-routes route on a
-grid and schedule in one launch; larger batches, or the path knob
+persistent 16-row GEMMs (K >= 512), batches of at most 8 tokens route and
+schedule inside every block of the gate/up GEMM with no launch before it,
+and batches of up to 1024 token-routes are ranked there after the router
+launch; otherwise batches of at most 1024 token-routes route on a grid and
+schedule in one launch; larger batches, or the path knob
 moe_fused_schedule=off for any batch, take the router launch and the chunked
 schedule launches. All run the same selection code and the same stable
 ranking, so the selections, combine weights and block outputs must be
@@ -131,18 +133,19 @@ def test_fused_router_schedule_matches_separate_launches(rng, monkeypatch, weigh
     (4, 2, 64, False, False),
     (4, 6, 32, True, True),     # few experts: routes of one token land on few tiles
     (5, 8, 256, False, False),  # split SwiGLU: the down GEMM reads block 0's tables
-    (8, 8, 256, True, True),
-    (9, 8, 256, False, True),   # waves route two tokens each
+    (8, 8, 256, True, True),    # the most tokens routed in the GEMM (one per wave)
+    (9, 8, 256, False, True),   # router launch, ranking in the GEMM
     (12, 4, 32, True, False),
-    (16, 8, 256, True, True),   # 144 token-routes over three waves' bitmaps
-    (16, 16, 64, False, False),  # 272 token-routes, 256 selections: the limits
+    (16, 8, 256, True, True),   # 144 token-routes over three groups' bitmaps
+    (16, 16, 64, False, False),  # 272 token-routes, 256 selections
 ])
 def test_gate_up_gemm_that_routes_matches_separate_launches(rng, monkeypatch, weights, tokens,
                                                             top_k, routed, bias, ties):
-    """Batches of at most 16 tokens at K >= 512: the persistent gate/up GEMM
+    """Batches of at most 8 tokens at K >= 512: the persistent gate/up GEMM
     routes and schedules the batch in every block (no router or schedule
-    launch); on the split SwiGLU (5 to 16 tokens, and MXFP4 at any of these
-    sizes) its block 0 also writes the schedule the down GEMM reads.
+    launch); from 9 tokens the router launch selects and every block ranks
+    the selections. On the split SwiGLU (5 tokens and more in W4A16, every
+    size in MXFP4) block 0 also writes the schedule the down GEMM reads.
     Selections, weights and outputs bit-identical to the router and chunked
     schedule launches (path knob off), and the block against the oracle on
     every token."""
@@ -178,7 +181,7 @@ def test_gate_up_gemm_that_routes_matches_separate_launches(rng, monkeypatch, we
 
 @pytest.mark.parametrize("weights", ["w4a16", "mxfp4"])
 @pytest.mark.parametrize("tokens,top_k,routed,h,bias", [
-    (17, 8, 256, 1024, True),   # one token past the in-GEMM routing
+    (17, 8, 256, 1024, True),
     (24, 8, 64, 512, False),
     (40, 6, 256, 1024, True),
     (64, 8, 256, 1024, False),  # 576 token-routes: two entries per thread
@@ -187,7 +190,7 @@ def test_gate_up_gemm_that_routes_matches_separate_launches(rng, monkeypatch, we
 ])
 def test_gate_up_gemm_that_ranks_the_router_selections(rng, monkeypatch, weights, tokens, top_k,
                                                        routed, h, bias):
-    """Batches above 16 tokens on the split SwiGLU with at most 1024
+    """Batches above 8 tokens on the split SwiGLU with at most 1024
     token-routes: the router launch, then every block of the gate/up GEMM
     ranks its selections and block 0 writes the schedule for the down GEMM
     (no schedule launch). Selections, weights and outputs bit-identical to
@@ -227,8 +230,9 @@ def test_gate_up_gemm_that_ranks_the_router_selections(rng, monkeypatch, weights
 def test_gate_up_gemm_that_routes_under_graph_replay(rng, tokens):
     """The same launch captured in a HIP graph and replayed with new logits
     copied in between: every replay matches an eager call on those logits
-    (4 tokens: the token-major W2 launch follows; 12: the split SwiGLU's down
-    GEMM reads the schedule that the gate/up launch wrote)."""
+    (4 tokens: the gate/up GEMM routes and the token-major W2 launch follows;
+    12: the router launch selects, the gate/up GEMM ranks, and the split
+    SwiGLU's down GEMM reads the schedule that the gate/up launch wrote)."""
     from local_kimi_amd.kernels import w4a16_moe_forward
 
     top_k, routed, h, inter = 8, 256, 512, 256
