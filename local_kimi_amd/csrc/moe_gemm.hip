@@ -476,12 +476,11 @@ __device__ inline void lds_direct4(u32x4_t rs, const void* lds, uint32_t voff, u
 // streaming kernel stages it) and -136 * sum(x) per 128-wide group, summed
 // in the staging's order: one 16-lane DPP row per (row, group), lane c on
 // chunk c, so the sums are bit-identical to the in-kernel staging's.
-__global__ void __launch_bounds__(256)
-pair_rows_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xp,
-                 float* __restrict__ neg, uint32_t units) {
-  // unit = row * (k / 128) + group, so its chunk sits at 128 unit + 8 c
-  const uint32_t unit = (blockIdx.x * 256u + threadIdx.x) >> 4;
-  const bool live = unit < units;  // uniform over each 16-lane row
+// Unit u of the pairing (row u / (k / 128), group u % (k / 128)) by one
+// 16-lane row: lane c pairs chunk c and the row sums the group (live is
+// uniform over the row; a dead row loads unit 0 and stores nothing).
+__device__ inline void pair_unit(const uint16_t* __restrict__ x, uint16_t* __restrict__ xp,
+                                 float* __restrict__ neg, uint32_t unit, bool live) {
   const uint32_t u = live ? unit : 0u;
   const int64_t off = static_cast<int64_t>(u) * 128 + (threadIdx.x & 15) * 8;
   const uint4 v = *reinterpret_cast<const uint4*>(x + off);
@@ -493,6 +492,35 @@ pair_rows_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xp,
     *reinterpret_cast<uint4*>(xp + off) = make_uint4(q[0], q[1], q[2], q[3]);
     if ((threadIdx.x & 15) == 0) neg[u] = -kCodeOffset * sx;
   }
+}
+
+__global__ void __launch_bounds__(256)
+pair_rows_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xp,
+                 float* __restrict__ neg, uint32_t units) {
+  // unit = row * (k / 128) + group, so its chunk sits at 128 unit + 8 c
+  const uint32_t unit = (blockIdx.x * 256u + threadIdx.x) >> 4;
+  pair_unit(x, xp, neg, unit, unit < units);  // uniform over each 16-lane row
+}
+
+// The router and the activation pairing of a prefill-sized batch in one
+// launch: block t routes token t in its first wave (route_token, as the
+// router kernel does: engine/klinear/router.py:47-85) and pairs token t's
+// k / 128 groups in its 16-lane rows (pair_unit, as pair_rows_kernel does),
+// so the selections, weights and paired rows are those two launches' bits.
+constexpr int kRoutePairThreads = 320;
+
+template <int EPL>
+__global__ void __launch_bounds__(kRoutePairThreads)
+route_pair_kernel(const float* __restrict__ logits, const float* __restrict__ bias,
+                  int64_t* __restrict__ idx, float* __restrict__ w, int experts, int top_k,
+                  float scaling, int renorm, const uint16_t* __restrict__ x,
+                  uint16_t* __restrict__ xp, float* __restrict__ neg, int groups) {
+  const int64_t t = blockIdx.x;
+  if (threadIdx.x < kWave)
+    route_token<EPL>(logits + t * experts, bias, experts, top_k, -1, scaling, renorm,
+                     idx + t * top_k, w + t * top_k);
+  for (int gq = threadIdx.x >> 4; gq < groups; gq += kRoutePairThreads / 16)  // per 16-lane row
+    pair_unit(x, xp, neg, static_cast<uint32_t>(t * groups + gq), true);
 }
 
 // Zero line read by ring reloads past the last k-step. Every wave reads the
@@ -2664,6 +2692,20 @@ int pair_rows_launch(const uint16_t* x, uint16_t* xp, float* neg, int64_t rows, 
   return check_launch("moe activation pairing");
 }
 
+// route_pair_kernel over `tokens` tokens of k (k % 128 == 0, at most 256
+// routed experts; validated by the caller)
+int route_pair_launch(const float* logits, const float* bias, int64_t* idx, float* w,
+                      int64_t tokens, int64_t routed, int64_t top_k, float scaling, int renorm,
+                      const uint16_t* x, uint16_t* xp, float* neg, int64_t k, hipStream_t s) {
+  LK_REQUIRE(k % 128 == 0 && tokens * (k / 128) < (1LL << 27) && routed <= 256 &&
+                 tokens <= 2147483647LL,
+             "router + pairing: unsupported size");
+  route_pair_kernel<4><<<static_cast<unsigned>(tokens), kRoutePairThreads, 0, s>>>(
+      logits, bias, idx, w, static_cast<int>(routed), static_cast<int>(top_k), scaling, renorm,
+      x, xp, neg, static_cast<int>(k / 128));
+  return check_launch("moe router + activation pairing");
+}
+
 enum class Mode { Gather, Scatter, GatherScatter, Dense };
 
 template <int FMT, int MATS, int NT, bool WIDE>
@@ -3524,6 +3566,13 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   const int tr = mt == 1 ? kSmallTileRows : kTileRows;
   // W4A16 G = 128 on 64-row tiles: x and the activations go in paired
   const bool paired = !mx && mt == 4 && group == 128;
+  // ...and when the batch takes the router launch (the 64-row tiles route
+  // neither in the GEMM nor in the one-launch schedule), that launch also
+  // pairs them (route_pair_kernel): one launch instead of two; the path knob
+  // of the fused schedules turns it off
+  const bool route_pairs = paired && experts - 1 <= 256 &&
+                           path_choice(kKnobMoeFusedSchedule) != 1 &&
+                           !route_schedule_fits(tokens, experts - 1, top_k);
   const int64_t tb = max_tiles_for(entries, experts, tr);
   // Few tokens (W4A16): the activations go to (token, route) rows and one
   // token-major launch does W2, the combine and the shared expert, instead of
@@ -3558,9 +3607,11 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
   if (paired) {
     g.a_pair = reinterpret_cast<uint16_t*>(ws + l.x_pair);
     g.a_neg = reinterpret_cast<float*>(ws + l.x_neg);
-    if (int rc = pair_rows_launch(x, const_cast<uint16_t*>(g.a_pair), const_cast<float*>(g.a_neg),
-                                  tokens, h, s))
-      return rc;
+    if (!route_pairs) {
+      if (int rc = pair_rows_launch(x, const_cast<uint16_t*>(g.a_pair),
+                                    const_cast<float*>(g.a_neg), tokens, h, s))
+        return rc;
+    }
   }
   g.wp[0] = w1_packed;
   g.ws[0] = w1_scales;
@@ -3679,8 +3730,13 @@ static int moe_forward_common(bool mx, const uint16_t* x, const float* logits, c
                                        tiles, count, tr, mtiles, mcount, s))
       return rc;
   } else {
-    if (int rc = lk_moe_router(logits, bias, expert_indices, weights, tokens, experts - 1, top_k,
-                               routed_scaling_factor, renormalize, stream))
+    if (int rc = route_pairs
+                     ? route_pair_launch(logits, bias, expert_indices, weights, tokens, experts - 1,
+                                         top_k, routed_scaling_factor, renormalize, x,
+                                         const_cast<uint16_t*>(g.a_pair),
+                                         const_cast<float*>(g.a_neg), h, s)
+                     : lk_moe_router(logits, bias, expert_indices, weights, tokens, experts - 1,
+                                     top_k, routed_scaling_factor, renormalize, stream))
       return rc;
     const RouteTable rt{expert_indices, top_k, routes, experts, experts - 1};
     if (int rc = schedule_launch(rt, entries, ws, l.sched, offsets, perm, tiles, count, tr, s,

@@ -15,7 +15,9 @@ quantized-matmul tolerance (1e-2 relative / 2e-2 absolute in bf16), with the
 expert indices bit-exact. Cases: with and without a router bias, tied logits
 (equal keys keep the lower expert id first), both sides of the 8-token
 routing limit, the largest one-launch schedule (113 tokens x 9 routes = 1017
-token-routes) and one token past it, and both weight formats.
+token-routes) and one token past it, batches on the 64-row tiles (whose
+router launch also writes the paired activation rows in W4A16), and both
+weight formats.
 """
 
 from __future__ import annotations
@@ -88,6 +90,8 @@ def _fused_and_split(monkeypatch, fn, *args):
     (113, 8, True, False),   # 1017 token-routes: the largest one-launch schedule
     (114, 8, False, False),  # 1026 token-routes: separate launches on both sides
     (200, 4, True, True),    # 1000 token-routes at top-4
+    (231, 8, True, False),   # 2079 token-routes: 64-row tiles, the router launch pairs x
+    (300, 8, False, True),
 ])
 def test_fused_router_schedule_matches_separate_launches(rng, monkeypatch, weights, tokens, top_k,
                                                          bias, ties):
